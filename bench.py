@@ -1,0 +1,182 @@
+"""Benchmark of libmxfp6gemm on one MI355X: MXFP6 GEMM TFLOPs and fraction of the dense MXFP6
+MFMA peak.
+
+A step is one mxfp6_gemm_async call (the whole hot path: tile kernel, plus the split-K reduce when
+the shape splits) over operands already resident in HBM. Default workload: M = N = K = 8192, FP16
+out, A and B drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX rule.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--all] [--no-cpu]
+
+Prints one JSON line per workload (only the default one unless --all).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mxfp6-gemm_amd"))
+
+import numpy as np  # noqa: E402
+
+import mxfp6_amd as mx  # noqa: E402
+
+SEED = 0x4D584636
+# MI355X published dense MXFP6 / MXFP4 MFMA peak (TFLOP/s) and HBM bandwidth (GB/s)
+PEAK_TFLOPS = 10100.0
+PEAK_HBM_GBS = 8000.0
+
+# name -> (M, N, K, out_type, (dist_a, sigma_a), (dist_b, sigma_b), description)
+CONFIGS = {
+    "c1": (256, 256, 1024, mx.OUT_F32, (mx.DIST_NORMAL, 1.0), (mx.DIST_NORMAL, 1.0),
+           "A,B ~ N(0,1)"),
+    "c2": (8192, 8192, 8192, mx.OUT_F16, (mx.DIST_NORMAL, 1.0), (mx.DIST_NORMAL, 1.0),
+           "A,B ~ N(0,1)"),
+    "c3": (2048, 6144, 16128, mx.OUT_F16, (mx.DIST_NORMAL, 2.0), (mx.DIST_UNIFORM, 1.0),
+           "A ~ N(0,4) (sigma 2), B ~ U[-1,1]"),
+    "c4": (2048, 1024, 105728, mx.OUT_F16, (mx.DIST_NORMAL, 1.0), (mx.DIST_NORMAL, 1.0),
+           "A,B ~ N(0,1)"),
+    "c5": (2048, 5120, 105728, mx.OUT_BF16, (mx.DIST_STUDENT_T3, 1.0),
+           (mx.DIST_STUDENT_T3, 1.0), "A,B ~ Student-t(3)"),
+}
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def alg_bytes(M, N, K, out_type):
+    """Algorithmic HBM bytes of one GEMM: packed A and B, one scale byte per 32 elements, D."""
+    return (M + N) * K * 3 // 4 + (M + N) * K // 32 + M * N * mx.OUT_BYTES[out_type]
+
+
+def cpu_baseline(p, target_cpu_s=12.0):
+    """The reference CPU GEMM's arithmetic (dequantise to FP32, sequential FP32 dot per output,
+    oracle restatement pinned bit-exact to tests/reference.hpp) on a bounded sample of rows of the
+    same operands, on this host's cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rows = np.arange(1, dtype=np.int32)
+    t0 = time.perf_counter()
+    oracle.gemm_f32_seq(p.a_packed, p.a_row_bytes, p.a_scales, p.b_packed, p.b_row_bytes,
+                        p.b_scales, p.M, p.N, p.K, rows=rows, nthreads=1)
+    per_row = max(time.perf_counter() - t0, 1e-4)
+    nrows = int(min(p.M, max(threads, round(target_cpu_s / per_row))))
+    rows = np.linspace(0, p.M - 1, nrows).astype(np.int32)
+    t0 = time.perf_counter()
+    oracle.gemm_f32_seq(p.a_packed, p.a_row_bytes, p.a_scales, p.b_packed, p.b_row_bytes,
+                        p.b_scales, p.M, p.N, p.K, rows=rows, nthreads=threads)
+    wall = time.perf_counter() - t0
+    return {"value": round(2.0 * nrows * p.N * p.K / wall / 1e12, 6), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{nrows} of {p.M} rows of A x all {p.N} columns (cost linear in rows), "
+                      f"{wall:.2f} s wall on {threads} threads"}
+
+
+def run_config(name, steps, warmup, with_cpu):
+    import torch
+
+    M, N, K, out_type, (da, sa_), (db, sb_), desc = CONFIGS[name]
+    cfg_idx = int(name[1:])
+    t0 = time.perf_counter()
+    p = mx.make_problem(M, N, K, da, sa_, db, sb_, seed=SEED ^ cfg_idx)
+    tile = mx.choose_tile(M, N, p.Kp)
+    S = mx.splitk_segments(M, N, p.Kp)
+    bsh, sa, sb = p.layouts(tile)
+    dev = torch.device("cuda:0")
+    dA = torch.from_numpy(p.a_packed).to(dev)
+    dB = torch.from_numpy(bsh).to(dev)
+    dsa = torch.from_numpy(sa).to(dev)
+    dsb = torch.from_numpy(sb).to(dev)
+    D = torch.empty(M * N * mx.OUT_BYTES[out_type], dtype=torch.uint8, device=dev)
+    ws_bytes = mx.workspace_size(M, N, p.Kp)
+    ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
+    log(f"[bench] {name}: {M}x{N}x{K} (Kp {p.Kp}) tile {tile} S {S} ws {ws_bytes} B; "
+        f"inputs ready in {time.perf_counter() - t0:.1f} s")
+    stream = torch.cuda.current_stream()
+    args = (out_type, M, N, p.Kp, dA.data_ptr(), dB.data_ptr(), dsa.data_ptr(), dsb.data_ptr(),
+            D.data_ptr(), p.a_row_bytes, ws.data_ptr() if ws_bytes else 0, ws_bytes)
+
+    def step():
+        rc = mx.gemm(*args, stream=stream.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"mxfp6_gemm failed: {mx.STATUS.get(rc, rc)}")
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - w0) * 1e3
+    ms = ev0.elapsed_time(ev1) / steps
+    flops = 2.0 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+    # best of 4 reps of 20 back-to-back launches (the reference's own methodology)
+    best = ms
+    for _ in range(4):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(20):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) / 20)
+    log(f"[bench] {name}: {ms * 1e3:.1f} us/step over {steps} steps ({tflops:.1f} TFLOP/s), "
+        f"best-of-reps {best * 1e3:.1f} us, wall {wall_ms:.1f} ms")
+    out = {
+        "metric": "MXFP6 GEMM TFLOPs (FP16 out) and % of MXFP6 MFMA peak, 1xMI355X",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp6_e2m3 (fp32 accumulate)",
+        "data": "synthetic",
+        "config": {"workload": f"mxfp6_gemm_{M}x{N}x{K}_{mx.OUT_NAMES[out_type]}", "M": M, "N": N,
+                   "K": K, "Kp": p.Kp, "out": mx.OUT_NAMES[out_type], "inputs": desc,
+                   "tile": list(tile), "splitk": S, "a_layout": "compact",
+                   "parallelism": "single GPU"},
+        "pct_of_peak": round(100.0 * tflops / PEAK_TFLOPS, 2),
+        "best_rep_tflops": round(flops / (best * 1e-3) / 1e12, 2),
+        "hbm_gbs_alg": round(alg_bytes(M, N, K, out_type) / (ms * 1e-3) / 1e9, 1),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_TFLOPS, 4), "traffic": None},
+    }
+    if with_cpu:
+        log(f"[bench] {name}: CPU baseline ...")
+        out["cpu_baseline"] = cpu_baseline(p)
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--all", action="store_true", help="every workload, one JSON line each")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py runs on exactly one GPU; --gpus {a.gpus} is not supported (the MXFP6 "
+              "GEMM here is a single-GPU library; multi-GPU sharding is design-only).",
+              file=sys.stderr)
+        sys.exit(2)
+    names = sorted(CONFIGS) if a.all else [a.config]
+    for n in names:
+        print(json.dumps(run_config(n, a.steps, a.warmup, not a.no_cpu)), flush=True)
+
+
+if __name__ == "__main__":
+    main()

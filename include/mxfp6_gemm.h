@@ -1,0 +1,155 @@
+/* libmxfp6gemm — C ABI of the MI355X (gfx950) MXFP6 GEMM.
+ *
+ * Plain C: pointers, ints and sizes only, no C++ or HIP types, so any FFI (ctypes, cgo, JNI,
+ * N-API) binds it. Each entry point names the reference interface it stands for
+ * (eeezio/mxfp6-gemm, path:line). The C++ API of include/mxfp6/gemm.hpp is exported from the
+ * same library and calls the same code.
+ *
+ * Conventions
+ *   - Functions returning int return an mxfp6_status (0 = success). The reference API has no
+ *     status; these codes are additive. Invalid arguments are reported, never launched.
+ *   - Device pointers (d*, ws) are caller-owned device memory; nothing here allocates or frees
+ *     device memory.
+ *   - `stream` is a hipStream_t passed as void*; NULL is the null stream.
+ *   - out_type: 0 = FP32, 1 = FP16, 2 = BF16 (the order of mxfp6::OutType).
+ */
+#ifndef MXFP6_GEMM_H
+#define MXFP6_GEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mxfp6_status {
+    MXFP6_OK = 0,
+    MXFP6_ERR_NULL = 1,      /* a required pointer is NULL */
+    MXFP6_ERR_SHAPE = 2,     /* M, N, Kp or a row stride violates the kernel's requirements */
+    MXFP6_ERR_OUT_TYPE = 3,  /* out_type not in {0, 1, 2} */
+    MXFP6_ERR_TILE = 4,      /* tile not implemented, or it does not divide the shape */
+    MXFP6_ERR_ARG = 5,       /* other invalid argument */
+    MXFP6_ERR_HIP = 6        /* the HIP runtime reported an error at launch */
+} mxfp6_status;
+
+/* ---- GEMM (reference include/mxfp6/gemm.hpp, src/gemm.cpp) -------------------------------- */
+
+/* kpad(K): K rounded up to a multiple of K_TILE = 192.   Replaces gemm.hpp:30-33. */
+int mxfp6_kpad(int K);
+
+/* choose_tile(M, N, Kp) -> tile[4] = {MT, NT, MPW, NPW}.   Replaces gemm.hpp:46 / gemm.cpp:12-59. */
+int mxfp6_choose_tile(int M, int N, int Kp, int tile[4]);
+
+/* gemm_workspace_size(M, N, Kp): split-K FP32 workspace bytes, 0 if unsplit.
+ * Replaces gemm.hpp:53 / gemm.cpp:61-63. */
+size_t mxfp6_gemm_workspace_size(int M, int N, int Kp);
+
+/* Number of K segments gemm() uses for (M, N, Kp) when given a sufficient workspace.
+ * Replaces src/dispatch.hpp:30-53 (detail::splitk_S). */
+int mxfp6_splitk_segments(int M, int N, int Kp);
+
+/* gemm(ot, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, B_row_bytes, ws, ws_bytes) on the
+ * null stream. Same arguments and semantics as gemm.hpp:63-64 / gemm.cpp:65-83, plus a status:
+ * a shape that would split with a NULL or short workspace runs unsplit (stderr warning, status
+ * MXFP6_OK), as the reference does. */
+int mxfp6_gemm(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
+               const uint8_t* dsA, const uint8_t* dsB, void* dD, int A_row_bytes, int B_row_bytes,
+               void* ws, size_t ws_bytes);
+
+/* mxfp6_gemm on an explicit HIP stream (additive; the reference has no stream argument). */
+int mxfp6_gemm_async(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
+                     const uint8_t* dsA, const uint8_t* dsB, void* dD, int A_row_bytes,
+                     int B_row_bytes, void* ws, size_t ws_bytes, void* stream);
+
+/* gemm_force_tile: run the tile {MT, NT, MPW, NPW} given by the caller instead of the router's
+ * choice, unsplit. Test-only in the reference (src/gemm.cpp:85-107, not in its header); the
+ * scales must be tiled with this tile's MPW/NPW. Rejects tiles the library does not implement. */
+int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4], const void* dA,
+                          const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
+                          int A_row_bytes, int B_row_bytes, void* stream);
+
+/* The direct kernel (one wave per 32x32 block, operands read straight from global memory, any
+ * scale grouping mpw/npw in 1..4) with an explicit K split count. A second, independent GPU
+ * implementation used to cross-check the pipelined kernels; no counterpart in the reference.
+ * splits > 1 needs ws of splits*M*N*4 bytes. */
+int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, int npw, const void* dA,
+                      const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
+                      int A_row_bytes, int splits, void* ws, size_t ws_bytes, void* stream);
+
+/* ---- element formats (reference include/mxfp6/types.hpp) ---------------------------------- */
+
+float mxfp6_fp6_e2m3_to_float(uint8_t code);    /* types.hpp:13-24 */
+uint8_t mxfp6_float_to_fp6_e2m3(float v);       /* types.hpp:26-72 */
+float mxfp6_e8m0_to_float(uint8_t code);        /* types.hpp:78-81 */
+uint8_t mxfp6_float_to_e8m0(float v);           /* types.hpp:83-92 */
+int mxfp6_pack_fp6(const uint8_t* vals, int n, uint8_t* packed);   /* types.hpp:97-117 */
+int mxfp6_unpack_fp6(const uint8_t* packed, int n, uint8_t* vals); /* types.hpp:104-122 */
+
+/* ---- host layouts (reference include/mxfp6/preprocess.hpp) -------------------------------- */
+
+/* a_compact_end_pad(K).   preprocess.hpp:26-28 */
+int mxfp6_a_compact_end_pad(int K);
+
+/* pad_scales_k: scales[dim][K/32] -> out[dim][kpad(K)/32], tail code 127.   preprocess.hpp:32-38 */
+int mxfp6_pad_scales_k(const uint8_t* scales, int dim, int K, uint8_t* out);
+
+/* quantize_to_mxfp6: mat[rows][cols] -> packed[rows][3*cols/4], scales[rows][cols/32].
+ * preprocess.hpp:51-97 */
+int mxfp6_quantize(const float* mat, int rows, int cols, uint8_t* packed, uint8_t* scales);
+
+/* dequantize_mxfp6: packed + scales -> out[rows][cols].   preprocess.hpp:100-109 */
+int mxfp6_dequantize(const uint8_t* packed, const uint8_t* scales, int rows, int cols, float* out);
+
+/* preprocess_B: B[K][N] row-major -> quantised B^T: packed[N][3*K/4], scales[N][K/32].
+ * preprocess.hpp:112-118 */
+int mxfp6_preprocess_b(const float* B, int K, int N, uint8_t* packed, uint8_t* scales);
+
+/* preprocess_scale: scales[dim][K/32] -> out[dim/32][K/64][64].   preprocess.hpp:136-162 */
+int mxfp6_preprocess_scale(const uint8_t* scales, int dim, int K, uint8_t* out);
+
+/* preshuffle_B: packed B^T[N][row_bytes] (row_bytes >= 3*K/4) -> out[N/32][K/64][1536].
+ * preprocess.hpp:182-207 (the reference reads rows of exactly 3*K/4 bytes). */
+int mxfp6_preshuffle_b(const uint8_t* packed, int N, int K, int row_bytes, uint8_t* out);
+
+/* tile_scale: preprocess_scale output for (dim, K) -> grouped layout.   preprocess.hpp:216-233 */
+size_t mxfp6_tile_scale_bytes(int dim, int K, int group, int subs);
+int mxfp6_tile_scale(const uint8_t* pscale, int dim, int K, int group, int subs, uint8_t* out);
+
+/* ---- synthetic operands (the benchmark workloads) ----------------------------------------- */
+
+/* Distributions of mxfp6_gen_operand. */
+enum { MXFP6_DIST_NORMAL = 0, MXFP6_DIST_UNIFORM = 1, MXFP6_DIST_STUDENT_T3 = 2 };
+
+/* Fill rows x K values (K % 32 == 0) from a PCG32 stream (O'Neill; state seeded by (seed,
+ * stream), row r starting at draw r * draws_per_row so rows are independent of the thread
+ * count) and quantise every 32-block with the OCP MX rule: scale = 2^(floor(log2 amax) - 2),
+ * codes = nearest E2M3 of x / scale (saturating at 7.5), all-zero block -> code 127.
+ *   dist: MXFP6_DIST_NORMAL (N(0, sigma^2)), MXFP6_DIST_UNIFORM (U[-sigma, sigma]),
+ *         MXFP6_DIST_STUDENT_T3 (sigma * t with 3 degrees of freedom)
+ *   packed: rows x row_bytes bytes; row r's codes at r * row_bytes, 3*K/4 bytes; bytes past
+ *           3*K/4 in a row (up to row_bytes) are set to 0 (a zero K-tail)
+ *   scales: rows x scale_cols bytes; columns past K/32 set to 127
+ *   nthreads <= 0 uses the hardware concurrency. */
+int mxfp6_gen_operand(int rows, int K, int dist, double sigma, uint64_t seed, uint64_t stream,
+                      uint8_t* packed, size_t row_bytes, uint8_t* scales, int scale_cols,
+                      int nthreads);
+
+/* The same values as mxfp6_gen_operand before quantisation (float), for tests. */
+int mxfp6_gen_values(int rows, int K, int dist, double sigma, uint64_t seed, uint64_t stream,
+                     float* out, int nthreads);
+
+/* Prepare kernel-ready device-layout buffers on the host from raw packed codes and scales:
+ *   B: packed B^T[N][b_row_bytes] (Kp codes per row) -> preshuffled bsh (N/32 * Kp/64 * 1536 B)
+ *   scales[dim][Kp/32] -> tiled (preprocess_scale then tile_scale(group, 3)).
+ * Multi-threaded versions of preshuffle_B and tile_scale(preprocess_scale(..)). */
+int mxfp6_prepare_b(const uint8_t* packed, int N, int Kp, size_t b_row_bytes, uint8_t* bsh,
+                    int nthreads);
+int mxfp6_prepare_scales(const uint8_t* scales, int dim, int Kp, int group, uint8_t* tiled,
+                         int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXFP6_GEMM_H */

@@ -1,0 +1,78 @@
+// HIP launch layer: maps a host plan (mxfp6_launch_desc) onto kernel instantiations, grids and
+// a stream. This file and the kernels it includes are the only HIP code in the library.
+#include "../hip_layer.h"
+#include "direct_kernel.hpp"
+#include "reduce_kernel.hpp"
+#include "tile_kernel.hpp"
+
+using namespace mxfp6_dev;
+
+namespace {
+
+template <typename OutT>
+int launch_reduce(const mxfp6_launch_desc* d, hipStream_t st) {
+    const size_t total = (size_t)d->M * d->N;
+    const unsigned blocks = (unsigned)((total / 4 + 255) / 256);
+    reduce_splitk_kernel<OutT><<<dim3(blocks), dim3(256), 0, st>>>(d->ws, static_cast<OutT*>(d->D),
+                                                                  total, d->splits);
+    return 0;
+}
+
+template <typename OutT>
+int launch_direct(const mxfp6_launch_desc* d, hipStream_t st) {
+    const dim3 grid((unsigned)(d->M / 64), (unsigned)(d->N / 64), (unsigned)d->splits);
+    const uint8_t* A = static_cast<const uint8_t*>(d->A);
+    const uint8_t* B = static_cast<const uint8_t*>(d->Bsh);
+    if (d->splits > 1) {
+        direct_kernel<float, true><<<grid, dim3(256), 0, st>>>(A, B, d->sA, d->sB, nullptr, d->ws,
+                                                              d->M, d->N, d->Kp, d->A_row_bytes,
+                                                              d->mpw, d->npw, d->splits);
+        return launch_reduce<OutT>(d, st);
+    }
+    direct_kernel<OutT, false><<<grid, dim3(256), 0, st>>>(A, B, d->sA, d->sB,
+                                                          static_cast<OutT*>(d->D), nullptr, d->M,
+                                                          d->N, d->Kp, d->A_row_bytes, d->mpw,
+                                                          d->npw, 1);
+    return 0;
+}
+
+template <typename OutT>
+int launch_typed(const mxfp6_launch_desc* d, hipStream_t st) {
+    switch (d->kernel) {
+        case MXFP6_KERNEL_DIRECT:
+            return launch_direct<OutT>(d, st);
+        case MXFP6_KERNEL_TILE: {
+            const int rc = tile_launch<OutT>(d, st);
+            if (rc != 0 || d->splits <= 1) return rc;
+            return launch_reduce<OutT>(d, st);
+        }
+        default:
+            return 1;
+    }
+}
+
+}  // namespace
+
+extern "C" int mxfp6_hip_launch(const mxfp6_launch_desc* d) {
+    hipStream_t st = static_cast<hipStream_t>(d->stream);
+    int rc;
+    switch (d->out_type) {
+        case 0:
+            rc = launch_typed<float>(d, st);
+            break;
+        case 1:
+            rc = launch_typed<__half>(d, st);
+            break;
+        case 2:
+            rc = launch_typed<__hip_bfloat16>(d, st);
+            break;
+        default:
+            return 1;
+    }
+    if (rc != 0) return rc;
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+extern "C" int mxfp6_hip_has_tile(int MT, int NT, int mpw, int npw) {
+    return tile_supported(MT, NT, mpw, npw) ? 1 : 0;
+}

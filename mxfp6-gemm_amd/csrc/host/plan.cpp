@@ -1,0 +1,264 @@
+// Host plan of libmxfp6gemm: shape router, split-K planner, argument checks and the public entry
+// points (C++ API of include/mxfp6/gemm.hpp and the GEMM part of the C ABI in
+// include/mxfp6_gemm.h). Plain C++17 with no HIP header: every device action goes through the
+// thin launch layer declared in hip_layer.h.
+#include <cstdio>
+
+#include "../hip_layer.h"
+#include "mxfp6/gemm.hpp"
+#include "mxfp6_gemm.h"
+#include "plan.hpp"
+
+namespace mxfp6 {
+namespace plan {
+
+// ---- router ------------------------------------------------------------------------------
+//
+// Candidate tiles (each an instantiation of the pipelined kernel, 4 waves per workgroup):
+//   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3
+//   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4
+//   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2
+// A candidate must divide the shape. Its cost is the number of CU waves its grid needs times the
+// work of one workgroup (proportional to NT at a fixed MT): ceil(wg / CUS) * NT. The cheapest
+// wins; ties go to the wider tile, which re-reads A fewer times (A traffic ~ N/NT).
+// Workgroup-starved shapes are split along K afterwards (splitk_segments).
+TileChoice route(int M, int N, int Kp) {
+    (void)Kp;
+    static const TileChoice cands[] = {{128, 384, 4, 3}, {128, 256, 2, 4}, {128, 128, 2, 2}};
+    TileChoice best = {128, 128, 2, 2};
+    long best_cost = -1;
+    if (M <= 0 || N <= 0 || M % 128 != 0) return best;
+    for (const TileChoice& c : cands) {
+        if (N % c.NT != 0) continue;
+        const long wg = (long)(M / c.MT) * (N / c.NT);
+        const long cost = (wg + CUS - 1) / CUS * c.NT;
+        if (best_cost < 0 || cost < best_cost) {
+            best = c;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+// K segments for (M, N, Kp). A grid that fills at most half the CUs is split into
+// S = floor(CUS / base_wg) segments (the split grid then still fits one CU wave), each at least
+// MIN_TILES_PER_SEG K-tiles long so the per-segment prologue and the FP32 round trip of the
+// partials stay small against the segment's MFMA work.
+int splitk_segments(int M, int N, int Kp) {
+    if (M <= 0 || N <= 0 || Kp <= 0) return 1;
+    const TileChoice tc = route(M, N, Kp);
+    if (M % tc.MT != 0 || N % tc.NT != 0) return 1;
+    const long base_wg = (long)(M / tc.MT) * (N / tc.NT);
+    const int k_tiles = Kp / K_TILE;
+    if (base_wg <= 0 || 2 * base_wg > CUS) return 1;
+    long S = CUS / base_wg;
+    const long s_cap = k_tiles / MIN_TILES_PER_SEG;
+    if (S > s_cap) S = s_cap;
+    return S < 2 ? 1 : (int)S;
+}
+
+size_t workspace_bytes(int M, int N, int Kp) {
+    const int S = splitk_segments(M, N, Kp);
+    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+// ---- argument checks -----------------------------------------------------------------------
+
+int check_common(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
+                 const void* dsA, const void* dsB, const void* dD, int A_row_bytes) {
+    if (out_type < 0 || out_type > 2) return MXFP6_ERR_OUT_TYPE;
+    if (!dA || !dBsh || !dsA || !dsB || !dD) return MXFP6_ERR_NULL;
+    if (M <= 0 || N <= 0 || M % 128 != 0 || N % 128 != 0) return MXFP6_ERR_SHAPE;
+    if (Kp <= 0 || Kp % K_TILE != 0) return MXFP6_ERR_SHAPE;
+    // A rows are read for packed(Kp) bytes from row * A_row_bytes; a compact row (packed(K),
+    // K > Kp - K_TILE) is at most packed(K_TILE - 32) = 120 bytes shorter than packed(Kp).
+    const long packed_kp = (long)Kp / 4 * 3;
+    if (A_row_bytes <= 0 || A_row_bytes % 4 != 0 || A_row_bytes < packed_kp - 120)
+        return MXFP6_ERR_SHAPE;
+    return MXFP6_OK;
+}
+
+const char* status_text(int st) {
+    switch (st) {
+        case MXFP6_OK: return "ok";
+        case MXFP6_ERR_NULL: return "null pointer argument";
+        case MXFP6_ERR_SHAPE: return "unsupported shape (M, N multiples of 128; Kp multiple of 192; A_row_bytes)";
+        case MXFP6_ERR_OUT_TYPE: return "out_type must be F32, F16 or BF16";
+        case MXFP6_ERR_TILE: return "tile not implemented or does not divide the shape";
+        case MXFP6_ERR_ARG: return "invalid argument";
+        case MXFP6_ERR_HIP: return "HIP launch error";
+        default: return "unknown status";
+    }
+}
+
+// ---- launch ----------------------------------------------------------------------------------
+
+int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, int kernel,
+        const void* dA, const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
+        int A_row_bytes, void* ws, void* stream) {
+    mxfp6_launch_desc d;
+    d.kernel = kernel;
+    d.out_type = out_type;
+    d.M = M;
+    d.N = N;
+    d.Kp = Kp;
+    d.MT = tc.MT;
+    d.NT = tc.NT;
+    d.mpw = tc.MPW;
+    d.npw = tc.NPW;
+    d.splits = S;
+    d.A_row_bytes = A_row_bytes;
+    d.A = dA;
+    d.Bsh = dBsh;
+    d.sA = dsA;
+    d.sB = dsB;
+    d.D = dD;
+    d.ws = static_cast<float*>(ws);
+    d.stream = stream;
+    const int rc = mxfp6_hip_launch(&d);
+    return rc == 0 ? MXFP6_OK : rc == 1 ? MXFP6_ERR_TILE : MXFP6_ERR_HIP;
+}
+
+int kernel_for(const TileChoice& tc) {
+    return mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW) ? MXFP6_KERNEL_TILE
+                                                            : MXFP6_KERNEL_DIRECT;
+}
+
+int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
+                 const uint8_t* dsA, const uint8_t* dsB, void* dD, int A_row_bytes, void* ws,
+                 size_t ws_bytes, void* stream) {
+    const int st = check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
+    if (st != MXFP6_OK) return st;
+    const TileChoice tc = route(M, N, Kp);
+    if (N % tc.NT != 0 || M % tc.MT != 0) return MXFP6_ERR_TILE;
+    int S = splitk_segments(M, N, Kp);
+    if (S > 1) {
+        const size_t need = (size_t)S * (size_t)M * (size_t)N * sizeof(float);
+        if (ws == nullptr || ws_bytes < need) {
+            std::fprintf(stderr,
+                         "[mxfp6] %dx%dx%d: split-K over %d segments needs a %zu-byte workspace, "
+                         "got %zu; running unsplit. Size it with gemm_workspace_size().\n",
+                         M, N, Kp, S, need, ws_bytes);
+            S = 1;
+        }
+    }
+    return run(out_type, M, N, Kp, tc, S, kernel_for(tc), dA, dBsh, dsA, dsB, dD, A_row_bytes,
+               S > 1 ? ws : nullptr, stream);
+}
+
+bool tile_divides(const int tile[4], int M, int N) {
+    return tile[0] > 0 && tile[1] > 0 && M % tile[0] == 0 && N % tile[1] == 0 &&
+           tile[2] >= 1 && tile[2] <= 4 && tile[3] >= 1 && tile[3] <= 4 &&
+           (M / 32) % tile[2] == 0 && (N / 32) % tile[3] == 0;
+}
+
+}  // namespace plan
+
+// ---- C++ API (include/mxfp6/gemm.hpp) ---------------------------------------------------------
+
+TileChoice choose_tile(int M, int N, int Kp) {
+    return plan::route(M, N, Kp);
+}
+
+size_t gemm_workspace_size(int M, int N, int Kp) {
+    return plan::workspace_bytes(M, N, Kp);
+}
+
+void gemm(OutType ot, int M, int N, int Kp, const void* dA, const void* dBsh, const uint8_t* dsA,
+          const uint8_t* dsB, void* dD, int A_row_bytes, int B_row_bytes, void* ws,
+          size_t ws_bytes) {
+    (void)B_row_bytes;
+    const int st = plan::gemm_checked((int)ot, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws,
+                                      ws_bytes, nullptr);
+    if (st != MXFP6_OK)
+        std::fprintf(stderr, "[mxfp6] gemm %dx%dx%d not launched: %s\n", M, N, Kp,
+                     plan::status_text(st));
+}
+
+// Test hook with the reference's signature (src/gemm.cpp:89-107; not in the public header).
+void gemm_force_tile(OutType ot, int M, int N, int Kp, TileChoice tc, const void* dA,
+                     const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
+                     int A_row_bytes, int B_row_bytes) {
+    const int tile[4] = {tc.MT, tc.NT, tc.MPW, tc.NPW};
+    const int st = mxfp6_gemm_force_tile((int)ot, M, N, Kp, tile, dA, dBsh, dsA, dsB, dD,
+                                         A_row_bytes, B_row_bytes, nullptr);
+    if (st != MXFP6_OK)
+        std::fprintf(stderr, "[mxfp6] gemm_force_tile %dx%dx%d (%dx%d) not launched: %s\n", M, N,
+                     Kp, tc.MT, tc.NT, plan::status_text(st));
+}
+
+}  // namespace mxfp6
+
+// ---- C ABI: GEMM part of include/mxfp6_gemm.h -------------------------------------------------
+
+using namespace mxfp6;
+
+extern "C" int mxfp6_kpad(int K) {
+    return kpad(K);
+}
+
+extern "C" int mxfp6_choose_tile(int M, int N, int Kp, int tile[4]) {
+    if (!tile) return MXFP6_ERR_NULL;
+    const TileChoice tc = plan::route(M, N, Kp);
+    tile[0] = tc.MT;
+    tile[1] = tc.NT;
+    tile[2] = tc.MPW;
+    tile[3] = tc.NPW;
+    return MXFP6_OK;
+}
+
+extern "C" size_t mxfp6_gemm_workspace_size(int M, int N, int Kp) {
+    return plan::workspace_bytes(M, N, Kp);
+}
+
+extern "C" int mxfp6_splitk_segments(int M, int N, int Kp) {
+    return plan::splitk_segments(M, N, Kp);
+}
+
+extern "C" int mxfp6_gemm(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
+                          const uint8_t* dsA, const uint8_t* dsB, void* dD, int A_row_bytes,
+                          int B_row_bytes, void* ws, size_t ws_bytes) {
+    (void)B_row_bytes;
+    return plan::gemm_checked(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws,
+                              ws_bytes, nullptr);
+}
+
+extern "C" int mxfp6_gemm_async(int out_type, int M, int N, int Kp, const void* dA,
+                                const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
+                                int A_row_bytes, int B_row_bytes, void* ws, size_t ws_bytes,
+                                void* stream) {
+    (void)B_row_bytes;
+    return plan::gemm_checked(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws,
+                              ws_bytes, stream);
+}
+
+extern "C" int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4],
+                                     const void* dA, const void* dBsh, const uint8_t* dsA,
+                                     const uint8_t* dsB, void* dD, int A_row_bytes,
+                                     int B_row_bytes, void* stream) {
+    (void)B_row_bytes;
+    if (!tile) return MXFP6_ERR_NULL;
+    const int st = plan::check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
+    if (st != MXFP6_OK) return st;
+    if (!plan::tile_divides(tile, M, N)) return MXFP6_ERR_TILE;
+    const TileChoice tc = {tile[0], tile[1], tile[2], tile[3]};
+    if (!mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW)) return MXFP6_ERR_TILE;
+    return plan::run(out_type, M, N, Kp, tc, 1, MXFP6_KERNEL_TILE, dA, dBsh, dsA, dsB, dD,
+                     A_row_bytes, nullptr, stream);
+}
+
+extern "C" int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, int npw,
+                                 const void* dA, const void* dBsh, const uint8_t* dsA,
+                                 const uint8_t* dsB, void* dD, int A_row_bytes, int splits,
+                                 void* ws, size_t ws_bytes, void* stream) {
+    const int st = plan::check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
+    if (st != MXFP6_OK) return st;
+    if (mpw < 1 || mpw > 4 || npw < 1 || npw > 4 || (M / 32) % mpw != 0 || (N / 32) % npw != 0)
+        return MXFP6_ERR_ARG;
+    if (splits < 1 || splits > Kp / K_TILE) return MXFP6_ERR_ARG;
+    if (splits > 1 && (ws == nullptr || ws_bytes < (size_t)splits * M * N * sizeof(float)))
+        return MXFP6_ERR_ARG;
+    const TileChoice tc = {128, 128, mpw, npw};
+    return plan::run(out_type, M, N, Kp, tc, splits, MXFP6_KERNEL_DIRECT, dA, dBsh, dsA, dsB, dD,
+                     A_row_bytes, splits > 1 ? ws : nullptr, stream);
+}

@@ -1,0 +1,175 @@
+"""GPU parity of the MXFP6 GEMM against the FP64 oracle (tolerances in tests/checks.py).
+
+Inputs: the seeded PCG32 workload generator with the OCP MX scale rule; A compact
+(A_row_bytes = packed(K), a_compact_end_pad) unless stated; outputs poisoned with 0x5A so an
+unwritten element fails. Every launch goes through the library's C ABI.
+"""
+import numpy as np
+import pytest
+
+import checks
+import mxfp6_amd as mx
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def g():
+    import gpu_util
+    return gpu_util
+
+
+def _oracle(orc, p, rows=None):
+    return orc.problem_f64(p, rows=rows)
+
+
+# ---- the small benchmark workload, routed ------------------------------------------------------
+
+def test_small_config_fp32(g, orc):
+    """256x256x1024, FP32 out, N(0,1): the CPU-runnable benchmark workload, full check."""
+    p = mx.make_problem(256, 256, 1024)
+    dp = g.DevProblem(p, mx.choose_tile(256, 256, p.Kp))
+    D = g.run_routed(dp, mx.OUT_F32)
+    R, ab = _oracle(orc, p)
+    rel = checks.check_f32(D, R, ab)
+    g.say(f"    normwise max|D-R|/max|R| = {rel:.3e}")
+
+
+@pytest.mark.parametrize("out_type", [0, 1, 2])
+@pytest.mark.parametrize("M,N,K", [(128, 128, 192), (256, 384, 768), (384, 256, 960),
+                                   (512, 768, 1152)])
+def test_routed_small_shapes(g, orc, out_type, M, N, K):
+    p = mx.make_problem(M, N, K, seed=M * 3 + N * 7 + K)
+    dp = g.DevProblem(p, mx.choose_tile(M, N, p.Kp))
+    D = g.run_routed(dp, out_type)
+    R, ab = _oracle(orc, p)
+    checks.check(D, R, ab, out_type)
+
+
+@pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3)])
+@pytest.mark.parametrize("out_type", [0, 1, 2])
+def test_forced_tiles(g, orc, tile, out_type):
+    M, N, K = 256, 768, 960  # K-tail: kpad(960) = 1152
+    p = mx.make_problem(M, N, K, dist_a=mx.DIST_STUDENT_T3, dist_b=mx.DIST_STUDENT_T3, seed=11)
+    D = g.run_forced(g.DevProblem(p, tile), out_type)
+    R, ab = _oracle(orc, p)
+    checks.check(D, R, ab, out_type)
+
+
+# ---- the direct kernel (independent implementation) ------------------------------------------
+
+@pytest.mark.parametrize("groups", [(1, 1), (2, 2), (4, 3), (2, 4), (4, 4)])
+@pytest.mark.parametrize("out_type", [0, 1, 2])
+def test_direct_kernel(g, orc, groups, out_type):
+    M, N, K = 256, 384, 1024
+    if (N // 32) % groups[1] or (M // 32) % groups[0]:
+        pytest.skip("grouping does not divide")
+    p = mx.make_problem(M, N, K, seed=sum(groups) + out_type)
+    dp = g.DevProblem(p, (128, 128) + groups)
+    D = g.run_direct(dp, out_type)
+    R, ab = _oracle(orc, p)
+    checks.check(D, R, ab, out_type)
+
+
+@pytest.mark.parametrize("splits", [2, 3, 5])
+def test_direct_split_k(g, orc, splits):
+    p = mx.make_problem(256, 256, 3072, seed=splits)
+    dp = g.DevProblem(p, (128, 128, 2, 2))
+    D = g.run_direct(dp, mx.OUT_F16, splits=splits)
+    R, ab = _oracle(orc, p)
+    checks.check(D, R, ab, mx.OUT_F16)
+
+
+# ---- split-K through the router -----------------------------------------------------------------
+
+def test_routed_split_k_and_fallback(g, orc):
+    M, N, K = 512, 512, 3072
+    p = mx.make_problem(M, N, K, seed=21)
+    S = mx.splitk_segments(M, N, p.Kp)
+    assert S > 1
+    dp = g.DevProblem(p, mx.choose_tile(M, N, p.Kp))
+    R, ab = _oracle(orc, p)
+    for out_type in (0, 1, 2):
+        D = g.run_routed(dp, out_type, with_ws=True)
+        checks.check(D, R, ab, out_type)
+    # no workspace: runs unsplit (stderr warning), same bar
+    D = g.run_routed(dp, mx.OUT_F32, with_ws=False)
+    checks.check(D, R, ab, mx.OUT_F32)
+
+
+def test_split_k_uneven_segments_large_k(g, orc):
+    """Narrow N, large K: the split path with k_tiles % S != 0 (checked on sampled rows)."""
+    M, N, K = 2048, 1024, 12256  # kpad 12288 = 64 K-tiles
+    p = mx.make_problem(M, N, K, seed=31)
+    S = mx.splitk_segments(M, N, p.Kp)
+    assert S > 1
+    dp = g.DevProblem(p, mx.choose_tile(M, N, p.Kp))
+    rows = np.r_[0:8, 1000:1008, M - 8:M]
+    R, ab = _oracle(orc, p, rows)
+    D = g.run_routed(dp, mx.OUT_F32)
+    checks.check(D[rows], R, ab, mx.OUT_F32)
+
+
+# ---- layout variants and failure behaviour ------------------------------------------------------
+
+def test_compact_and_padded_a_agree(g):
+    M, N, K = 256, 256, 928
+    pc = mx.make_problem(M, N, K, seed=41, compact=True)
+    pp = mx.make_problem(M, N, K, seed=41, compact=False)
+    assert np.array_equal(pc.a_codes_view(), pp.a_codes_view())
+    t = mx.choose_tile(M, N, pc.Kp)
+    Dc = g.run_routed(g.DevProblem(pc, t), mx.OUT_F32)
+    Dp = g.run_routed(g.DevProblem(pp, t), mx.OUT_F32)
+    assert np.array_equal(Dc.view(np.uint32), Dp.view(np.uint32))
+
+
+def test_nan_scale_poisons_its_row(g, orc):
+    M, N, K = 256, 256, 768
+    p = mx.make_problem(M, N, K, seed=51)
+    p.a_scales[77, 5] = 255  # E8M0 NaN in one A block
+    dp = g.DevProblem(p, mx.choose_tile(M, N, p.Kp))
+    D = g.run_routed(dp, mx.OUT_F32)
+    R, ab = _oracle(orc, p)
+    assert np.isnan(D[77]).all()
+    checks.check_f32(D, R, ab)
+
+
+def test_stream_entry_point(g, orc):
+    import torch
+    p = mx.make_problem(256, 512, 1152, seed=61)
+    dp = g.DevProblem(p, mx.choose_tile(256, 512, p.Kp))
+    s = torch.cuda.Stream()
+    D = g.run_routed(dp, mx.OUT_BF16, stream=s)
+    R, ab = _oracle(orc, p)
+    checks.check(D, R, ab, mx.OUT_BF16)
+
+
+# ---- cross-library parity with the reference GPU library ----------------------------------------
+
+@pytest.mark.parametrize("M,N,K,out_type", [(512, 512, 768, 0), (768, 1280, 960, 1),
+                                            (4096, 4096, 768, 1), (2048, 1024, 12288, 0)])
+def test_reference_library_same_inputs(g, orc, ref_lib, M, N, K, out_type):
+    """Our D and the reference library's D on the same operands (each with the scale grouping
+    of its own router) both meet the oracle bar, and agree with each other."""
+    import ctypes as C
+    import torch
+    p = mx.make_problem(M, N, K, seed=M * 3 + N * 7 + K)
+    ours = g.run_routed(g.DevProblem(p, mx.choose_tile(M, N, p.Kp)), out_type)
+    t = (C.c_int * 4)()
+    ref_lib.ref_choose_tile(M, N, p.Kp, t)
+    dr = g.DevProblem(p, tuple(t))
+    D = dr.out(out_type)
+    wsb = ref_lib.ref_gemm_workspace_size(M, N, p.Kp)
+    ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device="cuda")
+    a, b, sa, sb = dr.ptrs()
+    g.say(f"  reference library {M}x{N}x{K} tile {tuple(t)} ws {wsb}")
+    ref_lib.ref_gemm(out_type, M, N, p.Kp, a, b, sa, sb, D.data_ptr(), p.a_row_bytes,
+                     p.b_row_bytes, ws.data_ptr() if wsb else None, wsb)
+    torch.cuda.synchronize()
+    theirs = g.to_f32(D, out_type, M, N)
+    rows = np.r_[0:16, M // 2:M // 2 + 16, M - 16:M]
+    R, ab = _oracle(orc, p, rows)
+    checks.check(ours[rows], R, ab, out_type)
+    checks.check(theirs[rows], R, ab, out_type)
+    same = float((ours.view(np.uint32) == theirs.view(np.uint32)).mean())
+    g.say(f"    bit-identical to the reference library: {100 * same:.2f}% of elements")
