@@ -5,48 +5,84 @@
 // FP32 AGPRs by v_mfma_scale_f32_32x32x64_f8f6f4 (FP6 E2M3 x FP6 E2M3, per-lane E8M0 scales).
 //
 // K is walked in K-tiles of 192 (three 64-wide slabs, the scale layout's grouping). Both operands
-// of a K-tile are copied global -> LDS by the direct-to-LDS DMA (global_load_lds_dwordx4), double
-// buffered: the copy of K-tile t+1 is issued right after the barrier that opens K-tile t and has
-// the whole MFMA work of K-tile t to land.
-//   B: its preshuffled layout is already in MFMA operand order (per 32x64 block: lane t's 16
-//      bytes at 16t, its last 8 bytes at 1024+8t), so a K-tile of one 32-column block is a
+// of a K-tile are copied global -> LDS by the direct-to-LDS DMA (global_load_lds_dwordx4) into a
+// two-stage ring.
+//   B: its preshuffled layout is already in MFMA operand order (per 32x64 block: lane t's first
+//      16 bytes at 16t, its last 8 at 1024+8t), so one 32-column block of a K-tile is a
 //      contiguous 4608-byte run copied verbatim; operand reads are linear ds_read_b128 + b64.
-//   A: rows of 144 bytes (the K-tile's 192 codes), copied row-major with 16-byte chunks
-//      (coalesced global reads); the operand of lane l is 24 bytes at row l%32, byte 24*(l/32)
-//      of the slab.
-//   Scales: per wave and K-tile one dwordx3 per operand from the tiled-scale layout (group =
-//      MPW for A, NPW for B); dword `sub` holds the scale bytes of the wave's blocks for slab
-//      `sub`, and the MFMA's op_sel picks the block's byte, so no shifts are needed.
+//   A: rows of 144 bytes (the K-tile's 192 codes) copied row-major in 16-byte chunks (coalesced
+//      global reads); lane l's operand is 24 bytes at row l%32, byte 24*(l/32) of the slab.
+//   Scales: the tiled-scale layout (group = MPW for A, NPW for B) keeps one group's scales of a
+//      K-tile in a contiguous 768-byte run (64 lanes x 3 dwords), so the workgroup's WM + WN runs
+//      ride the same DMA into the stage; a wave reads dword `sub` of its lane for slab `sub`, and
+//      the MFMA's op_sel picks the block's byte inside it.
+// Schedule per K-tile t (stage t%2), software-pipelined by one slab:
+//      read slab1 | MFMA slab0 | read slab2 | MFMA slab1 | wait own DMA, barrier, DMA(t+2) into
+//      this stage, read slab0 of t+1 | MFMA slab2
+// so the barrier, the DMA issue and the first LDS reads of the next K-tile overlap the last
+// slab's MFMAs, and the copy of K-tile t+1 has a whole K-tile of MFMA work to land.
+// The DMA is inline asm (M0 + global_load_lds in one statement): the compiler sees neither an
+// LDS store it cannot tell apart from the other stage's ds_reads (it would wait for the next
+// K-tile's copy before every read) nor any pending vector load in the main loop (its loop-merge
+// waits would do the same). The waits are explicit: each wave drains its own copies (vmcnt(0))
+// before the barrier that publishes a stage. The loop is peeled so its body has no branches.
+// Workgroup order: with XG > 0 the linear workgroup id is remapped so the workgroups running at
+// the same time on one XCD (ids congruent mod 8) cover an XG-row band of output tiles, sharing
+// A and B tiles in that XCD's L2.
 // Epilogue: lane l of block (mi, ni) holds column l%32 and rows 8g + 4(l/32) + r; D row-major.
-// Split-K (SPLIT): blockIdx.z selects a K segment and FP32 partials go to ws[z][M][N].
+// Split-K (SPLIT): blockIdx.z selects a K segment; FP32 partials go to ws[z][M][N].
 #pragma once
+#include <type_traits>
+
 #include "../hip_layer.h"
 #include "device_common.hpp"
 
 namespace mxfp6_dev {
 
-constexpr int KT_ELEMS = 192;        // K per K-tile
-constexpr int KT_ROW_BYTES = 144;    // packed bytes of one row per K-tile
-constexpr int KT_CHUNKS = 9;         // 16-byte chunks per row per K-tile
-constexpr int BLK_TILE_BYTES = 4608; // one 32-column B block per K-tile (3 x 1536)
+constexpr int KT_ELEMS = 192;         // K per K-tile
+constexpr int KT_ROW_BYTES = 144;     // packed bytes of one row per K-tile
+constexpr int KT_CHUNKS = 9;          // 16-byte chunks per row per K-tile
+constexpr int BLK_TILE_BYTES = 4608;  // one 32-column B block per K-tile (3 x 1536)
+constexpr int NXCD = 8;               // MI355X: 8 XCDs, workgroup id i runs on XCD i % 8
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Issue the DMA of `total` 16-byte chunks; chunk c of the workgroup's list goes to LDS
-// lds_base + 16*c, from the global address src(c). Thread tid handles c = i*256 + tid.
-template <int TOTAL, class Src>
-__device__ __forceinline__ void dma_chunks(char* lds_base, int wave, int lane, Src src) {
-#pragma unroll
-    for (int i = 0; i < (TOTAL + 255) / 256; i++) {
-        const int c0 = i * 256 + wave * 64;  // first chunk of this wave (wave-uniform)
-        const int c = c0 + lane;
-        if ((TOTAL % 256 == 0) || c < TOTAL) {
-            __builtin_amdgcn_global_load_lds(src(c), (lds_void*)(lds_base + c0 * 16), 16, 0, 0);
-        }
-    }
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-template <int MT, int NT, int WM, int WN, typename OutT, bool SPLIT>
+// 16 bytes per lane global -> LDS: lane l's bytes go to LDS m0 + 16*l. `lds` must be uniform.
+__device__ __forceinline__ void dma16(uint32_t lds, const void* gbase, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds), "v"(voff), "s"(gbase)
+                 : "memory");
+}
+
+// Same with a per-lane 64-bit global address.
+__device__ __forceinline__ void dma16_flat(uint32_t lds, const void* gaddr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(lds), "v"(gaddr)
+                 : "memory");
+}
+
+__device__ __forceinline__ void wait_vmcnt0() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// Bijective map of the linear workgroup id onto (tile_m, tile_n) such that each XCD receives a
+// contiguous run of the grouped order (groups of XG tile rows, tile_m fastest).
+__device__ __forceinline__ void xcd_tile(int gm, int gn, int XG, int pid, int& tm, int& tn) {
+    const int total = gm * gn;
+    const int per = total / NXCD, rem = total % NXCD;
+    const int x = pid % NXCD, j = pid / NXCD;
+    const int L = x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+    const int band = XG * gn;
+    const int grp = L / band, rows = min(XG, gm - grp * XG), w = L - grp * band;
+    tm = grp * XG + w % rows;
+    tn = w / rows;
+}
+
+template <int MT, int NT, int WM, int WN, int XG, typename OutT, bool SPLIT>
 __global__ void __launch_bounds__(256, 1)
     tile_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
@@ -56,39 +92,112 @@ __global__ void __launch_bounds__(256, 1)
     static_assert(WM * WN == 4, "4 waves per workgroup");
     static_assert(MPW >= 1 && MPW <= 4 && NPW >= 1 && NPW <= 4, "scale groups hold <= 4 blocks");
     constexpr int A_STAGE = MT * KT_ROW_BYTES, B_STAGE = NT * KT_ROW_BYTES;
+    constexpr int SC_GROUP = 64 * 12;  // one scale group per K-tile: 64 lanes x 3 dwords
+    constexpr int SC_STAGE = (WM + WN) * SC_GROUP;
+    constexpr int SC_CHUNKS = SC_STAGE / 16;
+    // the scale copy is one instruction; lanes past SC_CHUNKS inside a partly used wave land in
+    // this pad, waves entirely past it in the dummy area
+    constexpr int SC_PAD = (64 - SC_CHUNKS % 64) % 64 * 16;
+    constexpr int STAGE = A_STAGE + B_STAGE + SC_STAGE + SC_PAD;
+    // 1 KiB sink for the lanes of waves with no chunk in a partial DMA instruction: they copy a
+    // valid source there instead of branching around the copy (a branch would split the loop
+    // body into blocks and let the compiler sink MFMAs past the stage barrier)
+    constexpr int DUMMY = 2 * STAGE;
     constexpr int A_CHUNKS = MT * KT_CHUNKS, B_CHUNKS = NT * KT_CHUNKS;
-    __shared__ __attribute__((aligned(16))) char lds_a[2][A_STAGE];
-    __shared__ __attribute__((aligned(16))) char lds_b[2][B_STAGE];
+    static_assert(SC_CHUNKS <= 256, "one DMA instruction for the scales");
+    constexpr int A_ISS = (A_CHUNKS + 255) / 256, B_ISS = (B_CHUNKS + 255) / 256;
+    constexpr int B_BLK_CHUNKS = BLK_TILE_BYTES / 16;
+    __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE + 1024];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave / WN, wn = wave % WN;
-    const int wg_m = blockIdx.x, wg_n = blockIdx.y;
+    int wg_m = blockIdx.x, wg_n = blockIdx.y;
+    if constexpr (XG > 0) {
+        if (!SPLIT || ((gridDim.x * gridDim.y) % NXCD) == 0)
+            xcd_tile((int)gridDim.x, (int)gridDim.y, XG, (int)(blockIdx.y * gridDim.x + blockIdx.x),
+                     wg_m, wg_n);
+    }
     const int k64n = Kp / 64, k_tiles = Kp / KT_ELEMS;
     int kt0 = 0, nkt = k_tiles;
     if (SPLIT) split_segment(k_tiles, S, (int)blockIdx.z, kt0, nkt);
 
-    const uint8_t* a_rows = A + (size_t)wg_m * MT * A_row_bytes;
-    const uint8_t* b_cols = Bsh + (size_t)wg_n * (NT / 32) * k64n * OPBLK_BYTES;
-    // tiled scales of this wave: group (wg_m*WM + wm) of A, (wg_n*WN + wn) of B; 12 bytes per
-    // (K-tile, lane)
-    const uint8_t* sa_w = sA + ((size_t)(wg_m * WM + wm) * k_tiles * 64 + lane) * 12;
-    const uint8_t* sb_w = sB + ((size_t)(wg_n * WN + wn) * k_tiles * 64 + lane) * 12;
+    const uint8_t* a_base = A + (size_t)wg_m * MT * A_row_bytes;
+    const uint8_t* b_base = Bsh + (size_t)wg_n * (NT / 32) * k64n * OPBLK_BYTES;
 
-    auto issue_tile = [&](int kt, int buf) {
-        const size_t a_k = (size_t)kt * KT_ROW_BYTES;
-        dma_chunks<A_CHUNKS>(lds_a[buf], wave, lane, [&](int c) {
-            const int row = c / KT_CHUNKS, part = c - row * KT_CHUNKS;
-            return (const void*)(a_rows + (size_t)row * A_row_bytes + a_k + part * 16);
-        });
-        const size_t b_k = (size_t)kt * 3 * OPBLK_BYTES;
-        dma_chunks<B_CHUNKS>(lds_b[buf], wave, lane, [&](int c) {
-            const int blk = c / (BLK_TILE_BYTES / 16), r = c - blk * (BLK_TILE_BYTES / 16);
-            return (const void*)(b_cols + (size_t)blk * k64n * OPBLK_BYTES + b_k + r * 16);
-        });
+    // per-thread DMA source offsets (constant across K-tiles; the K-tile moves the base)
+    uint32_t a_voff[A_ISS], b_voff[B_ISS];
+#pragma unroll
+    for (int i = 0; i < A_ISS; i++) {
+        const int c = (i * 256 + tid) % A_CHUNKS, row = c / KT_CHUNKS, part = c - row * KT_CHUNKS;
+        a_voff[i] = (uint32_t)(row * A_row_bytes + part * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < B_ISS; i++) {
+        const int c = (i * 256 + tid) % B_CHUNKS, blk = c / B_BLK_CHUNKS, r = c - blk * B_BLK_CHUNKS;
+        b_voff[i] = (uint32_t)(blk * k64n * OPBLK_BYTES + r * 16);
+    }
+    // scale chunk of this thread: group tid/48 of [A groups of the workgroup | B groups],
+    // 16 bytes at r*16 of that group's 768-byte run for a K-tile (tiled-scale layout:
+    // byte ((g*k_tiles + kt)*64 + lane)*12 + 4*sub + j)
+    const uint8_t* sc_src;
+    {
+        const int t = tid < SC_CHUNKS ? tid : SC_CHUNKS - 1;
+        const int grp = t / 48, r = t - grp * 48;
+        const int g = grp < WM ? wg_m * WM + grp : wg_n * WN + (grp - WM);
+        sc_src = (grp < WM ? sA : sB) + (size_t)g * k_tiles * SC_GROUP + r * 16;
+    }
+    const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_u32(lds) + wave * 1024);
+    const uint32_t lds_dummy = __builtin_amdgcn_readfirstlane(lds_u32(lds) + DUMMY);
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+    // DMA instruction j (0 <= j < N_DMA) of K-tile kt into stage st: A chunks, B chunks, scales
+    constexpr int N_DMA = A_ISS + B_ISS + 1;
+    auto dma_op = [&](int j, int kt, int st) {
+        const uint32_t la = lds_wave + st * STAGE, lb = la + A_STAGE, ls = lb + B_STAGE;
+        if (j < A_ISS) {
+            const bool live = A_CHUNKS % 256 == 0 || j * 256 + wave_u * 64 < A_CHUNKS;
+            dma16(live ? la + j * 4096 : lds_dummy, a_base + (size_t)kt * KT_ROW_BYTES, a_voff[j]);
+        } else if (j < A_ISS + B_ISS) {
+            const int i = j - A_ISS;
+            const bool live = B_CHUNKS % 256 == 0 || i * 256 + wave_u * 64 < B_CHUNKS;
+            dma16(live ? lb + i * 4096 : lds_dummy, b_base + (size_t)kt * BLK_TILE_BYTES, b_voff[i]);
+        } else {
+            dma16_flat(wave_u * 64 < SC_CHUNKS ? ls : lds_dummy, sc_src + (size_t)kt * SC_GROUP);
+        }
     };
-    auto load_scales = [&](int kt, v3i& sa, v3i& sb) {
-        sa = *reinterpret_cast<const v3i*>(sa_w + (size_t)kt * 64 * 12);
-        sb = *reinterpret_cast<const v3i*>(sb_w + (size_t)kt * 64 * 12);
+    auto issue_tile = [&](int kt, int st) {
+#pragma unroll
+        for (int j = 0; j < N_DMA; j++) dma_op(j, kt, st);
+    };
+
+    // operand byte offsets inside a stage
+    const int a_off = (wm * MPW * 32 + (lane & 31)) * KT_ROW_BYTES + (lane >> 5) * 24;
+    const int b_off = A_STAGE + wn * NPW * BLK_TILE_BYTES + lane * 16;
+    const int b_off2 = A_STAGE + wn * NPW * BLK_TILE_BYTES + 1024 + lane * 8;
+    const int sa_off = A_STAGE + B_STAGE + wm * SC_GROUP + lane * 12;
+    const int sb_off = A_STAGE + B_STAGE + (WM + wn) * SC_GROUP + lane * 12;
+
+    struct Slab {
+        v8i a[MPW], b[NPW];
+        int sa, sb;
+    };
+    auto read_slab = [&](int st, int s, Slab& R) {
+        const char* base = lds + st * STAGE;
+#pragma unroll
+        for (int mi = 0; mi < MPW; mi++) {
+            const v6i_a8 x = *reinterpret_cast<const v6i_a8*>(base + a_off + mi * 32 * KT_ROW_BYTES + s * 48);
+            R.a[mi] = __builtin_shufflevector(x, x, 0, 1, 2, 3, 4, 5, -1, -1);
+        }
+#pragma unroll
+        for (int ni = 0; ni < NPW; ni++) {
+            const int o = ni * BLK_TILE_BYTES + s * OPBLK_BYTES;
+            const v4i y0 = *reinterpret_cast<const v4i*>(base + b_off + o);
+            const v2i y1 = *reinterpret_cast<const v2i*>(base + b_off2 + o);
+            const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
+            R.b[ni] = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
+        }
+        R.sa = *reinterpret_cast<const int*>(base + sa_off + s * 4);
+        R.sb = *reinterpret_cast<const int*>(base + sb_off + s * 4);
     };
 
     v16f acc[MPW][NPW];
@@ -97,62 +206,74 @@ __global__ void __launch_bounds__(256, 1)
 #pragma unroll
         for (int j = 0; j < NPW; j++) acc[i][j] = v16f{};
 
-    // operand byte offsets inside a stage
-    const int a_off = (wm * MPW * 32 + (lane & 31)) * KT_ROW_BYTES + (lane >> 5) * 24;
-    const int b_off = wn * NPW * BLK_TILE_BYTES + lane * 16;
-    const int b_off2 = wn * NPW * BLK_TILE_BYTES + 1024 + lane * 8;
-
-    v3i sa_cur, sb_cur, sa_nxt, sb_nxt;
-    issue_tile(kt0, 0);
-    load_scales(kt0, sa_cur, sb_cur);
-
-    for (int i = 0; i < nkt; i++) {
-        const int buf = i & 1;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (i + 1 < nkt) {
-            issue_tile(kt0 + i + 1, buf ^ 1);
-            load_scales(kt0 + i + 1, sa_nxt, sb_nxt);
-        }
-        const char* la = lds_a[buf];
-        const char* lb = lds_b[buf];
-#pragma unroll
-        for (int s = 0; s < 3; s++) {
-            v8i a[MPW], b[NPW];
-#pragma unroll
-            for (int mi = 0; mi < MPW; mi++) {
-                const char* p = la + a_off + mi * 32 * KT_ROW_BYTES + s * 48;
-                const v2i x0 = *reinterpret_cast<const v2i*>(p);
-                const v2i x1 = *reinterpret_cast<const v2i*>(p + 8);
-                const v2i x2 = *reinterpret_cast<const v2i*>(p + 16);
-                a[mi] = v8i{x0.x, x0.y, x1.x, x1.y, x2.x, x2.y, 0, 0};
-            }
-#pragma unroll
-            for (int ni = 0; ni < NPW; ni++) {
-                const v4i y0 = *reinterpret_cast<const v4i*>(lb + b_off + ni * BLK_TILE_BYTES + s * OPBLK_BYTES);
-                const v2i y1 = *reinterpret_cast<const v2i*>(lb + b_off2 + ni * BLK_TILE_BYTES + s * OPBLK_BYTES);
-                b[ni] = v8i{y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, 0, 0};
-            }
-            const int sav = sa_cur[s], sbv = sb_cur[s];
-#pragma unroll
-            for (int ni = 0; ni < NPW; ni++)
-#pragma unroll
-                for (int mi = 0; mi < MPW; mi++) {
-                    // op_sel selects byte mi of the A scale dword and byte ni of the B one
-                    switch (mi * 4 + ni) {
+    // MFMA k of a slab: block (mi, ni) = (k % MPW, k / MPW); op_sel picks byte mi of the A
+    // scale dword and byte ni of the B scale dword
+    auto mfma_one = [&](const Slab& R, int k) {
+        const int mi = k % MPW, ni = k / MPW;
+        switch (mi * 4 + ni) {
 #define MX_CASE(I, J) \
-    case I * 4 + J: acc[mi][ni] = mfma_fp6<I, J>(acc[mi][ni], a[mi], b[ni], sav, sbv); break;
-                        MX_CASE(0, 0) MX_CASE(0, 1) MX_CASE(0, 2) MX_CASE(0, 3)
-                        MX_CASE(1, 0) MX_CASE(1, 1) MX_CASE(1, 2) MX_CASE(1, 3)
-                        MX_CASE(2, 0) MX_CASE(2, 1) MX_CASE(2, 2) MX_CASE(2, 3)
-                        MX_CASE(3, 0) MX_CASE(3, 1) MX_CASE(3, 2) MX_CASE(3, 3)
+    case I * 4 + J: acc[I % MPW][J % NPW] = mfma_fp6<I, J>(acc[I % MPW][J % NPW], R.a[I % MPW], R.b[J % NPW], R.sa, R.sb); break;
+            MX_CASE(0, 0) MX_CASE(0, 1) MX_CASE(0, 2) MX_CASE(0, 3)
+            MX_CASE(1, 0) MX_CASE(1, 1) MX_CASE(1, 2) MX_CASE(1, 3)
+            MX_CASE(2, 0) MX_CASE(2, 1) MX_CASE(2, 2) MX_CASE(2, 3)
+            MX_CASE(3, 0) MX_CASE(3, 1) MX_CASE(3, 2) MX_CASE(3, 3)
 #undef MX_CASE
-                    }
-                }
         }
-        sa_cur = sa_nxt;
-        sb_cur = sb_nxt;
-    }
+    };
+    constexpr int NMF = MPW * NPW;
+    auto mfma_slab = [&](const Slab& R) {
+#pragma unroll
+        for (int k = 0; k < NMF; k++) mfma_one(R, k);
+    };
+
+    Slab R0, R1, R2;
+    // K-tile i from stage i%2; NEXT: K-tile i+1 follows (barrier + slab 0 read); DMA2: K-tile
+    // i+2 exists and is copied into this stage once every wave is done with it.
+    auto ktile = [&](int i, auto next_tag, auto dma2_tag) {
+        constexpr bool NEXT = decltype(next_tag)::value, DMA2 = decltype(dma2_tag)::value;
+        const int st = i & 1;
+        // phase boundaries are scheduling barriers: each phase's LDS reads overlap the
+        // previous slab's MFMAs, and no MFMA drifts across the stage barrier
+        read_slab(st, 1, R1);
+        mfma_slab(R0);
+        __builtin_amdgcn_sched_barrier(0);
+        read_slab(st, 2, R2);
+        mfma_slab(R1);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NEXT) {
+            wait_vmcnt0();    // this wave's copy of K-tile i+1 has landed
+            __syncthreads();  // every wave's copy landed; every wave finished reading stage st
+            read_slab(st ^ 1, 0, R0);
+            if constexpr (DMA2) {
+                // the copy of K-tile i+2 into this stage, spread over the slab's MFMAs
+                constexpr int PER = (N_DMA + NMF - 1) / NMF;
+#pragma unroll
+                for (int k = 0; k < NMF; k++) {
+                    mfma_one(R2, k);
+#pragma unroll
+                    for (int j = k * PER; j < (k + 1) * PER && j < N_DMA; j++)
+                        dma_op(j, kt0 + i + 2, st);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                return;
+            }
+        }
+        mfma_slab(R2);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+
+    // prologue: K-tile 0 resident, K-tile 1 in flight, slab 0 of K-tile 0 in registers
+    issue_tile(kt0, 0);
+    wait_vmcnt0();
+    __syncthreads();
+    if (nkt > 1) issue_tile(kt0 + 1, 1);
+    read_slab(0, 0, R0);
+    int i = 0;
+    for (; i + 2 < nkt; i++) ktile(i, T{}, T{});
+    if (i + 1 < nkt) ktile(i++, T{}, F{});
+    ktile(i, F{}, F{});
 
     // epilogue
     const int m_w = wg_m * MT + wm * MPW * 32 + 4 * (lane >> 5);
@@ -182,16 +303,16 @@ inline bool tile_supported(int MT, int NT, int mpw, int npw) {
            (MT == 256 && NT == 256 && mpw == 4 && npw == 4);
 }
 
-template <int MT, int NT, int WM, int WN, typename OutT>
+template <int MT, int NT, int WM, int WN, int XG, typename OutT>
 int tile_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     const dim3 grid((unsigned)(d->M / MT), (unsigned)(d->N / NT), (unsigned)d->splits);
     const uint8_t* A = static_cast<const uint8_t*>(d->A);
     const uint8_t* B = static_cast<const uint8_t*>(d->Bsh);
     if (d->splits > 1)
-        tile_kernel<MT, NT, WM, WN, float, true><<<grid, dim3(256), 0, st>>>(
+        tile_kernel<MT, NT, WM, WN, XG, float, true><<<grid, dim3(256), 0, st>>>(
             A, B, d->sA, d->sB, nullptr, d->ws, d->M, d->N, d->Kp, d->A_row_bytes, d->splits);
     else
-        tile_kernel<MT, NT, WM, WN, OutT, false><<<grid, dim3(256), 0, st>>>(
+        tile_kernel<MT, NT, WM, WN, XG, OutT, false><<<grid, dim3(256), 0, st>>>(
             A, B, d->sA, d->sB, static_cast<OutT*>(d->D), nullptr, d->M, d->N, d->Kp,
             d->A_row_bytes, 1);
     return 0;
@@ -200,10 +321,10 @@ int tile_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
 template <typename OutT>
 int tile_launch(const mxfp6_launch_desc* d, hipStream_t st) {
     if (!tile_supported(d->MT, d->NT, d->mpw, d->npw)) return 1;
-    if (d->MT == 128 && d->NT == 128) return tile_launch_t<128, 128, 2, 2, OutT>(d, st);
-    if (d->MT == 128 && d->NT == 256) return tile_launch_t<128, 256, 2, 2, OutT>(d, st);
-    if (d->MT == 128 && d->NT == 384) return tile_launch_t<128, 384, 1, 4, OutT>(d, st);
-    return tile_launch_t<256, 256, 2, 2, OutT>(d, st);
+    if (d->MT == 128 && d->NT == 128) return tile_launch_t<128, 128, 2, 2, 4, OutT>(d, st);
+    if (d->MT == 128 && d->NT == 256) return tile_launch_t<128, 256, 2, 2, 4, OutT>(d, st);
+    if (d->MT == 128 && d->NT == 384) return tile_launch_t<128, 384, 1, 4, 4, OutT>(d, st);
+    return tile_launch_t<256, 256, 2, 2, 4, OutT>(d, st);
 }
 
 }  // namespace mxfp6_dev

@@ -58,6 +58,6 @@ def test_argument_checks_reject_before_launch(mx):
     assert mx.gemm(0, 128, 128, 192, p, p, p, p, p, 6) == 2              # A row too short
     assert mx.gemm(0, 128, 128, 192, p, p, p, p, p, 146) == 2            # A row misaligned
     assert mx.gemm_force_tile(0, 128, 128, 192, (128, 384, 4, 3), p, p, p, p, p, 144) == 4
-    assert mx.gemm_force_tile(0, 256, 256, 192, (256, 256, 4, 4), p, p, p, p, p, 144) == 4
+    assert mx.gemm_force_tile(0, 256, 256, 192, (256, 128, 4, 2), p, p, p, p, p, 144) == 4  # not instantiated
     assert mx.gemm_direct(0, 128, 128, 192, 5, 2, p, p, p, p, p, 144) == 5
     assert mx.gemm_direct(0, 128, 128, 192, 2, 2, p, p, p, p, p, 144, splits=2) == 5

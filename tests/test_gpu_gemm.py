@@ -46,7 +46,8 @@ def test_routed_small_shapes(g, orc, out_type, M, N, K):
     checks.check(D, R, ab, out_type)
 
 
-@pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3)])
+@pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
+                                  (256, 256, 4, 4)])
 @pytest.mark.parametrize("out_type", [0, 1, 2])
 def test_forced_tiles(g, orc, tile, out_type):
     M, N, K = 256, 768, 960  # K-tail: kpad(960) = 1152
@@ -54,6 +55,31 @@ def test_forced_tiles(g, orc, tile, out_type):
     D = g.run_forced(g.DevProblem(p, tile), out_type)
     R, ab = _oracle(orc, p)
     checks.check(D, R, ab, out_type)
+
+
+@pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
+                                  (256, 256, 4, 4)])
+def test_pipelined_kernel_bitwise_equals_direct(g, tile):
+    """Both kernels add the same MFMA results in the same K order, so FP32 outputs are equal
+    bit for bit (covers every wave block, slab and stage of the pipelined kernel)."""
+    M, N, K = 512, 768, 2112  # 11 K-tiles: odd count, both ring stages, peeled tail
+    p = mx.make_problem(M, N, K, seed=71)
+    dp = g.DevProblem(p, tile)
+    Dt = g.run_forced(dp, mx.OUT_F32)
+    Dd = g.run_direct(dp, mx.OUT_F32)
+    assert np.array_equal(Dt.view(np.uint32), Dd.view(np.uint32))
+
+
+def test_pipelined_split_bitwise_equals_direct_split(g):
+    M, N, K = 512, 512, 3072
+    p = mx.make_problem(M, N, K, seed=81)
+    t = mx.choose_tile(M, N, p.Kp)
+    S = mx.splitk_segments(M, N, p.Kp)
+    assert S > 1
+    dp = g.DevProblem(p, t)
+    Dr = g.run_routed(dp, mx.OUT_F32)
+    Dd = g.run_direct(dp, mx.OUT_F32, splits=S)
+    assert np.array_equal(Dr.view(np.uint32), Dd.view(np.uint32))
 
 
 # ---- the direct kernel (independent implementation) ------------------------------------------
