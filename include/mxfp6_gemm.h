@@ -69,6 +69,14 @@ int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4],
                           const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
                           int A_row_bytes, int B_row_bytes, void* stream);
 
+/* Run an explicit plan: the pipelined kernel with tile {MT, NT, MPW, NPW} and `splits` K segments
+ * (splits > 1 needs ws of splits*M*N*4 bytes). For tuning and benchmarks of alternative plans; the
+ * scales must be tiled with this tile's MPW/NPW. No counterpart in the reference (it is the
+ * reference's gemm_force_tile, src/gemm.cpp:89-107, plus a split count). */
+int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int tile[4], int splits,
+                        const void* dA, const void* dBsh, const uint8_t* dsA, const uint8_t* dsB,
+                        void* dD, int A_row_bytes, void* ws, size_t ws_bytes, void* stream);
+
 /* The direct kernel (one wave per 32x32 block, operands read straight from global memory, any
  * scale grouping mpw/npw in 1..4) with an explicit K split count. A second, independent GPU
  * implementation used to cross-check the pipelined kernels; no counterpart in the reference.

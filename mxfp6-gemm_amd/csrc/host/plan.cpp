@@ -14,40 +14,29 @@ namespace plan {
 
 // ---- router ------------------------------------------------------------------------------
 //
-// Candidate tiles (each an instantiation of the pipelined kernel, 4 waves per workgroup):
-//   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3
-//   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4
-//   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2
-// A candidate must divide the shape. Its cost is the number of CU waves its grid needs times the
-// work of one workgroup (proportional to NT at a fixed MT): ceil(wg / CUS) * NT. The cheapest
-// wins; ties go to the wider tile, which re-reads A fewer times (A traffic ~ N/NT).
-// Workgroup-starved shapes are split along K afterwards (splitk_segments).
-TileChoice route(int M, int N, int Kp) {
-    (void)Kp;
-    static const TileChoice cands[] = {{128, 384, 4, 3}, {128, 256, 2, 4}, {128, 128, 2, 2}};
-    TileChoice best = {128, 128, 2, 2};
-    long best_cost = -1;
-    if (M <= 0 || N <= 0 || M % 128 != 0) return best;
-    for (const TileChoice& c : cands) {
-        if (N % c.NT != 0) continue;
-        const long wg = (long)(M / c.MT) * (N / c.NT);
-        const long cost = (wg + CUS - 1) / CUS * c.NT;
-        if (best_cost < 0 || cost < best_cost) {
-            best = c;
-            best_cost = cost;
-        }
-    }
-    return best;
-}
+// Candidate tiles (each an instantiation of the pipelined kernel, 4 waves per workgroup, one
+// workgroup per CU):
+//   256x256, waves 2x2, each wave 128x128 -> MPW 4, NPW 4   (work 4 units of 128x128)
+//   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3   (3 units)
+//   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4   (2 units)
+//   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (1 unit)
+// A candidate must divide the shape. Workgroup-starved grids are split along K (split_for). The
+// cost of a candidate is the number of CU waves its (split) grid needs times the work of one
+// workgroup: ceil(wg * S / CUS) * units / S. The cheapest wins; ties go to the larger tile, which
+// moves fewer operand bytes per flop (A is re-read N/NT times, B M/MT times).
+namespace {
+struct Cand {
+    TileChoice tc;
+    int units;
+};
+const Cand kCands[] = {{{256, 256, 4, 4}, 4}, {{128, 384, 4, 3}, 3}, {{128, 256, 2, 4}, 2},
+                       {{128, 128, 2, 2}, 1}};
 
-// K segments for (M, N, Kp). A grid that fills at most half the CUs is split into
-// S = floor(CUS / base_wg) segments (the split grid then still fits one CU wave), each at least
+// K segments for a tile on (M, N, Kp): a grid that fills at most half the CUs is split into
+// S = floor(CUS / base_wg) segments (the split grid still fits one CU wave), each at least
 // MIN_TILES_PER_SEG K-tiles long so the per-segment prologue and the FP32 round trip of the
 // partials stay small against the segment's MFMA work.
-int splitk_segments(int M, int N, int Kp) {
-    if (M <= 0 || N <= 0 || Kp <= 0) return 1;
-    const TileChoice tc = route(M, N, Kp);
-    if (M % tc.MT != 0 || N % tc.NT != 0) return 1;
+int split_for(const TileChoice& tc, int M, int N, int Kp) {
     const long base_wg = (long)(M / tc.MT) * (N / tc.NT);
     const int k_tiles = Kp / K_TILE;
     if (base_wg <= 0 || 2 * base_wg > CUS) return 1;
@@ -55,6 +44,31 @@ int splitk_segments(int M, int N, int Kp) {
     const long s_cap = k_tiles / MIN_TILES_PER_SEG;
     if (S > s_cap) S = s_cap;
     return S < 2 ? 1 : (int)S;
+}
+}  // namespace
+
+TileChoice route(int M, int N, int Kp) {
+    TileChoice best = {128, 128, 2, 2};
+    double best_cost = -1;
+    if (M <= 0 || N <= 0 || Kp <= 0) return best;
+    for (const Cand& c : kCands) {
+        if (M % c.tc.MT != 0 || N % c.tc.NT != 0) continue;
+        const long wg = (long)(M / c.tc.MT) * (N / c.tc.NT);
+        const int S = split_for(c.tc, M, N, Kp);
+        const double cost = (double)((wg * S + CUS - 1) / CUS) * c.units / S;
+        if (best_cost < 0 || cost < best_cost - 1e-9) {
+            best = c.tc;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+int splitk_segments(int M, int N, int Kp) {
+    if (M <= 0 || N <= 0 || Kp <= 0) return 1;
+    const TileChoice tc = route(M, N, Kp);
+    if (M % tc.MT != 0 || N % tc.NT != 0) return 1;
+    return split_for(tc, M, N, Kp);
 }
 
 size_t workspace_bytes(int M, int N, int Kp) {
@@ -245,6 +259,23 @@ extern "C" int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const i
     if (!mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW)) return MXFP6_ERR_TILE;
     return plan::run(out_type, M, N, Kp, tc, 1, MXFP6_KERNEL_TILE, dA, dBsh, dsA, dsB, dD,
                      A_row_bytes, nullptr, stream);
+}
+
+extern "C" int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int tile[4],
+                                   int splits, const void* dA, const void* dBsh,
+                                   const uint8_t* dsA, const uint8_t* dsB, void* dD,
+                                   int A_row_bytes, void* ws, size_t ws_bytes, void* stream) {
+    if (!tile) return MXFP6_ERR_NULL;
+    const int st = plan::check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
+    if (st != MXFP6_OK) return st;
+    if (!plan::tile_divides(tile, M, N)) return MXFP6_ERR_TILE;
+    const TileChoice tc = {tile[0], tile[1], tile[2], tile[3]};
+    if (!mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW)) return MXFP6_ERR_TILE;
+    if (splits < 1 || splits > Kp / K_TILE) return MXFP6_ERR_ARG;
+    if (splits > 1 && (ws == nullptr || ws_bytes < (size_t)splits * M * N * sizeof(float)))
+        return MXFP6_ERR_ARG;
+    return plan::run(out_type, M, N, Kp, tc, splits, MXFP6_KERNEL_TILE, dA, dBsh, dsA, dsB, dD,
+                     A_row_bytes, splits > 1 ? ws : nullptr, stream);
 }
 
 extern "C" int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, int npw,

@@ -46,6 +46,9 @@ SIGNATURES = {
                                    C.c_int, C.c_int, _vp, C.c_size_t, _vp]),
     "mxfp6_gemm_force_tile": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
                                         _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp]),
+    "mxfp6_gemm_explicit": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
+                                      C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, _vp, C.c_size_t,
+                                      _vp]),
     "mxfp6_gemm_direct": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp,
                                     _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp, C.c_size_t, _vp]),
     "mxfp6_fp6_e2m3_to_float": (C.c_float, [C.c_uint8]),
@@ -148,6 +151,13 @@ def gemm_force_tile(out_type, M, N, Kp, tile, dA, dBsh, dsA, dsB, dD, A_row_byte
     t = (C.c_int * 4)(*tile)
     return lib().mxfp6_gemm_force_tile(out_type, M, N, Kp, t, dA, dBsh, dsA, dsB, dD,
                                        A_row_bytes, 0, stream)
+
+
+def gemm_explicit(out_type, M, N, Kp, tile, splits, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws=0,
+                  ws_bytes=0, stream=None):
+    t = (C.c_int * 4)(*tile)
+    return lib().mxfp6_gemm_explicit(out_type, M, N, Kp, t, splits, dA, dBsh, dsA, dsB, dD,
+                                     A_row_bytes, ws or None, ws_bytes, stream)
 
 
 def gemm_direct(out_type, M, N, Kp, mpw, npw, dA, dBsh, dsA, dsB, dD, A_row_bytes, splits=1,

@@ -322,13 +322,16 @@ int o_gemm_f64(const uint8_t* a_packed, size_t a_row_bytes, const uint8_t* a_sca
 /* FP32 dequantised row: fp6 value (float) times e8m0 scale (float), as reference.hpp:20-22 via
  * dequantize_mxfp6 (preprocess.hpp:100-109). */
 static void dequant_row_f32(const uint8_t* packed, const uint8_t* scales, int K, float* out) {
-    uint8_t codes[4];
+    static float lut[64];
+    static int ready = 0;
+    if (!ready) {
+        for (int c = 0; c < 64; c++) lut[c] = (float)o_fp6_decode((uint8_t)c);
+        ready = 1;
+    }
     for (int g = 0; g < K / 4; g++) {
-        o_unpack(packed + 3 * g, 4, codes);
-        for (int i = 0; i < 4; i++) {
-            const int k = 4 * g + i;
-            out[k] = (float)o_fp6_decode(codes[i]) * (float)o_e8m0_decode(scales[k / 32]);
-        }
+        const uint32_t w = packed[3 * g] | ((uint32_t)packed[3 * g + 1] << 8) | ((uint32_t)packed[3 * g + 2] << 16);
+        const float s = (float)o_e8m0_decode(scales[(4 * g) / 32]);
+        for (int i = 0; i < 4; i++) out[4 * g + i] = lut[(w >> (6 * i)) & 63] * s;
     }
 }
 
@@ -360,23 +363,28 @@ static void* f32_trampoline(void* arg) {
     return f32_worker(arg);
 }
 
-int o_gemm_f32_seq(const uint8_t* a_packed, size_t a_row_bytes, const uint8_t* a_scales,
-                   int a_scale_cols, const uint8_t* b_packed, size_t b_row_bytes,
-                   const uint8_t* b_scales, int b_scale_cols, int M, int N, int K,
-                   const int* rows, int nrows, float* D, int nthreads) {
+int o_dequant_f32(const uint8_t* packed, size_t row_bytes, const uint8_t* scales,
+                  int scale_cols, int rows, int K, float* out) {
     if (K % 32 != 0) return 1;
-    float* bf = (float*)malloc(sizeof(float) * (size_t)N * K);
-    if (!bf) return 2;
-    for (int n = 0; n < N; n++)
-        dequant_row_f32(b_packed + (size_t)n * b_row_bytes, b_scales + (size_t)n * b_scale_cols, K,
-                        bf + (size_t)n * K);
+    dequant_row_f32(packed, scales, 32, out); /* initialise the table on this thread */
+    for (int r = 0; r < rows; r++)
+        dequant_row_f32(packed + (size_t)r * row_bytes, scales + (size_t)r * scale_cols, K,
+                        out + (size_t)r * K);
+    return 0;
+}
+
+int o_gemm_f32_seq_deq(const uint8_t* a_packed, size_t a_row_bytes, const uint8_t* a_scales,
+                       int a_scale_cols, const float* bf, int M, int N, int K, const int* rows,
+                       int nrows, float* D, int nthreads) {
+    if (K % 32 != 0) return 1;
+    float tmp[32];
+    dequant_row_f32(a_packed, a_scales, 32, tmp); /* initialise the table before the threads */
     gemm_job j;
     memset(&j, 0, sizeof j);
     j.ap = a_packed; j.as = a_scales; j.arb = a_row_bytes; j.asc = a_scale_cols;
     j.M = M; j.N = N; j.K = K; j.rows = rows; j.nrows = rows ? nrows : M;
     j.Df = D; j.nthreads = nthreads;
     f32_ctx c = {&j, bf};
-    /* run_pool passes the job; wrap the context instead */
     int nt = nthreads > 0 ? nthreads : (int)sysconf(_SC_NPROCESSORS_ONLN);
     if (nt < 1) nt = 1;
     if (nt > 64) nt = 64;
@@ -385,6 +393,19 @@ int o_gemm_f32_seq(const uint8_t* a_packed, size_t a_row_bytes, const uint8_t* a
     for (int t = 0; t < nt; t++) pthread_create(&th[t], NULL, f32_trampoline, &c);
     for (int t = 0; t < nt; t++) pthread_join(th[t], NULL);
     pthread_mutex_destroy(&j.mu);
-    free(bf);
     return 0;
+}
+
+int o_gemm_f32_seq(const uint8_t* a_packed, size_t a_row_bytes, const uint8_t* a_scales,
+                   int a_scale_cols, const uint8_t* b_packed, size_t b_row_bytes,
+                   const uint8_t* b_scales, int b_scale_cols, int M, int N, int K,
+                   const int* rows, int nrows, float* D, int nthreads) {
+    if (K % 32 != 0) return 1;
+    float* bf = (float*)malloc(sizeof(float) * (size_t)N * K);
+    if (!bf) return 2;
+    o_dequant_f32(b_packed, b_row_bytes, b_scales, b_scale_cols, N, K, bf);
+    const int rc = o_gemm_f32_seq_deq(a_packed, a_row_bytes, a_scales, a_scale_cols, bf, M, N, K,
+                                      rows, nrows, D, nthreads);
+    free(bf);
+    return rc;
 }

@@ -67,6 +67,14 @@ int o_gemm_f32_seq(const uint8_t* a_packed, size_t a_row_bytes, const uint8_t* a
                    const uint8_t* b_scales, int b_scale_cols, int M, int N, int K,
                    const int* rows, int nrows, float* D, int nthreads);
 
+/* The two halves of o_gemm_f32_seq: dequantise rows to FP32 once, then the sequential dots of
+ * the listed A rows against the dequantised B^T bf[N][K]. */
+int o_dequant_f32(const uint8_t* packed, size_t row_bytes, const uint8_t* scales,
+                  int scale_cols, int rows, int K, float* out);
+int o_gemm_f32_seq_deq(const uint8_t* a_packed, size_t a_row_bytes, const uint8_t* a_scales,
+                       int a_scale_cols, const float* bf, int M, int N, int K, const int* rows,
+                       int nrows, float* D, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

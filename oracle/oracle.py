@@ -36,6 +36,9 @@ _SIG = {
                              C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, C.c_int]),
     "o_gemm_f32_seq": (C.c_int, [_vp, C.c_size_t, _vp, C.c_int, _vp, C.c_size_t, _vp, C.c_int,
                                  C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int]),
+    "o_dequant_f32": (C.c_int, [_vp, C.c_size_t, _vp, C.c_int, C.c_int, C.c_int, _vp]),
+    "o_gemm_f32_seq_deq": (C.c_int, [_vp, C.c_size_t, _vp, C.c_int, _vp, C.c_int, C.c_int,
+                                     C.c_int, _vp, C.c_int, _vp, C.c_int]),
 }
 _REF_SIG = {
     "ref_fp6_decode": (C.c_float, [C.c_uint8]),
@@ -125,6 +128,24 @@ def gemm_f32_seq(a_packed, a_row_bytes, a_scales, b_packed, b_row_bytes, b_scale
                               None if ridx is None else _p(ridx), nr, _p(D), nthreads)
     if rc != 0:
         raise RuntimeError(f"o_gemm_f32_seq failed ({rc})")
+    return D
+
+
+def dequant_f32(packed, row_bytes, scales, rows, K):
+    scales = np.ascontiguousarray(scales)
+    out = np.empty((rows, K), dtype=np.float32)
+    if lib().o_dequant_f32(_p(packed), row_bytes, _p(scales), scales.shape[1], rows, K, _p(out)):
+        raise RuntimeError("o_dequant_f32 failed")
+    return out
+
+
+def gemm_f32_seq_deq(a_packed, a_row_bytes, a_scales, bf, M, N, K, rows, nthreads=0):
+    a_scales = np.ascontiguousarray(a_scales)
+    ridx = np.ascontiguousarray(rows, dtype=np.int32)
+    D = np.empty((len(ridx), N), dtype=np.float32)
+    if lib().o_gemm_f32_seq_deq(_p(a_packed), a_row_bytes, _p(a_scales), a_scales.shape[1],
+                                _p(bf), M, N, K, _p(ridx), len(ridx), _p(D), nthreads):
+        raise RuntimeError("o_gemm_f32_seq_deq failed")
     return D
 
 

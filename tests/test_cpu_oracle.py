@@ -83,6 +83,16 @@ def test_f32_seq_bit_exact_with_reference(mx, orc, ref_lib):
     assert (np.abs(R - D) <= K * 2.0 ** -24 * ab).all()
 
 
+def test_f32_seq_split_equals_whole(mx, orc):
+    p = mx.make_problem(32, 48, 576, seed=13)
+    D = orc.gemm_f32_seq(p.a_packed, p.a_row_bytes, p.a_scales, p.b_packed, p.b_row_bytes,
+                         p.b_scales, 32, 48, 576)
+    bf = orc.dequant_f32(p.b_packed, p.b_row_bytes, p.b_scales, 48, 576)
+    rows = [3, 0, 31]
+    Ds = orc.gemm_f32_seq_deq(p.a_packed, p.a_row_bytes, p.a_scales, bf, 32, 48, 576, rows)
+    assert np.array_equal(Ds.view(np.uint32), D[rows].view(np.uint32))
+
+
 def test_f64_row_subset_equals_full(mx, orc):
     p = mx.make_problem(96, 128, 576, seed=9)
     D, ab = orc.problem_f64(p)

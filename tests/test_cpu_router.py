@@ -16,7 +16,7 @@ GOLD = os.path.join(os.path.dirname(__file__), "golden")
 with open(os.path.join(GOLD, "ref_routing.json")) as f:
     REF = json.load(f)
 
-IMPLEMENTED = {(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3)}
+IMPLEMENTED = {(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3), (256, 256, 4, 4)}
 
 
 def _kpad(K):
@@ -84,10 +84,11 @@ def test_router_degenerate_shapes_do_not_trap(mx):
 
 
 def test_router_benchmark_shapes(mx):
-    # the MI355X routing of the five benchmark workloads (cost: CU waves x NT; ties -> wider NT)
+    # the MI355X routing of the five benchmark workloads (cost: CU waves x workgroup work, ties
+    # to the larger tile)
     want = {
         (256, 256, 1024): ((128, 128, 2, 2), 1),
-        (8192, 8192, 8192): ((128, 256, 2, 4), 1),
+        (8192, 8192, 8192): ((256, 256, 4, 4), 1),
         (2048, 6144, 16128): ((128, 384, 4, 3), 1),
         (2048, 1024, 105728): None,
         (2048, 5120, 105728): ((128, 128, 2, 2), 1),
