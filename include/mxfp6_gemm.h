@@ -41,8 +41,10 @@ int mxfp6_kpad(int K);
 /* choose_tile(M, N, Kp) -> tile[4] = {MT, NT, MPW, NPW}.   Replaces gemm.hpp:46 / gemm.cpp:12-59. */
 int mxfp6_choose_tile(int M, int N, int Kp, int tile[4]);
 
-/* gemm_workspace_size(M, N, Kp): split-K FP32 workspace bytes, 0 if unsplit.
- * Replaces gemm.hpp:53 / gemm.cpp:61-63. */
+/* gemm_workspace_size(M, N, Kp): workspace bytes gemm() uses for (M, N, Kp), 0 if none: the
+ * split-K FP32 partials of a split shape, plus (at the next 256-byte boundary) M * packed(Kp)
+ * bytes when the plan repacks A into the preshuffled operand layout first (mxfp6_gemm_repacks_a).
+ * Replaces gemm.hpp:53 / gemm.cpp:61-63 (there: the split-K partials only). */
 size_t mxfp6_gemm_workspace_size(int M, int N, int Kp);
 
 /* Number of K segments gemm() uses for (M, N, Kp) when given a sufficient workspace.
@@ -52,7 +54,8 @@ int mxfp6_splitk_segments(int M, int N, int Kp);
 /* gemm(ot, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, B_row_bytes, ws, ws_bytes) on the
  * null stream. Same arguments and semantics as gemm.hpp:63-64 / gemm.cpp:65-83, plus a status:
  * a shape that would split with a NULL or short workspace runs unsplit (stderr warning, status
- * MXFP6_OK), as the reference does. */
+ * MXFP6_OK), as the reference does. A workspace too short for the repacked A (but long enough
+ * for the partials) only skips the repack: same result, slower. */
 int mxfp6_gemm(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
                const uint8_t* dsA, const uint8_t* dsB, void* dD, int A_row_bytes, int B_row_bytes,
                void* ws, size_t ws_bytes);
@@ -69,13 +72,30 @@ int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4],
                           const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
                           int A_row_bytes, int B_row_bytes, void* stream);
 
-/* Run an explicit plan: the pipelined kernel with tile {MT, NT, MPW, NPW} and `splits` K segments
- * (splits > 1 needs ws of splits*M*N*4 bytes). For tuning and benchmarks of alternative plans; the
- * scales must be tiled with this tile's MPW/NPW. No counterpart in the reference (it is the
- * reference's gemm_force_tile, src/gemm.cpp:89-107, plus a split count). */
+/* Run an explicit plan: the pipelined kernel with tile {MT, NT, MPW, NPW}, `splits` K segments and
+ * a_repack (1: A is first repacked into the preshuffled layout). Needs ws of
+ * mxfp6_plan_workspace_size(M, N, Kp, splits, a_repack) bytes. For tuning and benchmarks of
+ * alternative plans; the scales must be tiled with this tile's MPW/NPW. No counterpart in the
+ * reference (it is the reference's gemm_force_tile, src/gemm.cpp:89-107, plus a split count and
+ * the repack switch). */
 int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int tile[4], int splits,
-                        const void* dA, const void* dBsh, const uint8_t* dsA, const uint8_t* dsB,
-                        void* dD, int A_row_bytes, void* ws, size_t ws_bytes, void* stream);
+                        int a_repack, const void* dA, const void* dBsh, const uint8_t* dsA,
+                        const uint8_t* dsB, void* dD, int A_row_bytes, void* ws, size_t ws_bytes,
+                        void* stream);
+
+/* Whether gemm() repacks A for (M, N, Kp) when its workspace allows. No counterpart in the
+ * reference (its kernels read A row-major). */
+int mxfp6_gemm_repacks_a(int M, int N, int Kp);
+
+/* Workspace bytes of an explicit plan (0 when splits == 1 and a_repack == 0). */
+size_t mxfp6_plan_workspace_size(int M, int N, int Kp, int splits, int a_repack);
+
+/* On-device preshuffle of `rows` (multiple of 32) row-major packed rows, each read for packed(Kp)
+ * bytes from src + r * row_bytes, into dst (rows * packed(Kp) bytes) in the layout of
+ * preshuffle_B (reference include/mxfp6/preprocess.hpp:182-207, which runs on the host). Used by
+ * gemm() to repack A; applied to B^T it gives preshuffle_B's output on the GPU. */
+int mxfp6_preshuffle_rows_async(const void* src, int row_bytes, int rows, int Kp, void* dst,
+                                void* stream);
 
 /* The direct kernel (one wave per 32x32 block, operands read straight from global memory, any
  * scale grouping mpw/npw in 1..4) with an explicit K split count. A second, independent GPU

@@ -3,7 +3,7 @@
 #include "../hip_layer.h"
 #include "direct_kernel.hpp"
 #include "reduce_kernel.hpp"
-#include "tile_kernel.hpp"
+#include "slab_kernel.hpp"
 
 using namespace mxfp6_dev;
 
@@ -42,7 +42,7 @@ int launch_typed(const mxfp6_launch_desc* d, hipStream_t st) {
         case MXFP6_KERNEL_DIRECT:
             return launch_direct<OutT>(d, st);
         case MXFP6_KERNEL_TILE: {
-            const int rc = tile_launch<OutT>(d, st);
+            const int rc = slab_launch<OutT>(d, st);
             if (rc != 0 || d->splits <= 1) return rc;
             return launch_reduce<OutT>(d, st);
         }
@@ -70,6 +70,15 @@ extern "C" int mxfp6_hip_launch(const mxfp6_launch_desc* d) {
             return 1;
     }
     if (rc != 0) return rc;
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+extern "C" int mxfp6_hip_repack(const void* src, int row_bytes, int rows, int Kp, void* dst,
+                                void* stream) {
+    const int k64n = Kp / 64;
+    repack_rows_kernel<<<dim3((unsigned)((k64n + REPACK_KK - 1) / REPACK_KK), (unsigned)(rows / 32)),
+                         dim3(REPACK_THREADS), 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint8_t*>(src), row_bytes, k64n, static_cast<uint8_t*>(dst));
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

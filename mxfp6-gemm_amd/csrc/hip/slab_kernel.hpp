@@ -1,0 +1,346 @@
+// Slab-ring MXFP6 tile kernel for gfx950.
+//
+// Same tile decomposition as tile_kernel.hpp (MT x NT per workgroup, WM x WN waves, each wave
+// MPW x NPW 32x32 blocks accumulated by v_mfma_scale_f32_32x32x64_f8f6f4), but the LDS ring holds
+// single 64-wide K slabs instead of 192-wide K-tiles: NS stages, each with the slab's A rows
+// (48 bytes per row), its B blocks (one 1536-byte preshuffled 32x64 block per 32 columns, copied
+// verbatim) and the workgroup's scale dwords for the slab (one dword per lane per scale group,
+// gathered from the tiled-scale layout with 4-byte LDS DMA). With one slab per stage:
+//   * every slab issues only D = A_ISS + B_ISS + SC_ISS copy instructions per wave, spread over
+//     that slab's MFMAs, so the vector-memory queue never fills and stalls the in-order issue of
+//     the next MFMA (a whole K-tile's copies issued at once did);
+//   * NS - 1 slabs are in flight ahead of the one being multiplied (latency slack);
+//   * a wave waits only for its own copies of the next slab: vmcnt((NS - 2) * D), exact because
+//     every wave issues the same D instructions per slab (waves with nothing to copy in a partial
+//     instruction copy into a dummy LDS area instead of branching).
+// Schedule of slab q (registers R[q%2] hold slab q, read during slab q-1):
+//     wait (own copies of slab q+1) | barrier | copy slab q+NS into stage q%NS, read slab q+1 into
+//     R[(q+1)%2], interleaved with the MFMAs of slab q
+// The barrier certifies slab q+1 (every wave's copies landed) and frees stage q%NS (every wave
+// read slab q before it). The loop body is branch-free (peeled head and tail).
+#pragma once
+
+#include "../hip_layer.h"
+#include "device_common.hpp"
+#include "repack_kernel.hpp"
+#include "tile_kernel.hpp"  // dma16, dma16_flat, lds_u32, opaque_v, xcd_tile, wait_vmcnt0
+
+namespace mxfp6_dev {
+
+// 4 bytes per lane global -> LDS: lane l's dword goes to LDS m0 + 4*l.
+__device__ __forceinline__ void dma4_flat(uint32_t lds, const void* gaddr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+                 :
+                 : "s"(lds), "v"(gaddr)
+                 : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int MT, int NT, int WM, int WN, int NS>
+struct SlabGeom {
+    static constexpr int MPW = MT / 32 / WM, NPW = NT / 32 / WN;
+    static constexpr int NWAVES = WM * WN, THREADS = 64 * NWAVES;
+    static constexpr int A_BYTES = MT * SLAB_BYTES;           // A rows of one slab
+    static constexpr int B_BYTES = NT / 32 * OPBLK_BYTES;      // B blocks of one slab
+    static constexpr int SC_GROUPS = WM + WN;                  // scale groups of the workgroup
+    static constexpr int SC_BYTES = SC_GROUPS * 256;           // one dword per lane per group
+    static constexpr int STAGE = A_BYTES + B_BYTES + SC_BYTES;
+    static constexpr int A_CHUNKS = A_BYTES / 16, B_CHUNKS = B_BYTES / 16;
+    static constexpr int A_ISS = (A_CHUNKS + THREADS - 1) / THREADS;
+    static constexpr int B_ISS = (B_CHUNKS + THREADS - 1) / THREADS;
+    static constexpr int SC_ISS = (SC_GROUPS + NWAVES - 1) / NWAVES;
+    static constexpr int D = A_ISS + B_ISS + SC_ISS;           // copy instructions per wave per slab
+    static constexpr int LDS = NS * STAGE + 1024;              // + dummy sink
+    static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole-wave chunks");
+    static_assert(STAGE % 16 == 0, "16-byte aligned stages");
+    static_assert((NS - 2) * D <= 63, "vmcnt range");
+};
+
+template <int MT, int NT, int WM, int WN, int NS, int XG, typename OutT, bool SPLIT, bool ASH>
+__global__ void __launch_bounds__(64 * WM * WN, 1)
+    slab_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
+                const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
+                OutT* __restrict__ D, float* __restrict__ ws, int M, int N, int Kp,
+                int A_row_bytes, int S) {
+    using G = SlabGeom<MT, NT, WM, WN, NS>;
+    constexpr int MPW = G::MPW, NPW = G::NPW, THREADS = G::THREADS, STAGE = G::STAGE;
+    static_assert(G::NWAVES == 4 || G::NWAVES == 8, "4 or 8 waves per workgroup");
+    static_assert(MPW >= 1 && MPW <= 4 && NPW >= 1 && NPW <= 4, "scale groups hold <= 4 blocks");
+    static_assert(NS >= 3, "ring depth");
+    __shared__ __attribute__((aligned(1024))) char lds[G::LDS];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave / WN, wn = wave % WN;
+    int wg_m = blockIdx.x, wg_n = blockIdx.y;
+    if constexpr (XG > 0) {
+        if (!SPLIT || ((gridDim.x * gridDim.y) % NXCD) == 0)
+            xcd_tile((int)gridDim.x, (int)gridDim.y, XG, (int)(blockIdx.y * gridDim.x + blockIdx.x),
+                     wg_m, wg_n);
+    }
+    const int k64n = Kp / 64, k_tiles = Kp / 192;
+    int kt0 = 0, nkt = k_tiles;
+    if (SPLIT) split_segment(k_tiles, S, (int)blockIdx.z, kt0, nkt);
+    const int q0 = kt0 * 3, nq = nkt * 3;  // first slab and slab count of this workgroup
+
+    const uint8_t* a_base = ASH ? A + (size_t)wg_m * (MT / 32) * k64n * OPBLK_BYTES
+                                : A + (size_t)wg_m * MT * A_row_bytes;
+    const uint8_t* b_base = Bsh + (size_t)wg_n * (NT / 32) * k64n * OPBLK_BYTES;
+
+    // per-thread copy sources (offsets from the slab's base, constant across slabs)
+    uint32_t a_voff[G::A_ISS], b_voff[G::B_ISS];
+#pragma unroll
+    for (int i = 0; i < G::A_ISS; i++) {
+        const int c = (i * THREADS + tid) % G::A_CHUNKS;
+        if (ASH) {
+            const int blk = c / 96, r = c - blk * 96;
+            a_voff[i] = (uint32_t)(blk * k64n * OPBLK_BYTES + r * 16);
+        } else {
+            const int row = c / 3, part = c - row * 3;
+            a_voff[i] = (uint32_t)(row * A_row_bytes + part * 16);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < G::B_ISS; i++) {
+        const int c = (i * THREADS + tid) % G::B_CHUNKS, blk = c / 96, r = c - blk * 96;
+        b_voff[i] = (uint32_t)(blk * k64n * OPBLK_BYTES + r * 16);
+    }
+    // scale gather: wave w copies group i*NWAVES + w of [A groups | B groups]; lane l's dword of
+    // slab q lives at ((g*k_tiles + q/3)*64 + l)*12 + 4*(q%3) of that group's tiled scales
+    const uint8_t* sc_src[G::SC_ISS];
+#pragma unroll
+    for (int i = 0; i < G::SC_ISS; i++) {
+        int grp = i * G::NWAVES + wave;
+        if (grp >= G::SC_GROUPS) grp = G::SC_GROUPS - 1;  // dummy copy: valid source
+        const int g = grp < WM ? wg_m * WM + grp : wg_n * WN + (grp - WM);
+        sc_src[i] = (grp < WM ? sA : sB) + ((size_t)g * k_tiles * 64 + lane) * 12;
+    }
+    const uint32_t lds0 = lds_u32(lds);
+    const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds0 + wave * 1024);
+    const uint32_t lds_sc_wave = __builtin_amdgcn_readfirstlane(lds0 + G::A_BYTES + G::B_BYTES + wave * 256);
+    const uint32_t lds_dummy = __builtin_amdgcn_readfirstlane(lds0 + NS * STAGE);
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+    // copy instruction j (0 <= j < D) of global slab q into stage st
+    auto dma_op = [&](int j, int q, int st) {
+        const uint32_t so = st * STAGE;
+        if (j < G::A_ISS) {
+            const bool live = G::A_CHUNKS % THREADS == 0 || j * THREADS + wave_u * 64 < G::A_CHUNKS;
+            dma16(live ? lds_wave + so + j * THREADS * 16 : lds_dummy,
+                  a_base + (size_t)q * (ASH ? OPBLK_BYTES : SLAB_BYTES), a_voff[j]);
+        } else if (j < G::A_ISS + G::B_ISS) {
+            const int i = j - G::A_ISS;
+            const bool live = G::B_CHUNKS % THREADS == 0 || i * THREADS + wave_u * 64 < G::B_CHUNKS;
+            dma16(live ? lds_wave + so + G::A_BYTES + i * THREADS * 16 : lds_dummy,
+                  b_base + (size_t)q * OPBLK_BYTES, b_voff[i]);
+        } else {
+            const int i = j - G::A_ISS - G::B_ISS;
+            const bool live = i * G::NWAVES + wave_u < G::SC_GROUPS;
+            dma4_flat(live ? lds_sc_wave + so + i * G::NWAVES * 256 : lds_dummy,
+                      sc_src[i] + (size_t)(q / 3) * 768 + (q % 3) * 4);
+        }
+    };
+
+    // operand reads (offsets hidden per operand so reads of different operands are not fused)
+    const lds_cptr lds3 = (lds_cptr)lds;
+    const int a_off = ASH ? wm * MPW * OPBLK_BYTES + lane * 16
+                          : (wm * MPW * 32 + (lane & 31)) * SLAB_BYTES + (lane >> 5) * 24;
+    const int b_off = G::A_BYTES + wn * NPW * OPBLK_BYTES + lane * 16;
+    const int sa_off = G::A_BYTES + G::B_BYTES + wm * 256 + lane * 4;
+    const int sb_off = G::A_BYTES + G::B_BYTES + (WM + wn) * 256 + lane * 4;
+    struct Slab {
+        v8i a[MPW], b[NPW];
+        int sa, sb;
+    };
+    // Operand reads of one slab as items: item 0 = both scale dwords, then the A and B operands in
+    // the order the slab's MFMAs first use them (MFMA k multiplies a[k % MPW] by b[k / MPW]).
+    constexpr int ITEMS = 1 + MPW + NPW;
+    auto read_item = [&](int item, uint32_t base, Slab& R) {
+        if (item == 0) {
+            R.sa = *reinterpret_cast<const __attribute__((address_space(3))) int*>(lds3 + base + sa_off);
+            R.sb = *reinterpret_cast<const __attribute__((address_space(3))) int*>(lds3 + base + sb_off);
+            return;
+        }
+        // items: 1 = A0, 2 = B0, 3 .. MPW+1 = A1 .. A(MPW-1), MPW+2 .. = B1 .. B(NPW-1)
+        int kind_b, idx;
+        if (item == 1) {
+            kind_b = 0, idx = 0;
+        } else if (item == 2) {
+            kind_b = 1, idx = 0;
+        } else if (item < 2 + MPW) {
+            kind_b = 0, idx = item - 2;
+        } else {
+            kind_b = 1, idx = item - 1 - MPW;
+        }
+        if (!kind_b && ASH) {
+            const uint32_t o = opaque_v(base + a_off + idx * OPBLK_BYTES);
+            const v4i y0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(lds3 + o);
+            const v2i y1 = *reinterpret_cast<const __attribute__((address_space(3))) v2i*>(lds3 + o + (1024 - 8 * lane));
+            const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
+            R.a[idx] = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
+        } else if (!kind_b) {
+            const uint32_t o = opaque_v(base + a_off + idx * 32 * SLAB_BYTES);
+            const v6i_a8 x = *reinterpret_cast<const __attribute__((address_space(3))) v6i_a8*>(lds3 + o);
+            R.a[idx] = __builtin_shufflevector(x, x, 0, 1, 2, 3, 4, 5, -1, -1);
+        } else {
+            const uint32_t o = opaque_v(base + b_off + idx * OPBLK_BYTES);
+            const v4i y0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(lds3 + o);
+            const v2i y1 = *reinterpret_cast<const __attribute__((address_space(3))) v2i*>(lds3 + o + (1024 - 8 * lane));
+            const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
+            R.b[idx] = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
+        }
+    };
+    auto read_slab = [&](int st, Slab& R) {
+#pragma unroll
+        for (int i = 0; i < ITEMS; i++) read_item(i, st * STAGE, R);
+    };
+
+    v16f acc[MPW][NPW];
+#pragma unroll
+    for (int i = 0; i < MPW; i++)
+#pragma unroll
+        for (int j = 0; j < NPW; j++) acc[i][j] = v16f{};
+    constexpr int NMF = MPW * NPW;
+    auto mfma_one = [&](const Slab& R, int k) {
+        const int mi = k % MPW, ni = k / MPW;
+        switch (mi * 4 + ni) {
+#define MX_CASE(I, J) \
+    case I * 4 + J: acc[I % MPW][J % NPW] = mfma_fp6<I, J>(acc[I % MPW][J % NPW], R.a[I % MPW], R.b[J % NPW], R.sa, R.sb); break;
+            MX_CASE(0, 0) MX_CASE(0, 1) MX_CASE(0, 2) MX_CASE(0, 3)
+            MX_CASE(1, 0) MX_CASE(1, 1) MX_CASE(1, 2) MX_CASE(1, 3)
+            MX_CASE(2, 0) MX_CASE(2, 1) MX_CASE(2, 2) MX_CASE(2, 3)
+            MX_CASE(3, 0) MX_CASE(3, 1) MX_CASE(3, 2) MX_CASE(3, 3)
+#undef MX_CASE
+        }
+    };
+
+    Slab R0, R1;
+    // Steady-state slab q: multiply Rc (slab q) while reading slab q+1 into Rn and copying slab
+    // q+NS into stage q%NS. Every wave has issued D copies per slab, so after the copies of slab
+    // q+1 exactly NS-2 newer slabs are in flight: vmcnt((NS-2)*D) leaves only them pending.
+    // Placement in the MFMA sequence: read item i after MFMA i * NMF / (ITEMS + 1) and copy j after
+    // MFMA j * NMF / D, so that no wave ever issues a burst of LDS or vector-memory instructions
+    // (with one wave per SIMD, a wave blocked on a full LDS or address queue idles its MFMA unit).
+    auto slab_step = [&](int q, Slab& Rc, Slab& Rn) {
+        const int st = q % NS;
+        wait_vmcnt<(NS - 2) * G::D>();
+        __syncthreads();  // slab q+1 landed for every wave; every wave is done reading stage st
+        const uint32_t rbase = ((q + 1) % NS) * STAGE;
+#pragma unroll
+        for (int k = 0; k < NMF; k++) {
+            mfma_one(Rc, k);
+#pragma unroll
+            for (int i = 0; i < ITEMS; i++)
+                if (i * NMF / (ITEMS + 1) == k) read_item(i, rbase, Rn);
+#pragma unroll
+            for (int j = 0; j < G::D; j++)
+                if (j * NMF / G::D == k) dma_op(j, q0 + q + NS, st);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // Tail slab q (the last NS+1 slabs): the same with runtime conditions, full waits and the
+    // remaining copies issued in one block.
+    auto tail_step = [&](int q, Slab& Rc, Slab& Rn) {
+        if (q + 1 < nq) {
+            wait_vmcnt0();
+            __syncthreads();
+            read_slab((q + 1) % NS, Rn);
+            if (q + NS < nq) {
+#pragma unroll
+                for (int j = 0; j < G::D; j++) dma_op(j, q0 + q + NS, q % NS);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NMF; k++) mfma_one(Rc, k);
+    };
+
+    // prologue: slabs 0..min(NS, nq)-1 in flight, slab 0 resident and read
+    const int pro = nq < NS ? nq : NS;
+    for (int q = 0; q < pro; q++)
+#pragma unroll
+        for (int j = 0; j < G::D; j++) dma_op(j, q0 + q, q);
+    wait_vmcnt0();
+    __syncthreads();
+    read_slab(0, R0);
+
+    int q = 0;
+    // two slabs per iteration keep the register roles static; the body is branch-free
+    for (; q + 1 + NS < nq; q += 2) {
+        slab_step(q, R0, R1);
+        slab_step(q + 1, R1, R0);
+    }
+    for (; q < nq; q += 2) {
+        tail_step(q, R0, R1);
+        if (q + 1 < nq) tail_step(q + 1, R1, R0);
+    }
+
+    // epilogue
+    wait_vmcnt0();
+    const int m_w = wg_m * MT + wm * MPW * 32 + 4 * (lane >> 5);
+    const int n_w = wg_n * NT + wn * NPW * 32 + (lane & 31);
+#pragma unroll
+    for (int mi = 0; mi < MPW; mi++)
+#pragma unroll
+        for (int ni = 0; ni < NPW; ni++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const size_t idx = (size_t)(m_w + mi * 32 + 8 * g + r) * N + n_w + ni * 32;
+                    if (SPLIT)
+                        ws[(size_t)blockIdx.z * M * N + idx] = acc[mi][ni][4 * g + r];
+                    else
+                        D[idx] = cvt_out<OutT>(acc[mi][ni][4 * g + r]);
+                }
+}
+
+// ---- instantiations and launch -------------------------------------------------------------------
+
+// Ring depth per tile: as many slabs as fit 160 KiB of LDS (128 x 128: half of it, two
+// workgroups per CU).
+template <int MT, int NT, int WM, int WN, int XG, int NS, typename OutT, bool ASH>
+void slab_launch_a(const mxfp6_launch_desc* d, const uint8_t* A, hipStream_t st) {
+    const dim3 grid((unsigned)(d->M / MT), (unsigned)(d->N / NT), (unsigned)d->splits);
+    const dim3 block(64 * WM * WN);
+    const uint8_t* B = static_cast<const uint8_t*>(d->Bsh);
+    if (d->splits > 1)
+        slab_kernel<MT, NT, WM, WN, NS, XG, float, true, ASH><<<grid, block, 0, st>>>(
+            A, B, d->sA, d->sB, nullptr, d->ws, d->M, d->N, d->Kp, d->A_row_bytes, d->splits);
+    else
+        slab_kernel<MT, NT, WM, WN, NS, XG, OutT, false, ASH><<<grid, block, 0, st>>>(
+            A, B, d->sA, d->sB, static_cast<OutT*>(d->D), nullptr, d->M, d->N, d->Kp,
+            d->A_row_bytes, 1);
+}
+
+template <int MT, int NT, int WM, int WN, int XG, int NS, typename OutT>
+int slab_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
+    static_assert(SlabGeom<MT, NT, WM, WN, NS>::LDS <= 160 * 1024, "LDS budget");
+    if (d->Ash != nullptr) {
+        // repack A into the preshuffled layout, then run the kernel on it
+        const int k64n = d->Kp / 64;
+        repack_rows_kernel<<<dim3((unsigned)((k64n + REPACK_KK - 1) / REPACK_KK), (unsigned)(d->M / 32)),
+                             dim3(REPACK_THREADS), 0, st>>>(static_cast<const uint8_t*>(d->A),
+                                                            d->A_row_bytes, k64n,
+                                                            static_cast<uint8_t*>(d->Ash));
+        slab_launch_a<MT, NT, WM, WN, XG, NS, OutT, true>(d, static_cast<const uint8_t*>(d->Ash), st);
+    } else {
+        slab_launch_a<MT, NT, WM, WN, XG, NS, OutT, false>(d, static_cast<const uint8_t*>(d->A), st);
+    }
+    return 0;
+}
+
+template <typename OutT>
+int slab_launch(const mxfp6_launch_desc* d, hipStream_t st) {
+    if (!tile_supported(d->MT, d->NT, d->mpw, d->npw)) return 1;
+    if (d->MT == 128 && d->NT == 128) return slab_launch_t<128, 128, 2, 2, 4, 6, OutT>(d, st);
+    if (d->MT == 128 && d->NT == 256) return slab_launch_t<128, 256, 2, 2, 4, 8, OutT>(d, st);
+    if (d->MT == 128 && d->NT == 384) return slab_launch_t<128, 384, 1, 4, 4, 6, OutT>(d, st);
+    if (d->mpw == 2) return slab_launch_t<256, 256, 4, 2, 4, 6, OutT>(d, st);
+    return slab_launch_t<256, 256, 2, 2, 4, 6, OutT>(d, st);
+}
+
+}  // namespace mxfp6_dev

@@ -65,6 +65,14 @@ __device__ __forceinline__ void dma16_flat(uint32_t lds, const void* gaddr) {
                  : "memory");
 }
 
+typedef __attribute__((address_space(3))) const char* lds_cptr;
+
+// Returns x unchanged, hidden from the optimizer (forces a VGPR, defeats offset folding).
+__device__ __forceinline__ uint32_t opaque_v(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 __device__ __forceinline__ void wait_vmcnt0() {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
@@ -83,13 +91,14 @@ __device__ __forceinline__ void xcd_tile(int gm, int gn, int XG, int pid, int& t
 }
 
 template <int MT, int NT, int WM, int WN, int XG, typename OutT, bool SPLIT>
-__global__ void __launch_bounds__(256, 1)
+__global__ void __launch_bounds__(64 * WM * WN, 1)
     tile_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
                 OutT* __restrict__ D, float* __restrict__ ws, int M, int N, int Kp,
                 int A_row_bytes, int S) {
     constexpr int MPW = MT / 32 / WM, NPW = NT / 32 / WN;
-    static_assert(WM * WN == 4, "4 waves per workgroup");
+    constexpr int NWAVES = WM * WN, THREADS = 64 * NWAVES;
+    static_assert(NWAVES == 4 || NWAVES == 8, "4 or 8 waves per workgroup");
     static_assert(MPW >= 1 && MPW <= 4 && NPW >= 1 && NPW <= 4, "scale groups hold <= 4 blocks");
     constexpr int A_STAGE = MT * KT_ROW_BYTES, B_STAGE = NT * KT_ROW_BYTES;
     constexpr int SC_GROUP = 64 * 12;  // one scale group per K-tile: 64 lanes x 3 dwords
@@ -104,8 +113,9 @@ __global__ void __launch_bounds__(256, 1)
     // body into blocks and let the compiler sink MFMAs past the stage barrier)
     constexpr int DUMMY = 2 * STAGE;
     constexpr int A_CHUNKS = MT * KT_CHUNKS, B_CHUNKS = NT * KT_CHUNKS;
-    static_assert(SC_CHUNKS <= 256, "one DMA instruction for the scales");
-    constexpr int A_ISS = (A_CHUNKS + 255) / 256, B_ISS = (B_CHUNKS + 255) / 256;
+    static_assert(SC_CHUNKS <= THREADS, "one DMA instruction for the scales");
+    constexpr int A_ISS = (A_CHUNKS + THREADS - 1) / THREADS;
+    constexpr int B_ISS = (B_CHUNKS + THREADS - 1) / THREADS;
     constexpr int B_BLK_CHUNKS = BLK_TILE_BYTES / 16;
     __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE + 1024];
 
@@ -128,12 +138,12 @@ __global__ void __launch_bounds__(256, 1)
     uint32_t a_voff[A_ISS], b_voff[B_ISS];
 #pragma unroll
     for (int i = 0; i < A_ISS; i++) {
-        const int c = (i * 256 + tid) % A_CHUNKS, row = c / KT_CHUNKS, part = c - row * KT_CHUNKS;
+        const int c = (i * THREADS + tid) % A_CHUNKS, row = c / KT_CHUNKS, part = c - row * KT_CHUNKS;
         a_voff[i] = (uint32_t)(row * A_row_bytes + part * 16);
     }
 #pragma unroll
     for (int i = 0; i < B_ISS; i++) {
-        const int c = (i * 256 + tid) % B_CHUNKS, blk = c / B_BLK_CHUNKS, r = c - blk * B_BLK_CHUNKS;
+        const int c = (i * THREADS + tid) % B_CHUNKS, blk = c / B_BLK_CHUNKS, r = c - blk * B_BLK_CHUNKS;
         b_voff[i] = (uint32_t)(blk * k64n * OPBLK_BYTES + r * 16);
     }
     // scale chunk of this thread: group tid/48 of [A groups of the workgroup | B groups],
@@ -155,12 +165,14 @@ __global__ void __launch_bounds__(256, 1)
     auto dma_op = [&](int j, int kt, int st) {
         const uint32_t la = lds_wave + st * STAGE, lb = la + A_STAGE, ls = lb + B_STAGE;
         if (j < A_ISS) {
-            const bool live = A_CHUNKS % 256 == 0 || j * 256 + wave_u * 64 < A_CHUNKS;
-            dma16(live ? la + j * 4096 : lds_dummy, a_base + (size_t)kt * KT_ROW_BYTES, a_voff[j]);
+            const bool live = A_CHUNKS % THREADS == 0 || j * THREADS + wave_u * 64 < A_CHUNKS;
+            dma16(live ? la + j * THREADS * 16 : lds_dummy, a_base + (size_t)kt * KT_ROW_BYTES,
+                  a_voff[j]);
         } else if (j < A_ISS + B_ISS) {
             const int i = j - A_ISS;
-            const bool live = B_CHUNKS % 256 == 0 || i * 256 + wave_u * 64 < B_CHUNKS;
-            dma16(live ? lb + i * 4096 : lds_dummy, b_base + (size_t)kt * BLK_TILE_BYTES, b_voff[i]);
+            const bool live = B_CHUNKS % THREADS == 0 || i * THREADS + wave_u * 64 < B_CHUNKS;
+            dma16(live ? lb + i * THREADS * 16 : lds_dummy, b_base + (size_t)kt * BLK_TILE_BYTES,
+                  b_voff[i]);
         } else {
             dma16_flat(wave_u * 64 < SC_CHUNKS ? ls : lds_dummy, sc_src + (size_t)kt * SC_GROUP);
         }
@@ -181,23 +193,29 @@ __global__ void __launch_bounds__(256, 1)
         v8i a[MPW], b[NPW];
         int sa, sb;
     };
+    // LDS operand reads. Each operand's byte offset goes through opaque_v(): with no common
+    // provable base the backend cannot fuse reads of different operands into ds_read2 forms,
+    // whose results it would then have to copy into each operand's 6-register tuple (each copy
+    // waiting on its read). A: one 24-byte (three 8-byte) read; B: 16 + 8 bytes.
+    const lds_cptr lds3 = (lds_cptr)lds;
     auto read_slab = [&](int st, int s, Slab& R) {
-        const char* base = lds + st * STAGE;
+        const uint32_t base = st * STAGE;
 #pragma unroll
         for (int mi = 0; mi < MPW; mi++) {
-            const v6i_a8 x = *reinterpret_cast<const v6i_a8*>(base + a_off + mi * 32 * KT_ROW_BYTES + s * 48);
+            const uint32_t o = opaque_v(base + a_off + mi * 32 * KT_ROW_BYTES + s * 48);
+            const v6i_a8 x = *reinterpret_cast<const __attribute__((address_space(3))) v6i_a8*>(lds3 + o);
             R.a[mi] = __builtin_shufflevector(x, x, 0, 1, 2, 3, 4, 5, -1, -1);
         }
 #pragma unroll
         for (int ni = 0; ni < NPW; ni++) {
-            const int o = ni * BLK_TILE_BYTES + s * OPBLK_BYTES;
-            const v4i y0 = *reinterpret_cast<const v4i*>(base + b_off + o);
-            const v2i y1 = *reinterpret_cast<const v2i*>(base + b_off2 + o);
+            const uint32_t o = opaque_v(base + b_off + ni * BLK_TILE_BYTES + s * OPBLK_BYTES);
+            const v4i y0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(lds3 + o);
+            const v2i y1 = *reinterpret_cast<const __attribute__((address_space(3))) v2i*>(lds3 + o + (1024 - 8 * lane));
             const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
             R.b[ni] = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
         }
-        R.sa = *reinterpret_cast<const int*>(base + sa_off + s * 4);
-        R.sb = *reinterpret_cast<const int*>(base + sb_off + s * 4);
+        R.sa = *reinterpret_cast<const __attribute__((address_space(3))) int*>(lds3 + base + sa_off + s * 4);
+        R.sb = *reinterpret_cast<const __attribute__((address_space(3))) int*>(lds3 + base + sb_off + s * 4);
     };
 
     v16f acc[MPW][NPW];
@@ -296,23 +314,27 @@ __global__ void __launch_bounds__(256, 1)
 
 // ---- instantiations and launch -------------------------------------------------------------------
 
+// (MT, NT, MPW, NPW) -> wave grid: the scale grouping fixes how many 32-blocks one wave holds,
+// so it also selects between the 4-wave and 8-wave instantiation of a tile.
 inline bool tile_supported(int MT, int NT, int mpw, int npw) {
     return (MT == 128 && NT == 128 && mpw == 2 && npw == 2) ||
            (MT == 128 && NT == 256 && mpw == 2 && npw == 4) ||
            (MT == 128 && NT == 384 && mpw == 4 && npw == 3) ||
-           (MT == 256 && NT == 256 && mpw == 4 && npw == 4);
+           (MT == 256 && NT == 256 && mpw == 4 && npw == 4) ||
+           (MT == 256 && NT == 256 && mpw == 2 && npw == 4);
 }
 
 template <int MT, int NT, int WM, int WN, int XG, typename OutT>
 int tile_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     const dim3 grid((unsigned)(d->M / MT), (unsigned)(d->N / NT), (unsigned)d->splits);
+    const dim3 block(64 * WM * WN);
     const uint8_t* A = static_cast<const uint8_t*>(d->A);
     const uint8_t* B = static_cast<const uint8_t*>(d->Bsh);
     if (d->splits > 1)
-        tile_kernel<MT, NT, WM, WN, XG, float, true><<<grid, dim3(256), 0, st>>>(
+        tile_kernel<MT, NT, WM, WN, XG, float, true><<<grid, block, 0, st>>>(
             A, B, d->sA, d->sB, nullptr, d->ws, d->M, d->N, d->Kp, d->A_row_bytes, d->splits);
     else
-        tile_kernel<MT, NT, WM, WN, XG, OutT, false><<<grid, dim3(256), 0, st>>>(
+        tile_kernel<MT, NT, WM, WN, XG, OutT, false><<<grid, block, 0, st>>>(
             A, B, d->sA, d->sB, static_cast<OutT*>(d->D), nullptr, d->M, d->N, d->Kp,
             d->A_row_bytes, 1);
     return 0;
@@ -324,6 +346,7 @@ int tile_launch(const mxfp6_launch_desc* d, hipStream_t st) {
     if (d->MT == 128 && d->NT == 128) return tile_launch_t<128, 128, 2, 2, 4, OutT>(d, st);
     if (d->MT == 128 && d->NT == 256) return tile_launch_t<128, 256, 2, 2, 4, OutT>(d, st);
     if (d->MT == 128 && d->NT == 384) return tile_launch_t<128, 384, 1, 4, 4, OutT>(d, st);
+    if (d->mpw == 2) return tile_launch_t<256, 256, 4, 2, 4, OutT>(d, st);
     return tile_launch_t<256, 256, 2, 2, 4, OutT>(d, st);
 }
 

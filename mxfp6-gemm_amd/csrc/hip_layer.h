@@ -31,12 +31,18 @@ typedef struct mxfp6_launch_desc {
     const uint8_t* sB;
     void* D;
     float* ws;         /* splits * M * N floats when splits > 1 */
+    void* Ash;         /* non-null: M * packed(Kp) bytes into which A is first repacked to the
+                          preshuffled operand layout (the kernel then reads that copy) */
     void* stream;      /* hipStream_t */
 } mxfp6_launch_desc;
 
 /* Returns 0 on success, 1 when no kernel instantiation matches the descriptor, 2 when the HIP
  * runtime reports a launch error. */
 int mxfp6_hip_launch(const mxfp6_launch_desc* d);
+
+/* Repacks rows (rows % 32 == 0) of a row-major packed operand, read for packed(Kp) bytes each,
+ * into the preshuffled operand layout at dst (rows * packed(Kp) bytes). 0 ok, 2 launch error. */
+int mxfp6_hip_repack(const void* src, int row_bytes, int rows, int Kp, void* dst, void* stream);
 
 /* Whether the tile kernel has an instantiation for MT x NT with scale grouping (mpw, npw). */
 int mxfp6_hip_has_tile(int MT, int NT, int mpw, int npw);

@@ -64,6 +64,36 @@ TileChoice route(int M, int N, int Kp) {
     return best;
 }
 
+// Whether A is first repacked into the preshuffled operand layout (an HBM-bound pass over A).
+// A row-major A costs the tile kernel's copies one 128-byte cache line per 48 useful bytes of a
+// row and slab; repacked, every copy is a contiguous 1 KiB. The pass pays when the kernel re-reads
+// each A row band many times, i.e. when the output has many tile columns.
+bool repack_for(const TileChoice& tc, int M, int N, int Kp) {
+    (void)M;
+    (void)Kp;
+    return N / tc.NT >= REPACK_MIN_TILE_COLS;
+}
+
+size_t split_bytes(int M, int N, int S) {
+    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+size_t repack_bytes(int M, int Kp) {
+    return (size_t)M * (size_t)(Kp / 4 * 3);
+}
+
+size_t plan_bytes(int M, int N, int Kp, int S, bool repack) {
+    const size_t sb = (split_bytes(M, N, S) + 255) / 256 * 256;
+    return sb + (repack ? repack_bytes(M, Kp) : 0);
+}
+
+bool route_repacks(int M, int N, int Kp) {
+    if (M <= 0 || N <= 0 || Kp <= 0) return false;
+    const TileChoice tc = route(M, N, Kp);
+    if (M % tc.MT != 0 || N % tc.NT != 0) return false;
+    return repack_for(tc, M, N, Kp);
+}
+
 int splitk_segments(int M, int N, int Kp) {
     if (M <= 0 || N <= 0 || Kp <= 0) return 1;
     const TileChoice tc = route(M, N, Kp);
@@ -73,7 +103,8 @@ int splitk_segments(int M, int N, int Kp) {
 
 size_t workspace_bytes(int M, int N, int Kp) {
     const int S = splitk_segments(M, N, Kp);
-    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+    const bool rp = route_repacks(M, N, Kp);
+    return (S > 1 || rp) ? plan_bytes(M, N, Kp, S, rp) : 0;
 }
 
 // ---- argument checks -----------------------------------------------------------------------
@@ -107,7 +138,9 @@ const char* status_text(int st) {
 
 // ---- launch ----------------------------------------------------------------------------------
 
-int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, int kernel,
+// ws: the workspace of the plan (S, repack): split partials first, then the repacked A at the
+// next 256-byte boundary.
+int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, bool repack, int kernel,
         const void* dA, const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
         int A_row_bytes, void* ws, void* stream) {
     mxfp6_launch_desc d;
@@ -127,7 +160,8 @@ int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, int ker
     d.sA = dsA;
     d.sB = dsB;
     d.D = dD;
-    d.ws = static_cast<float*>(ws);
+    d.ws = S > 1 ? static_cast<float*>(ws) : nullptr;
+    d.Ash = repack ? static_cast<uint8_t*>(ws) + (split_bytes(M, N, S) + 255) / 256 * 256 : nullptr;
     d.stream = stream;
     const int rc = mxfp6_hip_launch(&d);
     return rc == 0 ? MXFP6_OK : rc == 1 ? MXFP6_ERR_TILE : MXFP6_ERR_HIP;
@@ -145,19 +179,23 @@ int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void*
     if (st != MXFP6_OK) return st;
     const TileChoice tc = route(M, N, Kp);
     if (N % tc.NT != 0 || M % tc.MT != 0) return MXFP6_ERR_TILE;
-    int S = splitk_segments(M, N, Kp);
-    if (S > 1) {
-        const size_t need = (size_t)S * (size_t)M * (size_t)N * sizeof(float);
-        if (ws == nullptr || ws_bytes < need) {
-            std::fprintf(stderr,
-                         "[mxfp6] %dx%dx%d: split-K over %d segments needs a %zu-byte workspace, "
-                         "got %zu; running unsplit. Size it with gemm_workspace_size().\n",
-                         M, N, Kp, S, need, ws_bytes);
-            S = 1;
-        }
+    int S = split_for(tc, M, N, Kp);
+    bool rp = repack_for(tc, M, N, Kp);
+    const int kernel = kernel_for(tc);
+    if (kernel != MXFP6_KERNEL_TILE) rp = false;
+    if (ws == nullptr) ws_bytes = 0;
+    // A workspace too small for the repacked A drops the repack (a pure speed choice); one too
+    // small for the split-K partials as well runs unsplit, with the reference's warning.
+    if (rp && ws_bytes < plan_bytes(M, N, Kp, S, true)) rp = false;
+    if (S > 1 && ws_bytes < plan_bytes(M, N, Kp, S, false)) {
+        std::fprintf(stderr,
+                     "[mxfp6] %dx%dx%d: split-K over %d segments needs a %zu-byte workspace, "
+                     "got %zu; running unsplit. Size it with gemm_workspace_size().\n",
+                     M, N, Kp, S, split_bytes(M, N, S), ws_bytes);
+        S = 1;
     }
-    return run(out_type, M, N, Kp, tc, S, kernel_for(tc), dA, dBsh, dsA, dsB, dD, A_row_bytes,
-               S > 1 ? ws : nullptr, stream);
+    return run(out_type, M, N, Kp, tc, S, rp, kernel, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws,
+               stream);
 }
 
 bool tile_divides(const int tile[4], int M, int N) {
@@ -257,12 +295,12 @@ extern "C" int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const i
     if (!plan::tile_divides(tile, M, N)) return MXFP6_ERR_TILE;
     const TileChoice tc = {tile[0], tile[1], tile[2], tile[3]};
     if (!mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW)) return MXFP6_ERR_TILE;
-    return plan::run(out_type, M, N, Kp, tc, 1, MXFP6_KERNEL_TILE, dA, dBsh, dsA, dsB, dD,
+    return plan::run(out_type, M, N, Kp, tc, 1, false, MXFP6_KERNEL_TILE, dA, dBsh, dsA, dsB, dD,
                      A_row_bytes, nullptr, stream);
 }
 
 extern "C" int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int tile[4],
-                                   int splits, const void* dA, const void* dBsh,
+                                   int splits, int a_repack, const void* dA, const void* dBsh,
                                    const uint8_t* dsA, const uint8_t* dsB, void* dD,
                                    int A_row_bytes, void* ws, size_t ws_bytes, void* stream) {
     if (!tile) return MXFP6_ERR_NULL;
@@ -271,11 +309,12 @@ extern "C" int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int
     if (!plan::tile_divides(tile, M, N)) return MXFP6_ERR_TILE;
     const TileChoice tc = {tile[0], tile[1], tile[2], tile[3]};
     if (!mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW)) return MXFP6_ERR_TILE;
-    if (splits < 1 || splits > Kp / K_TILE) return MXFP6_ERR_ARG;
-    if (splits > 1 && (ws == nullptr || ws_bytes < (size_t)splits * M * N * sizeof(float)))
+    if (splits < 1 || splits > Kp / K_TILE || (a_repack != 0 && a_repack != 1)) return MXFP6_ERR_ARG;
+    if ((splits > 1 || a_repack) &&
+        (ws == nullptr || ws_bytes < plan::plan_bytes(M, N, Kp, splits, a_repack != 0)))
         return MXFP6_ERR_ARG;
-    return plan::run(out_type, M, N, Kp, tc, splits, MXFP6_KERNEL_TILE, dA, dBsh, dsA, dsB, dD,
-                     A_row_bytes, splits > 1 ? ws : nullptr, stream);
+    return plan::run(out_type, M, N, Kp, tc, splits, a_repack != 0, MXFP6_KERNEL_TILE, dA, dBsh,
+                     dsA, dsB, dD, A_row_bytes, ws, stream);
 }
 
 extern "C" int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, int npw,
@@ -290,6 +329,24 @@ extern "C" int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, in
     if (splits > 1 && (ws == nullptr || ws_bytes < (size_t)splits * M * N * sizeof(float)))
         return MXFP6_ERR_ARG;
     const TileChoice tc = {128, 128, mpw, npw};
-    return plan::run(out_type, M, N, Kp, tc, splits, MXFP6_KERNEL_DIRECT, dA, dBsh, dsA, dsB, dD,
-                     A_row_bytes, splits > 1 ? ws : nullptr, stream);
+    return plan::run(out_type, M, N, Kp, tc, splits, false, MXFP6_KERNEL_DIRECT, dA, dBsh, dsA,
+                     dsB, dD, A_row_bytes, splits > 1 ? ws : nullptr, stream);
+}
+
+extern "C" int mxfp6_gemm_repacks_a(int M, int N, int Kp) {
+    return plan::route_repacks(M, N, Kp) ? 1 : 0;
+}
+
+extern "C" size_t mxfp6_plan_workspace_size(int M, int N, int Kp, int splits, int a_repack) {
+    if (M <= 0 || N <= 0 || Kp <= 0 || splits < 1) return 0;
+    if (splits == 1 && !a_repack) return 0;
+    return plan::plan_bytes(M, N, Kp, splits, a_repack != 0);
+}
+
+extern "C" int mxfp6_preshuffle_rows_async(const void* src, int row_bytes, int rows, int Kp,
+                                           void* dst, void* stream) {
+    if (!src || !dst) return MXFP6_ERR_NULL;
+    if (rows <= 0 || rows % 32 != 0 || Kp <= 0 || Kp % K_TILE != 0) return MXFP6_ERR_SHAPE;
+    if (row_bytes <= 0 || row_bytes % 4 != 0 || row_bytes < Kp / 4 * 3 - 120) return MXFP6_ERR_SHAPE;
+    return mxfp6_hip_repack(src, row_bytes, rows, Kp, dst, stream) == 0 ? MXFP6_OK : MXFP6_ERR_HIP;
 }

@@ -12,10 +12,14 @@ namespace plan {
 constexpr int CUS = 256;
 // Shortest K segment of a split, in K-tiles of 192.
 constexpr int MIN_TILES_PER_SEG = 8;
+// Tile columns (N / NT) from which A is repacked to the preshuffled layout first.
+constexpr int REPACK_MIN_TILE_COLS = 8;
 
 TileChoice route(int M, int N, int Kp);
 int splitk_segments(int M, int N, int Kp);
 size_t workspace_bytes(int M, int N, int Kp);
+bool route_repacks(int M, int N, int Kp);
+size_t plan_bytes(int M, int N, int Kp, int S, bool repack);
 int check_common(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
                  const void* dsA, const void* dsB, const void* dD, int A_row_bytes);
 const char* status_text(int st);

@@ -47,8 +47,11 @@ SIGNATURES = {
     "mxfp6_gemm_force_tile": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
                                         _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp]),
     "mxfp6_gemm_explicit": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
-                                      C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, _vp, C.c_size_t,
-                                      _vp]),
+                                      C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, _vp,
+                                      C.c_size_t, _vp]),
+    "mxfp6_gemm_repacks_a": (C.c_int, [C.c_int, C.c_int, C.c_int]),
+    "mxfp6_plan_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "mxfp6_preshuffle_rows_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "mxfp6_gemm_direct": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp,
                                     _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp, C.c_size_t, _vp]),
     "mxfp6_fp6_e2m3_to_float": (C.c_float, [C.c_uint8]),
@@ -154,10 +157,24 @@ def gemm_force_tile(out_type, M, N, Kp, tile, dA, dBsh, dsA, dsB, dD, A_row_byte
 
 
 def gemm_explicit(out_type, M, N, Kp, tile, splits, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws=0,
-                  ws_bytes=0, stream=None):
+                  ws_bytes=0, stream=None, a_repack=0):
     t = (C.c_int * 4)(*tile)
-    return lib().mxfp6_gemm_explicit(out_type, M, N, Kp, t, splits, dA, dBsh, dsA, dsB, dD,
-                                     A_row_bytes, ws or None, ws_bytes, stream)
+    return lib().mxfp6_gemm_explicit(out_type, M, N, Kp, t, splits, a_repack, dA, dBsh, dsA, dsB,
+                                     dD, A_row_bytes, ws or None, ws_bytes, stream)
+
+
+def repacks_a(M, N, Kp):
+    """Whether gemm() repacks A into the preshuffled layout for this shape."""
+    return bool(lib().mxfp6_gemm_repacks_a(M, N, Kp))
+
+
+def plan_workspace_size(M, N, Kp, splits, a_repack):
+    return lib().mxfp6_plan_workspace_size(M, N, Kp, splits, int(a_repack))
+
+
+def preshuffle_rows(src, row_bytes, rows, Kp, dst, stream=None):
+    """On-device preshuffle of row-major packed rows (device pointers), preshuffle_B's layout."""
+    return lib().mxfp6_preshuffle_rows_async(src, row_bytes, rows, Kp, dst, stream)
 
 
 def gemm_direct(out_type, M, N, Kp, mpw, npw, dA, dBsh, dsA, dsB, dD, A_row_bytes, splits=1,

@@ -83,3 +83,19 @@ def run_direct(dp: DevProblem, out_type, splits=1):
     assert rc == 0, mx.STATUS.get(rc, rc)
     torch.cuda.synchronize()
     return to_f32(D, out_type, p.M, p.N)
+
+
+def run_explicit(dp: DevProblem, out_type, splits=1, a_repack=0):
+    p = dp.p
+    ws_bytes = mx.plan_workspace_size(p.M, p.N, p.Kp, splits, a_repack)
+    ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device="cuda")
+    D = dp.out(out_type)
+    a, b, sa, sb = dp.ptrs()
+    say(f"  explicit {dp.tile} {p.M}x{p.N}x{p.K} out {mx.OUT_NAMES[out_type]} S {splits} "
+        f"repack {a_repack}")
+    rc = mx.gemm_explicit(out_type, p.M, p.N, p.Kp, dp.tile, splits, a, b, sa, sb, D.data_ptr(),
+                          p.a_row_bytes, ws.data_ptr() if ws_bytes else 0, ws_bytes,
+                          a_repack=a_repack)
+    assert rc == 0, mx.STATUS.get(rc, rc)
+    torch.cuda.synchronize()
+    return to_f32(D, out_type, p.M, p.N)

@@ -68,8 +68,13 @@ def test_workspace_matches_split(mx):
             for K in (1024, 4096, 16128, 105728):
                 Kp = _kpad(K)
                 S = mx.splitk_segments(M, N, Kp)
+                rp = mx.repacks_a(M, N, Kp)
                 ws = mx.workspace_size(M, N, Kp)
-                assert (ws == 0) if S == 1 else (ws == S * M * N * 4), (M, N, K, S, ws)
+                # split partials first, then the repacked A at the next 256-byte boundary
+                split = S * M * N * 4 if S > 1 else 0
+                want = (split + 255) // 256 * 256 + (M * Kp // 4 * 3 if rp else 0)
+                assert ws == want, (M, N, K, S, rp, ws)
+                assert mx.plan_workspace_size(M, N, Kp, S, rp) == want
                 if S > 1:
                     t = mx.choose_tile(M, N, Kp)
                     base = (M // t[0]) * (N // t[1])

@@ -47,7 +47,7 @@ def test_routed_small_shapes(g, orc, out_type, M, N, K):
 
 
 @pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
-                                  (256, 256, 4, 4)])
+                                  (256, 256, 4, 4), (256, 256, 2, 4)])
 @pytest.mark.parametrize("out_type", [0, 1, 2])
 def test_forced_tiles(g, orc, tile, out_type):
     M, N, K = 256, 768, 960  # K-tail: kpad(960) = 1152
@@ -58,7 +58,7 @@ def test_forced_tiles(g, orc, tile, out_type):
 
 
 @pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
-                                  (256, 256, 4, 4)])
+                                  (256, 256, 4, 4), (256, 256, 2, 4)])
 def test_pipelined_kernel_bitwise_equals_direct(g, tile):
     """Both kernels add the same MFMA results in the same K order, so FP32 outputs are equal
     bit for bit (covers every wave block, slab and stage of the pipelined kernel)."""
@@ -80,6 +80,59 @@ def test_pipelined_split_bitwise_equals_direct_split(g):
     Dr = g.run_routed(dp, mx.OUT_F32)
     Dd = g.run_direct(dp, mx.OUT_F32, splits=S)
     assert np.array_equal(Dr.view(np.uint32), Dd.view(np.uint32))
+
+
+# ---- A repacked into the preshuffled layout ------------------------------------------------------
+
+@pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
+                                  (256, 256, 4, 4), (256, 256, 2, 4)])
+def test_repacked_a_bitwise_equals_direct(g, tile):
+    """The kernel reading the repacked A multiplies the same operands in the same order."""
+    M, N, K = 512, 768, 2112
+    p = mx.make_problem(M, N, K, seed=72)
+    dp = g.DevProblem(p, tile)
+    Dr = g.run_explicit(dp, mx.OUT_F32, a_repack=1)
+    Dd = g.run_direct(dp, mx.OUT_F32)
+    assert np.array_equal(Dr.view(np.uint32), Dd.view(np.uint32))
+
+
+def test_repacked_a_split_bitwise_equals_direct_split(g):
+    M, N, K = 512, 512, 3072
+    p = mx.make_problem(M, N, K, seed=82)
+    dp = g.DevProblem(p, (128, 128, 2, 2))
+    Dr = g.run_explicit(dp, mx.OUT_F32, splits=3, a_repack=1)
+    Dd = g.run_direct(dp, mx.OUT_F32, splits=3)
+    assert np.array_equal(Dr.view(np.uint32), Dd.view(np.uint32))
+
+
+@pytest.mark.parametrize("compact", [True, False])
+def test_device_preshuffle_matches_host_preshuffle(g, orc, compact):
+    """The on-device row preshuffle (the A repack) gives the host preshuffle_B's bytes, for
+    compact rows (over-read into the next row / end pad, as the kernels read them) and padded."""
+    import torch
+    M, K = 256, 960
+    p = mx.make_problem(M, 128, K, seed=5, compact=compact)
+    src = torch.from_numpy(p.a_packed).cuda()
+    dst = torch.full((M * p.Kp // 4 * 3,), 0x5A, dtype=torch.uint8, device="cuda")
+    rc = mx.preshuffle_rows(src.data_ptr(), p.a_row_bytes, M, p.Kp, dst.data_ptr())
+    assert rc == 0, mx.STATUS.get(rc, rc)
+    torch.cuda.synchronize()
+    host = orc.preshuffle_b(p.a_packed, M, p.Kp, p.a_row_bytes)
+    assert np.array_equal(dst.cpu().numpy(), host)
+
+
+def test_routed_repack_and_fallback(g, orc):
+    """A shape the router repacks A for: full workspace (repack) and none (row-major A) give
+    the same bits and pass the oracle."""
+    M, N, K = 256, 2048, 1024
+    p = mx.make_problem(M, N, K, seed=23)
+    assert mx.repacks_a(M, N, p.Kp)
+    dp = g.DevProblem(p, mx.choose_tile(M, N, p.Kp))
+    R, ab = _oracle(orc, p)
+    D1 = g.run_routed(dp, mx.OUT_F32, with_ws=True)
+    D0 = g.run_routed(dp, mx.OUT_F32, with_ws=False)
+    checks.check_f32(D1, R, ab)
+    assert np.array_equal(D1.view(np.uint32), D0.view(np.uint32))
 
 
 # ---- the direct kernel (independent implementation) ------------------------------------------
