@@ -1,18 +1,33 @@
 """Benchmark of libmxfp6gemm on one MI355X: MXFP6 GEMM TFLOPs and fraction of the dense MXFP6
 MFMA peak.
 
-A step is one mxfp6_gemm_async call (the whole hot path: tile kernel, plus the split-K reduce when
-the shape splits) over operands already resident in HBM. Default workload: M = N = K = 8192, FP16
-out, A and B drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX rule.
+A step is one mxfp6_gemm_async call: the whole hot path the router picks for the shape (for the
+default workload: the repack of A into the preshuffled layout, then the 256x256 tile kernel),
+over operands already resident in HBM. Default workload: M = N = K = 8192, FP16 out, A and B
+drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX rule.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--all] [--no-cpu]
 
-Prints one JSON line per workload (only the default one unless --all).
+Prints one JSON line per workload (only the default one unless --all). Besides the contract
+fields it reports:
+  roofline      the dominant kernel (the tile kernel) against the dense MXFP6 MFMA peak: its
+                algorithmic flops per launch / its average launch duration, timed live with HIP
+                events on the launch stream in a second loop of K steps that issues the step's
+                two launches separately (repack, then the tile kernel on the repacked A);
+                traffic = HBM bytes per launch from the committed rocprofv3 counter summary of
+                the same kernel and workload (FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel
+                calibration), null when no summary matches;
+  sclk_mhz      the graphics clock sampled (amd-smi) while the step loop runs, and frac_at_sclk,
+                the tile kernel's rate against the peak at that clock (4,194,304 flop/clk);
+  cpu_baseline  the reference CPU GEMM's arithmetic on this host (a bounded sample, scaled).
 """
 import argparse
 import json
 import os
+import re
+import subprocess
 import sys
+import threading
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -26,6 +41,8 @@ SEED = 0x4D584636
 # MI355X published dense MXFP6 / MXFP4 MFMA peak (TFLOP/s) and HBM bandwidth (GB/s)
 PEAK_TFLOPS = 10100.0
 PEAK_HBM_GBS = 8000.0
+# dense FP6 MFMA flops per clock of the whole chip: 256 CUs x 4 SIMDs x 4096
+FLOP_PER_CLK = 4194304.0
 
 # name -> (M, N, K, out_type, (dist_a, sigma_a), (dist_b, sigma_b), description)
 CONFIGS = {
@@ -40,6 +57,7 @@ CONFIGS = {
     "c5": (2048, 5120, 105728, mx.OUT_BF16, (mx.DIST_STUDENT_T3, 1.0),
            (mx.DIST_STUDENT_T3, 1.0), "A,B ~ Student-t(3)"),
 }
+PROFILES = os.path.join(ROOT, "profiles")
 
 
 def log(msg):
@@ -49,6 +67,59 @@ def log(msg):
 def alg_bytes(M, N, K, out_type):
     """Algorithmic HBM bytes of one GEMM: packed A and B, one scale byte per 32 elements, D."""
     return (M + N) * K * 3 // 4 + (M + N) * K // 32 + M * N * mx.OUT_BYTES[out_type]
+
+
+def workload_name(M, N, K, out_type):
+    return f"mxfp6_gemm_{M}x{N}x{K}_{mx.OUT_NAMES[out_type]}"
+
+
+def profiled_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` on `workload` from profiles/*_pmc.txt (lines
+    'workload: ...', 'kernel: ...', 'hbm_bytes_per_launch: N'), or None."""
+    if not os.path.isdir(PROFILES):
+        return None
+    for fn in sorted(os.listdir(PROFILES)):
+        if not fn.endswith("_pmc.txt"):
+            continue
+        with open(os.path.join(PROFILES, fn)) as f:
+            txt = f.read()
+        w = re.search(r"^workload:\s*(\S+)", txt, re.M)
+        k = re.search(r"^kernel:\s*(.+)$", txt, re.M)
+        b = re.search(r"^hbm_bytes_per_launch:\s*([0-9.eE+]+)", txt, re.M)
+        if w and k and b and w.group(1) == workload and k.group(1).strip() == kernel:
+            return float(b.group(1))
+    return None
+
+
+class ClockSampler:
+    """Samples the graphics clock (amd-smi metric -c, a child process) while work runs."""
+
+    def __init__(self):
+        self.mhz = []
+        self._stop = threading.Event()
+        self._th = threading.Thread(target=self._run, daemon=True)
+
+    def _run(self):
+        time.sleep(0.3)
+        while not self._stop.is_set():
+            try:
+                o = subprocess.run(["amd-smi", "metric", "-c"], capture_output=True, text=True,
+                                   timeout=10).stdout
+            except (OSError, subprocess.SubprocessError):
+                return
+            self.mhz.extend(int(x) for x in re.findall(r"GFX_\d+:\s+CLK:\s+(\d+) MHz", o))
+            self._stop.wait(0.5)
+
+    def __enter__(self):
+        self._th.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._th.join(timeout=15)
+
+    def mean(self):
+        return sum(self.mhz) / len(self.mhz) if self.mhz else None
 
 
 def cpu_baseline(p, target_cpu_s=12.0):
@@ -82,7 +153,20 @@ def cpu_baseline(p, target_cpu_s=12.0):
                       f"scaled x{p.M / nrows:.1f}: {full:.1f} s per GEMM"}
 
 
-def run_config(name, steps, warmup, with_cpu):
+def copy_calibration(mib=256, reps=5):
+    """A plain device copy of known size (torch's copy kernel), for scaling the FETCH_SIZE and
+    WRITE_SIZE counters: each launch reads and writes exactly `mib` MiB."""
+    import torch
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] copy calibration: {reps} copies of {mib} MiB")
+
+
+def run_config(name, steps, warmup, with_cpu, with_clock=True):
     import torch
 
     M, N, K, out_type, (da, sa_), (db, sb_), desc = CONFIGS[name]
@@ -91,6 +175,7 @@ def run_config(name, steps, warmup, with_cpu):
     p = mx.make_problem(M, N, K, da, sa_, db, sb_, seed=SEED ^ cfg_idx)
     tile = mx.choose_tile(M, N, p.Kp)
     S = mx.splitk_segments(M, N, p.Kp)
+    repack = mx.repacks_a(M, N, p.Kp)
     bsh, sa, sb = p.layouts(tile)
     dev = torch.device("cuda:0")
     dA = torch.from_numpy(p.a_packed).to(dev)
@@ -100,20 +185,23 @@ def run_config(name, steps, warmup, with_cpu):
     D = torch.empty(M * N * mx.OUT_BYTES[out_type], dtype=torch.uint8, device=dev)
     ws_bytes = mx.workspace_size(M, N, p.Kp)
     ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
-    log(f"[bench] {name}: {M}x{N}x{K} (Kp {p.Kp}) tile {tile} S {S} ws {ws_bytes} B; "
-        f"inputs ready in {time.perf_counter() - t0:.1f} s")
+    log(f"[bench] {name}: {M}x{N}x{K} (Kp {p.Kp}) tile {tile} S {S} repack A {repack} "
+        f"ws {ws_bytes} B; inputs ready in {time.perf_counter() - t0:.1f} s")
     stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
     args = (out_type, M, N, p.Kp, dA.data_ptr(), dB.data_ptr(), dsa.data_ptr(), dsb.data_ptr(),
             D.data_ptr(), p.a_row_bytes, ws.data_ptr() if ws_bytes else 0, ws_bytes)
 
     def step():
-        rc = mx.gemm(*args, stream=stream.cuda_stream)
+        rc = mx.gemm(*args, stream=sp)
         if rc != 0:
             raise RuntimeError(f"mxfp6_gemm failed: {mx.STATUS.get(rc, rc)}")
 
+    flops = 2.0 * M * N * K
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    # timed region: exactly `steps` steps between two synchronisations
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     w0 = time.perf_counter()
     ev0.record(stream)
@@ -123,20 +211,60 @@ def run_config(name, steps, warmup, with_cpu):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - w0) * 1e3
     ms = ev0.elapsed_time(ev1) / steps
-    flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
-    # best of 4 reps of 20 back-to-back launches (the reference's own methodology)
-    best = ms
-    for _ in range(4):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(20):
-            step()
-        e1.record(stream)
+
+    # dominant kernel: the same launches issued one by one, HIP events around the tile kernel
+    kernel_name = "slab_kernel"
+    if S == 1 and repack:
+        ash = torch.empty(M * p.Kp // 4 * 3, dtype=torch.uint8, device=dev)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(steps)]
+
+        def split_step(i):
+            # what gemm() does for this plan, launch by launch: repack A, then the tile kernel
+            # reading the repacked copy (A layout 2)
+            if mx.preshuffle_rows(dA.data_ptr(), p.a_row_bytes, M, p.Kp, ash.data_ptr(), sp):
+                raise RuntimeError("repack failed")
+            if i >= 0:
+                evs[i][0].record(stream)
+            rc = mx.gemm_explicit(out_type, M, N, p.Kp, tile, 1, ash.data_ptr(), dB.data_ptr(),
+                                  dsa.data_ptr(), dsb.data_ptr(), D.data_ptr(), p.a_row_bytes,
+                                  stream=sp, a_layout=mx.A_PRESHUFFLED)
+            if rc != 0:
+                raise RuntimeError(f"mxfp6_gemm_explicit failed: {mx.STATUS.get(rc, rc)}")
+            if i >= 0:
+                evs[i][1].record(stream)
+
+        for _ in range(max(2, warmup // 2)):
+            split_step(-1)
         torch.cuda.synchronize()
-        best = min(best, e0.elapsed_time(e1) / 20)
+        for i in range(steps):
+            split_step(i)
+        torch.cuda.synchronize()
+        k_ms = sum(a.elapsed_time(b) for a, b in evs) / steps
+        kernel_scope = "tile kernel alone (repack of A timed outside)"
+    else:
+        k_ms = ms
+        kernel_scope = "whole step (" + ("tile kernel + split-K reduce" if S > 1 else
+                                         "tile kernel") + ")"
+    k_tflops = flops / (k_ms * 1e-3) / 1e12
+
+    # clock while the step loop runs
+    sclk = None
+    if with_clock:
+        with ClockSampler() as clk:
+            t_end = time.time() + 2.0
+            while time.time() < t_end:
+                for _ in range(10):
+                    step()
+                torch.cuda.synchronize()
+        sclk = clk.mean()
+
     log(f"[bench] {name}: {ms * 1e3:.1f} us/step over {steps} steps ({tflops:.1f} TFLOP/s), "
-        f"best-of-reps {best * 1e3:.1f} us, wall {wall_ms:.1f} ms")
+        f"tile kernel {k_ms * 1e3:.1f} us ({k_tflops:.1f} TFLOP/s), wall {wall_ms:.1f} ms, "
+        f"sclk {sclk if sclk is None else round(sclk)} MHz")
+    workload = workload_name(M, N, K, out_type)
+    traffic = profiled_traffic(workload, kernel_name)
     out = {
         "metric": "MXFP6 GEMM TFLOPs (FP16 out) and % of MXFP6 MFMA peak, 1xMI355X",
         "value": round(tflops, 2),
@@ -150,15 +278,18 @@ def run_config(name, steps, warmup, with_cpu):
         "vs_baseline": None,
         "dtype": "mxfp6_e2m3 (fp32 accumulate)",
         "data": "synthetic",
-        "config": {"workload": f"mxfp6_gemm_{M}x{N}x{K}_{mx.OUT_NAMES[out_type]}", "M": M, "N": N,
-                   "K": K, "Kp": p.Kp, "out": mx.OUT_NAMES[out_type], "inputs": desc,
-                   "tile": list(tile), "splitk": S, "a_layout": "compact",
+        "config": {"workload": workload, "M": M, "N": N, "K": K, "Kp": p.Kp,
+                   "out": mx.OUT_NAMES[out_type], "inputs": desc, "tile": list(tile),
+                   "splitk": S, "a_repacked": repack, "a_layout": "compact row-major",
                    "parallelism": "single GPU"},
         "pct_of_peak": round(100.0 * tflops / PEAK_TFLOPS, 2),
-        "best_rep_tflops": round(flops / (best * 1e-3) / 1e12, 2),
         "hbm_gbs_alg": round(alg_bytes(M, N, K, out_type) / (ms * 1e-3) / 1e9, 1),
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_TFLOPS, 4), "traffic": None},
+        "roofline": {"bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(k_tflops / PEAK_TFLOPS, 4),
+                     "traffic": traffic, "kernel": kernel_name, "scope": kernel_scope,
+                     "kernel_ms": round(k_ms, 6)},
+        "sclk_mhz": None if sclk is None else round(sclk),
+        "frac_at_sclk": None if sclk is None else round(k_tflops * 1e12 / (FLOP_PER_CLK * sclk * 1e6), 4),
     }
     if with_cpu:
         log(f"[bench] {name}: CPU baseline ...")
@@ -174,15 +305,22 @@ def main():
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--all", action="store_true", help="every workload, one JSON line each")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-clock", action="store_true", help="skip the clock sampling (profiling)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run the 256 MiB copy kernel that calibrates the HBM byte counters")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on exactly one GPU; --gpus {a.gpus} is not supported (the MXFP6 "
               "GEMM here is a single-GPU library; multi-GPU sharding is design-only).",
               file=sys.stderr)
         sys.exit(2)
+    if a.copy_calibration:
+        copy_calibration()
+        return
     names = sorted(CONFIGS) if a.all else [a.config]
     for n in names:
-        print(json.dumps(run_config(n, a.steps, a.warmup, not a.no_cpu)), flush=True)
+        print(json.dumps(run_config(n, a.steps, a.warmup, not a.no_cpu, not a.no_clock)),
+              flush=True)
 
 
 if __name__ == "__main__":

@@ -73,13 +73,15 @@ int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4],
                           int A_row_bytes, int B_row_bytes, void* stream);
 
 /* Run an explicit plan: the pipelined kernel with tile {MT, NT, MPW, NPW}, `splits` K segments and
- * a_repack (1: A is first repacked into the preshuffled layout). Needs ws of
- * mxfp6_plan_workspace_size(M, N, Kp, splits, a_repack) bytes. For tuning and benchmarks of
- * alternative plans; the scales must be tiled with this tile's MPW/NPW. No counterpart in the
- * reference (it is the reference's gemm_force_tile, src/gemm.cpp:89-107, plus a split count and
- * the repack switch). */
+ * an A layout: 0 = row-major A (A_row_bytes per row); 1 = repack row-major A into the workspace in
+ * the preshuffled operand layout first, then read that; 2 = dA already holds A in the preshuffled
+ * layout (mxfp6_preshuffle_rows_async output; A_row_bytes is then only checked). Needs ws of
+ * mxfp6_plan_workspace_size(M, N, Kp, splits, a_layout == 1) bytes. For tuning, benchmarks and
+ * callers that keep A preshuffled; the scales must be tiled with this tile's MPW/NPW. No
+ * counterpart in the reference (it is the reference's gemm_force_tile, src/gemm.cpp:89-107, plus a
+ * split count and the A layout). */
 int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int tile[4], int splits,
-                        int a_repack, const void* dA, const void* dBsh, const uint8_t* dsA,
+                        int a_layout, const void* dA, const void* dBsh, const uint8_t* dsA,
                         const uint8_t* dsB, void* dD, int A_row_bytes, void* ws, size_t ws_bytes,
                         void* stream);
 

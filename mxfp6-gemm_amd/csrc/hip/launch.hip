@@ -75,10 +75,8 @@ extern "C" int mxfp6_hip_launch(const mxfp6_launch_desc* d) {
 
 extern "C" int mxfp6_hip_repack(const void* src, int row_bytes, int rows, int Kp, void* dst,
                                 void* stream) {
-    const int k64n = Kp / 64;
-    repack_rows_kernel<<<dim3((unsigned)((k64n + REPACK_KK - 1) / REPACK_KK), (unsigned)(rows / 32)),
-                         dim3(REPACK_THREADS), 0, static_cast<hipStream_t>(stream)>>>(
-        static_cast<const uint8_t*>(src), row_bytes, k64n, static_cast<uint8_t*>(dst));
+    repack_rows_launch(static_cast<const uint8_t*>(src), row_bytes, rows, Kp / 64,
+                       static_cast<uint8_t*>(dst), static_cast<hipStream_t>(stream));
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

@@ -9,44 +9,78 @@
 // 1024 + 8t. This is the layout preshuffle_B gives B^T, so a repacked A is read by the same
 // contiguous copies and linear LDS reads as B.
 //
-// HBM-bound: each workgroup writes KK consecutive tiles of one row block (a contiguous run) and
-// reads the matching contiguous 48*KK-byte span of each of its 32 rows. Loads are 4-byte (rows
-// are only 4-byte aligned), stores are 16-byte.
+// HBM-bound transpose through LDS: a workgroup takes one 32-row block and REPACK_KK consecutive
+// slabs. It reads the block's 32 row segments of 48 * REPACK_KK bytes with coalesced loads (VEC
+// bytes per lane, consecutive lanes on consecutive bytes of a row; VEC = 16, 8 or 4 by the row
+// alignment) into LDS, then writes the REPACK_KK output tiles, one contiguous run, with 16-byte
+// stores whose pieces it gathers from LDS.
 #pragma once
 #include "device_common.hpp"
 
 namespace mxfp6_dev {
 
-constexpr int REPACK_KK = 12;       // K slabs per workgroup
+constexpr int REPACK_KK = 16;          // K slabs per workgroup
 constexpr int REPACK_THREADS = 256;
+constexpr int REPACK_SEG = 48 * REPACK_KK;  // bytes of one row segment (768)
 
+template <int VEC>
 __global__ void __launch_bounds__(REPACK_THREADS)
     repack_rows_kernel(const uint8_t* __restrict__ src, int row_bytes, int k64n,
                        uint8_t* __restrict__ dst) {
+    __shared__ __attribute__((aligned(16))) uint8_t seg[32 * REPACK_SEG];
     const int mb = blockIdx.y;
     const int kk0 = blockIdx.x * REPACK_KK;
     const int nkk = min(REPACK_KK, k64n - kk0);
-    const int chunks = nkk * 96;  // 16-byte output chunks of this workgroup
-    const uint8_t* rows0 = src + (size_t)mb * 32 * row_bytes;
-    uint8_t* out = dst + ((size_t)mb * k64n + kk0) * OPBLK_BYTES;
-    for (int c = threadIdx.x; c < chunks; c += REPACK_THREADS) {
-        const int j = c / 96, u = c - j * 96;
-        const int kbyte = (kk0 + j) * SLAB_BYTES;
-        uint32_t w[4];
-        if (u < 64) {
-            // lane u's first 16 bytes
-            const int i = u & 31, h = u >> 5;
-            const uint32_t* s = reinterpret_cast<const uint32_t*>(rows0 + (size_t)i * row_bytes + kbyte + 24 * h);
-            w[0] = s[0], w[1] = s[1], w[2] = s[2], w[3] = s[3];
-        } else {
-            // the last 8 bytes of lanes 2p and 2p+1 (same K-half, rows i and i+1)
-            const int t = 2 * (u - 64), i = t & 31, h = t >> 5;
-            const uint32_t* s0 = reinterpret_cast<const uint32_t*>(rows0 + (size_t)i * row_bytes + kbyte + 24 * h + 16);
-            const uint32_t* s1 = reinterpret_cast<const uint32_t*>(rows0 + (size_t)(i + 1) * row_bytes + kbyte + 24 * h + 16);
-            w[0] = s0[0], w[1] = s0[1], w[2] = s1[0], w[3] = s1[1];
-        }
-        *reinterpret_cast<v4i*>(out + (size_t)c * 16) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    const int seg_bytes = nkk * SLAB_BYTES;
+    const uint8_t* rows0 = src + (size_t)mb * 32 * row_bytes + (size_t)kk0 * SLAB_BYTES;
+
+    // phase 1: 32 row segments -> LDS (row-major, REPACK_SEG bytes per row)
+    const int per_row = seg_bytes / VEC;
+    for (int c = threadIdx.x; c < 32 * per_row; c += REPACK_THREADS) {
+        const int i = c / per_row, o = (c - i * per_row) * VEC;
+        const uint8_t* s = rows0 + (size_t)i * row_bytes + o;
+        uint8_t* d = seg + i * REPACK_SEG + o;
+        if constexpr (VEC == 16)
+            *reinterpret_cast<v4i*>(d) = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(s));
+        else if constexpr (VEC == 8)
+            *reinterpret_cast<v2i*>(d) = __builtin_nontemporal_load(reinterpret_cast<const v2i*>(s));
+        else
+            *reinterpret_cast<int*>(d) = __builtin_nontemporal_load(reinterpret_cast<const int*>(s));
     }
+    __syncthreads();
+
+    // phase 2: output chunk c (16 bytes) of tile j: lanes u < 64 take their first 16 bytes,
+    // chunks 64..95 the last 8 bytes of lanes 2p and 2p+1
+    uint8_t* out = dst + ((size_t)mb * k64n + kk0) * OPBLK_BYTES;
+    for (int c = threadIdx.x; c < nkk * 96; c += REPACK_THREADS) {
+        const int j = c / 96, u = c - j * 96;
+        v2i lo, hi;
+        if (u < 64) {
+            const uint8_t* s = seg + (u & 31) * REPACK_SEG + j * SLAB_BYTES + 24 * (u >> 5);
+            lo = *reinterpret_cast<const v2i*>(s);
+            hi = *reinterpret_cast<const v2i*>(s + 8);
+        } else {
+            const int t = 2 * (u - 64), i = t & 31, h = t >> 5;
+            const uint8_t* s = seg + i * REPACK_SEG + j * SLAB_BYTES + 24 * h + 16;
+            lo = *reinterpret_cast<const v2i*>(s);
+            hi = *reinterpret_cast<const v2i*>(s + REPACK_SEG);
+        }
+        // streaming store: the copy is read once by the next kernel, keep it out of L2
+        __builtin_nontemporal_store(v4i{lo.x, lo.y, hi.x, hi.y}, reinterpret_cast<v4i*>(out + (size_t)c * 16));
+    }
+}
+
+// Launch: the widest load the source rows' alignment allows.
+inline void repack_rows_launch(const uint8_t* src, int row_bytes, int rows, int k64n,
+                               uint8_t* dst, hipStream_t st) {
+    const dim3 grid((unsigned)((k64n + REPACK_KK - 1) / REPACK_KK), (unsigned)(rows / 32));
+    const uintptr_t align = reinterpret_cast<uintptr_t>(src) | (uintptr_t)row_bytes;
+    if (align % 16 == 0)
+        repack_rows_kernel<16><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, k64n, dst);
+    else if (align % 8 == 0)
+        repack_rows_kernel<8><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, k64n, dst);
+    else
+        repack_rows_kernel<4><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, k64n, dst);
 }
 
 }  // namespace mxfp6_dev

@@ -293,8 +293,8 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
                     const size_t idx = (size_t)(m_w + mi * 32 + 8 * g + r) * N + n_w + ni * 32;
                     if (SPLIT)
                         ws[(size_t)blockIdx.z * M * N + idx] = acc[mi][ni][4 * g + r];
-                    else
-                        D[idx] = cvt_out<OutT>(acc[mi][ni][4 * g + r]);
+                    else  // D is not read again here: a streaming store keeps L2 for operands
+                        store_out_nt(D + idx, acc[mi][ni][4 * g + r]);
                 }
 }
 
@@ -319,14 +319,13 @@ void slab_launch_a(const mxfp6_launch_desc* d, const uint8_t* A, hipStream_t st)
 template <int MT, int NT, int WM, int WN, int XG, int NS, typename OutT>
 int slab_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     static_assert(SlabGeom<MT, NT, WM, WN, NS>::LDS <= 160 * 1024, "LDS budget");
-    if (d->Ash != nullptr) {
+    if (d->a_layout == MXFP6_A_REPACK) {
         // repack A into the preshuffled layout, then run the kernel on it
-        const int k64n = d->Kp / 64;
-        repack_rows_kernel<<<dim3((unsigned)((k64n + REPACK_KK - 1) / REPACK_KK), (unsigned)(d->M / 32)),
-                             dim3(REPACK_THREADS), 0, st>>>(static_cast<const uint8_t*>(d->A),
-                                                            d->A_row_bytes, k64n,
-                                                            static_cast<uint8_t*>(d->Ash));
+        repack_rows_launch(static_cast<const uint8_t*>(d->A), d->A_row_bytes, d->M, d->Kp / 64,
+                           static_cast<uint8_t*>(d->Ash), st);
         slab_launch_a<MT, NT, WM, WN, XG, NS, OutT, true>(d, static_cast<const uint8_t*>(d->Ash), st);
+    } else if (d->a_layout == MXFP6_A_PRESHUFFLED) {
+        slab_launch_a<MT, NT, WM, WN, XG, NS, OutT, true>(d, static_cast<const uint8_t*>(d->A), st);
     } else {
         slab_launch_a<MT, NT, WM, WN, XG, NS, OutT, false>(d, static_cast<const uint8_t*>(d->A), st);
     }

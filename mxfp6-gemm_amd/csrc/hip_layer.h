@@ -11,6 +11,9 @@
 extern "C" {
 #endif
 
+/* How the tile kernel finds A. */
+enum mxfp6_a_layout { MXFP6_A_ROWS = 0, MXFP6_A_REPACK = 1, MXFP6_A_PRESHUFFLED = 2 };
+
 /* Kernel families of the HIP layer. */
 enum mxfp6_kernel_id {
     MXFP6_KERNEL_DIRECT = 0, /* one wave per 32x32 block, operands straight from global memory */
@@ -31,8 +34,10 @@ typedef struct mxfp6_launch_desc {
     const uint8_t* sB;
     void* D;
     float* ws;         /* splits * M * N floats when splits > 1 */
-    void* Ash;         /* non-null: M * packed(Kp) bytes into which A is first repacked to the
-                          preshuffled operand layout (the kernel then reads that copy) */
+    int a_layout;      /* MXFP6_A_ROWS: A row-major (A_row_bytes per row);
+                          MXFP6_A_REPACK: repack A into Ash first, the kernel reads Ash;
+                          MXFP6_A_PRESHUFFLED: A is already in the preshuffled operand layout */
+    void* Ash;         /* MXFP6_A_REPACK: M * packed(Kp) bytes */
     void* stream;      /* hipStream_t */
 } mxfp6_launch_desc;
 

@@ -20,10 +20,14 @@ namespace plan {
 //   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3   (3 units)
 //   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4   (2 units)
 //   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (1 unit)
-// A candidate must divide the shape. Workgroup-starved grids are split along K (split_for). The
-// cost of a candidate is the number of CU waves its (split) grid needs times the work of one
-// workgroup: ceil(wg * S / CUS) * units / S. The cheapest wins; ties go to the larger tile, which
-// moves fewer operand bytes per flop (A is re-read N/NT times, B M/MT times).
+// The kernel is bound by the per-CU global->LDS copy rate (64 B/clk per CU on MI355X), so the
+// tile that moves the fewest operand bytes per flop, 256x256, is preferred whenever it divides
+// the shape and its (split) grid has at least BIG_TILE_MIN_WG workgroups: measured on MI355X it
+// beats a smaller tile that fills every CU (a 256x256 workgroup does 4/3 to 4x the work per
+// copied byte). Otherwise a candidate must divide the shape, workgroup-starved grids are split
+// along K (split_for), and the cost of a candidate is the number of CU waves its (split) grid
+// needs times the work of one workgroup: ceil(wg * S / CUS) * units / S. The cheapest wins; ties
+// go to the larger tile.
 namespace {
 struct Cand {
     TileChoice tc;
@@ -51,6 +55,10 @@ TileChoice route(int M, int N, int Kp) {
     TileChoice best = {128, 128, 2, 2};
     double best_cost = -1;
     if (M <= 0 || N <= 0 || Kp <= 0) return best;
+    const TileChoice& big = kCands[0].tc;
+    if (M % big.MT == 0 && N % big.NT == 0 &&
+        (long)(M / big.MT) * (N / big.NT) * split_for(big, M, N, Kp) >= BIG_TILE_MIN_WG)
+        return big;
     for (const Cand& c : kCands) {
         if (M % c.tc.MT != 0 || N % c.tc.NT != 0) continue;
         const long wg = (long)(M / c.tc.MT) * (N / c.tc.NT);
@@ -138,9 +146,9 @@ const char* status_text(int st) {
 
 // ---- launch ----------------------------------------------------------------------------------
 
-// ws: the workspace of the plan (S, repack): split partials first, then the repacked A at the
-// next 256-byte boundary.
-int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, bool repack, int kernel,
+// ws: the workspace of the plan (S, a_layout): split partials first, then (MXFP6_A_REPACK) the
+// repacked A at the next 256-byte boundary.
+int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, int a_layout, int kernel,
         const void* dA, const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
         int A_row_bytes, void* ws, void* stream) {
     mxfp6_launch_desc d;
@@ -161,7 +169,10 @@ int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, bool re
     d.sB = dsB;
     d.D = dD;
     d.ws = S > 1 ? static_cast<float*>(ws) : nullptr;
-    d.Ash = repack ? static_cast<uint8_t*>(ws) + (split_bytes(M, N, S) + 255) / 256 * 256 : nullptr;
+    d.a_layout = a_layout;
+    d.Ash = a_layout == MXFP6_A_REPACK
+                ? static_cast<uint8_t*>(ws) + (split_bytes(M, N, S) + 255) / 256 * 256
+                : nullptr;
     d.stream = stream;
     const int rc = mxfp6_hip_launch(&d);
     return rc == 0 ? MXFP6_OK : rc == 1 ? MXFP6_ERR_TILE : MXFP6_ERR_HIP;
@@ -194,8 +205,8 @@ int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void*
                      M, N, Kp, S, split_bytes(M, N, S), ws_bytes);
         S = 1;
     }
-    return run(out_type, M, N, Kp, tc, S, rp, kernel, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws,
-               stream);
+    return run(out_type, M, N, Kp, tc, S, rp ? MXFP6_A_REPACK : MXFP6_A_ROWS, kernel, dA, dBsh, dsA,
+               dsB, dD, A_row_bytes, ws, stream);
 }
 
 bool tile_divides(const int tile[4], int M, int N) {
@@ -295,12 +306,12 @@ extern "C" int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const i
     if (!plan::tile_divides(tile, M, N)) return MXFP6_ERR_TILE;
     const TileChoice tc = {tile[0], tile[1], tile[2], tile[3]};
     if (!mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW)) return MXFP6_ERR_TILE;
-    return plan::run(out_type, M, N, Kp, tc, 1, false, MXFP6_KERNEL_TILE, dA, dBsh, dsA, dsB, dD,
-                     A_row_bytes, nullptr, stream);
+    return plan::run(out_type, M, N, Kp, tc, 1, MXFP6_A_ROWS, MXFP6_KERNEL_TILE, dA, dBsh, dsA,
+                     dsB, dD, A_row_bytes, nullptr, stream);
 }
 
 extern "C" int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int tile[4],
-                                   int splits, int a_repack, const void* dA, const void* dBsh,
+                                   int splits, int a_layout, const void* dA, const void* dBsh,
                                    const uint8_t* dsA, const uint8_t* dsB, void* dD,
                                    int A_row_bytes, void* ws, size_t ws_bytes, void* stream) {
     if (!tile) return MXFP6_ERR_NULL;
@@ -309,12 +320,15 @@ extern "C" int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int
     if (!plan::tile_divides(tile, M, N)) return MXFP6_ERR_TILE;
     const TileChoice tc = {tile[0], tile[1], tile[2], tile[3]};
     if (!mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW)) return MXFP6_ERR_TILE;
-    if (splits < 1 || splits > Kp / K_TILE || (a_repack != 0 && a_repack != 1)) return MXFP6_ERR_ARG;
-    if ((splits > 1 || a_repack) &&
-        (ws == nullptr || ws_bytes < plan::plan_bytes(M, N, Kp, splits, a_repack != 0)))
+    if (splits < 1 || splits > Kp / K_TILE || a_layout < MXFP6_A_ROWS ||
+        a_layout > MXFP6_A_PRESHUFFLED)
         return MXFP6_ERR_ARG;
-    return plan::run(out_type, M, N, Kp, tc, splits, a_repack != 0, MXFP6_KERNEL_TILE, dA, dBsh,
-                     dsA, dsB, dD, A_row_bytes, ws, stream);
+    const bool repack = a_layout == MXFP6_A_REPACK;
+    if ((splits > 1 || repack) &&
+        (ws == nullptr || ws_bytes < plan::plan_bytes(M, N, Kp, splits, repack)))
+        return MXFP6_ERR_ARG;
+    return plan::run(out_type, M, N, Kp, tc, splits, a_layout, MXFP6_KERNEL_TILE, dA, dBsh, dsA,
+                     dsB, dD, A_row_bytes, ws, stream);
 }
 
 extern "C" int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, int npw,
@@ -329,8 +343,8 @@ extern "C" int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, in
     if (splits > 1 && (ws == nullptr || ws_bytes < (size_t)splits * M * N * sizeof(float)))
         return MXFP6_ERR_ARG;
     const TileChoice tc = {128, 128, mpw, npw};
-    return plan::run(out_type, M, N, Kp, tc, splits, false, MXFP6_KERNEL_DIRECT, dA, dBsh, dsA,
-                     dsB, dD, A_row_bytes, splits > 1 ? ws : nullptr, stream);
+    return plan::run(out_type, M, N, Kp, tc, splits, MXFP6_A_ROWS, MXFP6_KERNEL_DIRECT, dA, dBsh,
+                     dsA, dsB, dD, A_row_bytes, splits > 1 ? ws : nullptr, stream);
 }
 
 extern "C" int mxfp6_gemm_repacks_a(int M, int N, int Kp) {

@@ -12,6 +12,8 @@ namespace plan {
 constexpr int CUS = 256;
 // Shortest K segment of a split, in K-tiles of 192.
 constexpr int MIN_TILES_PER_SEG = 8;
+// Smallest (split) grid for which the 256x256 tile is taken without comparing costs.
+constexpr long BIG_TILE_MIN_WG = 64;
 // Tile columns (N / NT) from which A is repacked to the preshuffled layout first.
 constexpr int REPACK_MIN_TILE_COLS = 8;
 

@@ -156,10 +156,13 @@ def gemm_force_tile(out_type, M, N, Kp, tile, dA, dBsh, dsA, dsB, dD, A_row_byte
                                        A_row_bytes, 0, stream)
 
 
+A_ROWS, A_REPACK, A_PRESHUFFLED = 0, 1, 2
+
+
 def gemm_explicit(out_type, M, N, Kp, tile, splits, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws=0,
-                  ws_bytes=0, stream=None, a_repack=0):
+                  ws_bytes=0, stream=None, a_layout=A_ROWS):
     t = (C.c_int * 4)(*tile)
-    return lib().mxfp6_gemm_explicit(out_type, M, N, Kp, t, splits, a_repack, dA, dBsh, dsA, dsB,
+    return lib().mxfp6_gemm_explicit(out_type, M, N, Kp, t, splits, a_layout, dA, dBsh, dsA, dsB,
                                      dD, A_row_bytes, ws or None, ws_bytes, stream)
 
 

@@ -85,17 +85,20 @@ def run_direct(dp: DevProblem, out_type, splits=1):
     return to_f32(D, out_type, p.M, p.N)
 
 
-def run_explicit(dp: DevProblem, out_type, splits=1, a_repack=0):
+def run_explicit(dp: DevProblem, out_type, splits=1, a_layout=0, a_dev=None):
+    """a_layout 2 reads A from a_dev (a device tensor holding A preshuffled)."""
     p = dp.p
-    ws_bytes = mx.plan_workspace_size(p.M, p.N, p.Kp, splits, a_repack)
+    ws_bytes = mx.plan_workspace_size(p.M, p.N, p.Kp, splits, a_layout == 1)
     ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device="cuda")
     D = dp.out(out_type)
     a, b, sa, sb = dp.ptrs()
+    if a_dev is not None:
+        a = a_dev.data_ptr()
     say(f"  explicit {dp.tile} {p.M}x{p.N}x{p.K} out {mx.OUT_NAMES[out_type]} S {splits} "
-        f"repack {a_repack}")
+        f"A layout {a_layout}")
     rc = mx.gemm_explicit(out_type, p.M, p.N, p.Kp, dp.tile, splits, a, b, sa, sb, D.data_ptr(),
                           p.a_row_bytes, ws.data_ptr() if ws_bytes else 0, ws_bytes,
-                          a_repack=a_repack)
+                          a_layout=a_layout)
     assert rc == 0, mx.STATUS.get(rc, rc)
     torch.cuda.synchronize()
     return to_f32(D, out_type, p.M, p.N)

@@ -89,14 +89,14 @@ def test_router_degenerate_shapes_do_not_trap(mx):
 
 
 def test_router_benchmark_shapes(mx):
-    # the MI355X routing of the five benchmark workloads (cost: CU waves x workgroup work, ties
-    # to the larger tile)
+    # the MI355X routing of the five benchmark workloads (256x256 whenever its grid has >= 64
+    # workgroups, else cost: CU waves x workgroup work, ties to the larger tile)
     want = {
         (256, 256, 1024): ((128, 128, 2, 2), 1),
         (8192, 8192, 8192): ((256, 256, 4, 4), 1),
-        (2048, 6144, 16128): ((128, 384, 4, 3), 1),
+        (2048, 6144, 16128): ((256, 256, 4, 4), 1),
         (2048, 1024, 105728): None,
-        (2048, 5120, 105728): ((128, 128, 2, 2), 1),
+        (2048, 5120, 105728): ((256, 256, 4, 4), 1),
     }
     for (M, N, K), exp in want.items():
         t = mx.choose_tile(M, N, _kpad(K))
@@ -105,3 +105,8 @@ def test_router_benchmark_shapes(mx):
             assert S > 1 and (M // t[0]) * (N // t[1]) * S <= 256
         else:
             assert (tuple(t), S) == exp, (M, N, K, t, S)
+    # A is repacked where the output has >= 8 tile columns
+    for (M, N, K), rp in {(8192, 8192, 8192): True, (2048, 6144, 16128): True,
+                          (2048, 1024, 105728): False, (2048, 5120, 105728): True,
+                          (256, 256, 1024): False}.items():
+        assert mx.repacks_a(M, N, _kpad(K)) == rp, (M, N, K)

@@ -91,7 +91,7 @@ def test_repacked_a_bitwise_equals_direct(g, tile):
     M, N, K = 512, 768, 2112
     p = mx.make_problem(M, N, K, seed=72)
     dp = g.DevProblem(p, tile)
-    Dr = g.run_explicit(dp, mx.OUT_F32, a_repack=1)
+    Dr = g.run_explicit(dp, mx.OUT_F32, a_layout=1)
     Dd = g.run_direct(dp, mx.OUT_F32)
     assert np.array_equal(Dr.view(np.uint32), Dd.view(np.uint32))
 
@@ -100,7 +100,7 @@ def test_repacked_a_split_bitwise_equals_direct_split(g):
     M, N, K = 512, 512, 3072
     p = mx.make_problem(M, N, K, seed=82)
     dp = g.DevProblem(p, (128, 128, 2, 2))
-    Dr = g.run_explicit(dp, mx.OUT_F32, splits=3, a_repack=1)
+    Dr = g.run_explicit(dp, mx.OUT_F32, splits=3, a_layout=1)
     Dd = g.run_direct(dp, mx.OUT_F32, splits=3)
     assert np.array_equal(Dr.view(np.uint32), Dd.view(np.uint32))
 
@@ -119,6 +119,19 @@ def test_device_preshuffle_matches_host_preshuffle(g, orc, compact):
     torch.cuda.synchronize()
     host = orc.preshuffle_b(p.a_packed, M, p.Kp, p.a_row_bytes)
     assert np.array_equal(dst.cpu().numpy(), host)
+
+
+def test_preshuffled_a_input(g):
+    """A handed over already preshuffled (layout 2) gives the repack path's bits."""
+    import torch
+    M, N, K = 256, 512, 1536
+    p = mx.make_problem(M, N, K, seed=24)
+    dp = g.DevProblem(p, (256, 256, 4, 4))
+    ash = torch.empty(M * p.Kp // 4 * 3, dtype=torch.uint8, device="cuda")
+    assert mx.preshuffle_rows(dp.a.data_ptr(), p.a_row_bytes, M, p.Kp, ash.data_ptr()) == 0
+    D2 = g.run_explicit(dp, mx.OUT_F32, a_layout=2, a_dev=ash)
+    D1 = g.run_explicit(dp, mx.OUT_F32, a_layout=1)
+    assert np.array_equal(D1.view(np.uint32), D2.view(np.uint32))
 
 
 def test_routed_repack_and_fallback(g, orc):
@@ -200,6 +213,35 @@ def test_compact_and_padded_a_agree(g):
     Dc = g.run_routed(g.DevProblem(pc, t), mx.OUT_F32)
     Dp = g.run_routed(g.DevProblem(pp, t), mx.OUT_F32)
     assert np.array_equal(Dc.view(np.uint32), Dp.view(np.uint32))
+
+
+@pytest.mark.parametrize("pad", [4, 8, 16])
+def test_row_stride_alignments(g, pad):
+    """A rows at a stride of packed(Kp) + pad bytes (4-, 8- and 16-byte aligned rows): the
+    row-major path, the repack path (its 4/8/16-byte load variants) and the device preshuffle
+    all give the bits of the padded-row problem."""
+    import dataclasses
+    import torch
+    M, N, K = 256, 2048, 992  # Kp 1152; N/NT >= 8 so gemm() repacks
+    pp = mx.make_problem(M, N, K, seed=43, compact=False)
+    rb = pp.a_row_bytes + pad
+    a = np.zeros(M * rb, dtype=np.uint8)
+    a.reshape(M, rb)[:, :pp.a_row_bytes] = pp.a_packed[:M * pp.a_row_bytes].reshape(M, -1)
+    ps = dataclasses.replace(pp, a_packed=a, a_row_bytes=rb)
+    t = mx.choose_tile(M, N, pp.Kp)
+    assert mx.repacks_a(M, N, pp.Kp)
+    ref = g.run_routed(g.DevProblem(pp, t), mx.OUT_F32)
+    dps = g.DevProblem(ps, t)
+    for got in (g.run_routed(dps, mx.OUT_F32), g.run_routed(dps, mx.OUT_F32, with_ws=False),
+                g.run_explicit(dps, mx.OUT_F32, a_layout=1)):
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    ash_p = torch.empty(M * pp.Kp // 4 * 3, dtype=torch.uint8, device="cuda")
+    ash_s = torch.empty_like(ash_p)
+    dpp = g.DevProblem(pp, t)
+    assert mx.preshuffle_rows(dpp.a.data_ptr(), pp.a_row_bytes, M, pp.Kp, ash_p.data_ptr()) == 0
+    assert mx.preshuffle_rows(dps.a.data_ptr(), rb, M, pp.Kp, ash_s.data_ptr()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(ash_p, ash_s)
 
 
 def test_nan_scale_poisons_its_row(g, orc):
