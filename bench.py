@@ -17,17 +17,13 @@ fields it reports:
                 traffic = HBM bytes per launch from the committed rocprofv3 counter summary of
                 the same kernel and workload (FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel
                 calibration), null when no summary matches;
-  sclk_mhz      the graphics clock sampled (amd-smi) while the step loop runs, and frac_at_sclk,
-                the tile kernel's rate against the peak at that clock (4,194,304 flop/clk);
   cpu_baseline  the reference CPU GEMM's arithmetic on this host (a bounded sample, scaled).
 """
 import argparse
 import json
 import os
 import re
-import subprocess
 import sys
-import threading
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -41,8 +37,6 @@ SEED = 0x4D584636
 # MI355X published dense MXFP6 / MXFP4 MFMA peak (TFLOP/s) and HBM bandwidth (GB/s)
 PEAK_TFLOPS = 10100.0
 PEAK_HBM_GBS = 8000.0
-# dense FP6 MFMA flops per clock of the whole chip: 256 CUs x 4 SIMDs x 4096
-FLOP_PER_CLK = 4194304.0
 
 # name -> (M, N, K, out_type, (dist_a, sigma_a), (dist_b, sigma_b), description)
 CONFIGS = {
@@ -91,37 +85,6 @@ def profiled_traffic(workload, kernel):
     return None
 
 
-class ClockSampler:
-    """Samples the graphics clock (amd-smi metric -c, a child process) while work runs."""
-
-    def __init__(self):
-        self.mhz = []
-        self._stop = threading.Event()
-        self._th = threading.Thread(target=self._run, daemon=True)
-
-    def _run(self):
-        time.sleep(0.3)
-        while not self._stop.is_set():
-            try:
-                o = subprocess.run(["amd-smi", "metric", "-c"], capture_output=True, text=True,
-                                   timeout=10).stdout
-            except (OSError, subprocess.SubprocessError):
-                return
-            self.mhz.extend(int(x) for x in re.findall(r"GFX_\d+:\s+CLK:\s+(\d+) MHz", o))
-            self._stop.wait(0.5)
-
-    def __enter__(self):
-        self._th.start()
-        return self
-
-    def __exit__(self, *exc):
-        self._stop.set()
-        self._th.join(timeout=15)
-
-    def mean(self):
-        return sum(self.mhz) / len(self.mhz) if self.mhz else None
-
-
 def cpu_baseline(p, target_cpu_s=12.0):
     """The reference CPU GEMM's arithmetic (tests/reference.hpp: dequantise both operands to FP32,
     then one sequential FP32 dot per output; the oracle's restatement, pinned bit-exact to the
@@ -166,7 +129,7 @@ def copy_calibration(mib=256, reps=5):
     log(f"[bench] copy calibration: {reps} copies of {mib} MiB")
 
 
-def run_config(name, steps, warmup, with_cpu, with_clock=True):
+def run_config(name, steps, warmup, with_cpu):
     import torch
 
     M, N, K, out_type, (da, sa_), (db, sb_), desc = CONFIGS[name]
@@ -249,20 +212,8 @@ def run_config(name, steps, warmup, with_cpu, with_clock=True):
                                          "tile kernel") + ")"
     k_tflops = flops / (k_ms * 1e-3) / 1e12
 
-    # clock while the step loop runs
-    sclk = None
-    if with_clock:
-        with ClockSampler() as clk:
-            t_end = time.time() + 2.0
-            while time.time() < t_end:
-                for _ in range(10):
-                    step()
-                torch.cuda.synchronize()
-        sclk = clk.mean()
-
     log(f"[bench] {name}: {ms * 1e3:.1f} us/step over {steps} steps ({tflops:.1f} TFLOP/s), "
-        f"tile kernel {k_ms * 1e3:.1f} us ({k_tflops:.1f} TFLOP/s), wall {wall_ms:.1f} ms, "
-        f"sclk {sclk if sclk is None else round(sclk)} MHz")
+        f"tile kernel {k_ms * 1e3:.1f} us ({k_tflops:.1f} TFLOP/s), wall {wall_ms:.1f} ms")
     workload = workload_name(M, N, K, out_type)
     traffic = profiled_traffic(workload, kernel_name)
     out = {
@@ -288,8 +239,6 @@ def run_config(name, steps, warmup, with_cpu, with_clock=True):
                      "unit": "TFLOP/s", "frac": round(k_tflops / PEAK_TFLOPS, 4),
                      "traffic": traffic, "kernel": kernel_name, "scope": kernel_scope,
                      "kernel_ms": round(k_ms, 6)},
-        "sclk_mhz": None if sclk is None else round(sclk),
-        "frac_at_sclk": None if sclk is None else round(k_tflops * 1e12 / (FLOP_PER_CLK * sclk * 1e6), 4),
     }
     if with_cpu:
         log(f"[bench] {name}: CPU baseline ...")
@@ -300,12 +249,14 @@ def run_config(name, steps, warmup, with_cpu, with_clock=True):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # long enough for the power controller's clock transient at the start of a burst of GEMMs
+    # to settle (tens of milliseconds on MI355X)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--all", action="store_true", help="every workload, one JSON line each")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-clock", action="store_true", help="skip the clock sampling (profiling)")
+    ap.add_argument("--no-clock", action="store_true", help=argparse.SUPPRESS)  # accepted, no-op
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run the 256 MiB copy kernel that calibrates the HBM byte counters")
     a = ap.parse_args()
@@ -319,8 +270,7 @@ def main():
         return
     names = sorted(CONFIGS) if a.all else [a.config]
     for n in names:
-        print(json.dumps(run_config(n, a.steps, a.warmup, not a.no_cpu, not a.no_clock)),
-              flush=True)
+        print(json.dumps(run_config(n, a.steps, a.warmup, not a.no_cpu)), flush=True)
 
 
 if __name__ == "__main__":

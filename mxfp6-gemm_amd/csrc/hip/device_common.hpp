@@ -49,17 +49,6 @@ __device__ __forceinline__ __hip_bfloat16 cvt_out<__hip_bfloat16>(float v) {
     return __float2bfloat16(v);
 }
 
-// Streaming (non-temporal) store of v converted to OutT: for output that this library does not
-// read again, so it does not evict operand lines from L2.
-template <typename OutT>
-__device__ __forceinline__ void store_out_nt(OutT* p, float v) {
-    const OutT o = cvt_out<OutT>(v);
-    if constexpr (sizeof(OutT) == 4)
-        __builtin_nontemporal_store(v, reinterpret_cast<float*>(p));
-    else
-        __builtin_nontemporal_store(*reinterpret_cast<const uint16_t*>(&o), reinterpret_cast<uint16_t*>(p));
-}
-
 // First K-tile and K-tile count of split segment z when k_tiles tiles are divided into S
 // segments: the first k_tiles % S segments take one extra tile.
 __device__ __forceinline__ void split_segment(int k_tiles, int S, int z, int& kt0, int& nkt) {

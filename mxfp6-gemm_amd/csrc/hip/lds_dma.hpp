@@ -1,0 +1,60 @@
+// gfx950 building blocks of the LDS-pipelined kernels: direct-to-LDS copies (global_load_lds),
+// explicit vector-memory waits, opaque LDS offsets and the XCD-aware workgroup order.
+//
+// The copies are inline asm (M0 + global_load_lds in one statement) so the compiler sees neither an
+// LDS store it could not tell apart from other stages' ds_reads (it would wait for every copy
+// before every read) nor a pending vector load (its loop-merge waits would do the same); the
+// kernels keep the vector-memory count themselves (s_waitcnt vmcnt).
+#pragma once
+#include "device_common.hpp"
+
+namespace mxfp6_dev {
+
+constexpr int NXCD = 8;  // MI355X: 8 XCDs, workgroup id i runs on XCD i % 8
+
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// 16 bytes per lane global -> LDS: lane l's bytes go to LDS m0 + 16*l. `lds` must be uniform.
+__device__ __forceinline__ void dma16(uint32_t lds, const void* gbase, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds), "v"(voff), "s"(gbase)
+                 : "memory");
+}
+
+// Same with a per-lane 64-bit global address.
+__device__ __forceinline__ void dma16_flat(uint32_t lds, const void* gaddr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(lds), "v"(gaddr)
+                 : "memory");
+}
+
+typedef __attribute__((address_space(3))) const char* lds_cptr;
+
+// Returns x unchanged, hidden from the optimizer (forces a VGPR, defeats offset folding).
+__device__ __forceinline__ uint32_t opaque_v(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+__device__ __forceinline__ void wait_vmcnt0() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// Bijective map of the linear workgroup id onto (tile_m, tile_n) such that each XCD receives a
+// contiguous run of the grouped order (groups of XG tile rows, tile_m fastest).
+__device__ __forceinline__ void xcd_tile(int gm, int gn, int XG, int pid, int& tm, int& tn) {
+    const int total = gm * gn;
+    const int per = total / NXCD, rem = total % NXCD;
+    const int x = pid % NXCD, j = pid / NXCD;
+    const int L = x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+    const int band = XG * gn;
+    const int grp = L / band, rows = min(XG, gm - grp * XG), w = L - grp * band;
+    tm = grp * XG + w % rows;
+    tn = w / rows;
+}
+
+}  // namespace mxfp6_dev

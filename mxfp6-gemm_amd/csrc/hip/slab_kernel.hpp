@@ -1,29 +1,41 @@
-// Slab-ring MXFP6 tile kernel for gfx950.
+// Tile kernel of libmxfp6gemm for gfx950: an LDS ring of 64-wide K slabs.
 //
-// Same tile decomposition as tile_kernel.hpp (MT x NT per workgroup, WM x WN waves, each wave
-// MPW x NPW 32x32 blocks accumulated by v_mfma_scale_f32_32x32x64_f8f6f4), but the LDS ring holds
-// single 64-wide K slabs instead of 192-wide K-tiles: NS stages, each with the slab's A rows
-// (48 bytes per row), its B blocks (one 1536-byte preshuffled 32x64 block per 32 columns, copied
-// verbatim) and the workgroup's scale dwords for the slab (one dword per lane per scale group,
-// gathered from the tiled-scale layout with 4-byte LDS DMA). With one slab per stage:
-//   * every slab issues only D = A_ISS + B_ISS + SC_ISS copy instructions per wave, spread over
-//     that slab's MFMAs, so the vector-memory queue never fills and stalls the in-order issue of
-//     the next MFMA (a whole K-tile's copies issued at once did);
-//   * NS - 1 slabs are in flight ahead of the one being multiplied (latency slack);
-//   * a wave waits only for its own copies of the next slab: vmcnt((NS - 2) * D), exact because
-//     every wave issues the same D instructions per slab (waves with nothing to copy in a partial
-//     instruction copy into a dummy LDS area instead of branching).
+// One workgroup computes an MT x NT tile of D with WM x WN waves; wave (wm, wn) owns MPW x NPW
+// 32x32 blocks, accumulated in FP32 AGPRs by v_mfma_scale_f32_32x32x64_f8f6f4 (FP6 E2M3 x FP6
+// E2M3, per-lane E8M0 scales picked by op_sel). K is walked in slabs of 64 (48 packed bytes per
+// row). The LDS ring holds NS slabs; a stage holds the slab's A operand blocks, its B blocks and
+// the workgroup's scale dwords for the slab:
+//   B  preshuffled (preshuffle_B): one 32x64 block is a contiguous 1536-byte tile already in MFMA
+//      operand order (lane t: 16 bytes at 16t, 8 bytes at 1024 + 8t), copied verbatim and read
+//      with linear ds_read_b128 + ds_read_b64 (conflict-free).
+//   A  either repacked into the same preshuffled layout (ASH; the repack kernel runs first) and
+//      then handled exactly like B, or row-major (A_row_bytes per row): each row's 48 bytes copied
+//      in 16-byte chunks, lane l reading 24 bytes at row l%32, byte 24*(l/32) (ds_read_b64 x3,
+//      two-way bank conflicts, and a copy touches ~30 cache lines per KiB instead of 8).
+//   scales  the tiled-scale layout keeps lane l's three slab dwords of a K-tile together; one
+//      4-byte LDS copy per scale group gathers the slab's dword of every lane.
+// Copies are global_load_lds (direct to LDS). Per slab every wave issues the same D copy
+// instructions (waves with nothing to copy in a partial instruction copy into a dummy LDS area
+// instead of branching), spread over the slab's MFMAs, so that:
+//   * the in-order issue of MFMAs never stalls behind a burst of copies or LDS reads;
+//   * NS - 1 slabs are in flight ahead of the one being multiplied;
+//   * a wave waits only for its own copies of the next slab: vmcnt((NS - 2) * D) is exact.
 // Schedule of slab q (registers R[q%2] hold slab q, read during slab q-1):
-//     wait (own copies of slab q+1) | barrier | copy slab q+NS into stage q%NS, read slab q+1 into
-//     R[(q+1)%2], interleaved with the MFMAs of slab q
+//     wait (own copies of slab q+1) | barrier | MFMAs of slab q, interleaved with the copy of
+//     slab q+NS into stage q%NS and the reads of slab q+1 into R[(q+1)%2]
 // The barrier certifies slab q+1 (every wave's copies landed) and frees stage q%NS (every wave
-// read slab q before it). The loop body is branch-free (peeled head and tail).
+// finished reading slab q: its LDS reads completed before the barrier). The steady-state loop
+// body is branch-free; the last NS+1 slabs run a tail step with runtime conditions.
+// Workgroup order: with XG > 0 the linear workgroup id is remapped so the workgroups running at
+// the same time on one XCD cover an XG-row band of output tiles (shared A and B lines in that
+// XCD's L2). Epilogue: lane l of block (mi, ni) holds column l%32 and rows 8g + 4(l/32) + r;
+// D row-major; with SPLIT, FP32 partials of K segment blockIdx.z go to ws[z][M][N].
 #pragma once
 
 #include "../hip_layer.h"
 #include "device_common.hpp"
+#include "lds_dma.hpp"
 #include "repack_kernel.hpp"
-#include "tile_kernel.hpp"  // dma16, dma16_flat, lds_u32, opaque_v, xcd_tile, wait_vmcnt0
 
 namespace mxfp6_dev {
 
@@ -293,12 +305,22 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
                     const size_t idx = (size_t)(m_w + mi * 32 + 8 * g + r) * N + n_w + ni * 32;
                     if (SPLIT)
                         ws[(size_t)blockIdx.z * M * N + idx] = acc[mi][ni][4 * g + r];
-                    else  // D is not read again here: a streaming store keeps L2 for operands
-                        store_out_nt(D + idx, acc[mi][ni][4 * g + r]);
+                    else
+                        D[idx] = cvt_out<OutT>(acc[mi][ni][4 * g + r]);
                 }
 }
 
 // ---- instantiations and launch -------------------------------------------------------------------
+
+// (MT, NT, MPW, NPW) -> wave grid: the scale grouping fixes how many 32-blocks one wave holds,
+// so it also selects between the 4-wave and 8-wave instantiation of a tile.
+inline bool tile_supported(int MT, int NT, int mpw, int npw) {
+    return (MT == 128 && NT == 128 && mpw == 2 && npw == 2) ||
+           (MT == 128 && NT == 256 && mpw == 2 && npw == 4) ||
+           (MT == 128 && NT == 384 && mpw == 4 && npw == 3) ||
+           (MT == 256 && NT == 256 && mpw == 4 && npw == 4) ||
+           (MT == 256 && NT == 256 && mpw == 2 && npw == 4);
+}
 
 // Ring depth per tile: as many slabs as fit 160 KiB of LDS (128 x 128: half of it, two
 // workgroups per CU).
