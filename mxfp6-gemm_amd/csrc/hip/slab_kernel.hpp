@@ -234,9 +234,12 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
     // Steady-state slab q: multiply Rc (slab q) while reading slab q+1 into Rn and copying slab
     // q+NS into stage q%NS. Every wave has issued D copies per slab, so after the copies of slab
     // q+1 exactly NS-2 newer slabs are in flight: vmcnt((NS-2)*D) leaves only them pending.
-    // Placement in the MFMA sequence: read item i after MFMA i * NMF / (ITEMS + 1) and copy j after
-    // MFMA j * NMF / D, so that no wave ever issues a burst of LDS or vector-memory instructions
-    // (with one wave per SIMD, a wave blocked on a full LDS or address queue idles its MFMA unit).
+    // Placement in the MFMA sequence: the copies spread over the first half of the slab's MFMAs
+    // (copy j after MFMA j * (NMF/2) / D), the operand reads over the second half (item i after
+    // MFMA NMF/2 + i * (NMF/2) / ITEMS). No wave issues a burst of LDS or vector-memory
+    // instructions (with one wave per SIMD, a wave blocked on a full queue idles its MFMA unit),
+    // and the copies' LDS writes and the operand reads do not compete for the LDS at the same time
+    // (measured at 8192^3: 810 cycles per slab against 890 with both spread over the whole slab).
     auto slab_step = [&](int q, Slab& Rc, Slab& Rn) {
         const int st = q % NS;
         wait_vmcnt<(NS - 2) * G::D>();
@@ -247,10 +250,10 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
             mfma_one(Rc, k);
 #pragma unroll
             for (int i = 0; i < ITEMS; i++)
-                if (i * NMF / (ITEMS + 1) == k) read_item(i, rbase, Rn);
+                if (NMF / 2 + i * (NMF / 2) / ITEMS == k) read_item(i, rbase, Rn);
 #pragma unroll
             for (int j = 0; j < G::D; j++)
-                if (j * NMF / G::D == k) dma_op(j, q0 + q + NS, st);
+                if (j * (NMF / 2) / G::D == k) dma_op(j, q0 + q + NS, st);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -319,6 +322,7 @@ inline bool tile_supported(int MT, int NT, int mpw, int npw) {
            (MT == 128 && NT == 256 && mpw == 2 && npw == 4) ||
            (MT == 128 && NT == 384 && mpw == 4 && npw == 3) ||
            (MT == 256 && NT == 256 && mpw == 4 && npw == 4) ||
+           (MT == 256 && NT == 192 && mpw == 4 && npw == 3) ||
            (MT == 256 && NT == 256 && mpw == 2 && npw == 4);
 }
 
@@ -360,6 +364,7 @@ int slab_launch(const mxfp6_launch_desc* d, hipStream_t st) {
     if (d->MT == 128 && d->NT == 128) return slab_launch_t<128, 128, 2, 2, 4, 6, OutT>(d, st);
     if (d->MT == 128 && d->NT == 256) return slab_launch_t<128, 256, 2, 2, 4, 8, OutT>(d, st);
     if (d->MT == 128 && d->NT == 384) return slab_launch_t<128, 384, 1, 4, 4, 6, OutT>(d, st);
+    if (d->MT == 256 && d->NT == 192) return slab_launch_t<256, 192, 2, 2, 4, 6, OutT>(d, st);
     if (d->mpw == 2) return slab_launch_t<256, 256, 4, 2, 4, 6, OutT>(d, st);
     return slab_launch_t<256, 256, 2, 2, 4, 6, OutT>(d, st);
 }

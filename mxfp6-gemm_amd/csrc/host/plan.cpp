@@ -17,24 +17,26 @@ namespace plan {
 // Candidate tiles (each an instantiation of the pipelined kernel, 4 waves per workgroup, one
 // workgroup per CU):
 //   256x256, waves 2x2, each wave 128x128 -> MPW 4, NPW 4   (work 4 units of 128x128)
+//   256x192, waves 2x2, each wave 128x96  -> MPW 4, NPW 3   (3 units)
 //   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3   (3 units)
 //   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4   (2 units)
 //   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (1 unit)
 // The kernel is bound by the per-CU global->LDS copy rate (64 B/clk per CU on MI355X), so the
-// tile that moves the fewest operand bytes per flop, 256x256, is preferred whenever it divides
-// the shape and its (split) grid has at least BIG_TILE_MIN_WG workgroups: measured on MI355X it
-// beats a smaller tile that fills every CU (a 256x256 workgroup does 4/3 to 4x the work per
-// copied byte). Otherwise a candidate must divide the shape, workgroup-starved grids are split
-// along K (split_for), and the cost of a candidate is the number of CU waves its (split) grid
-// needs times the work of one workgroup: ceil(wg * S / CUS) * units / S. The cheapest wins; ties
-// go to the larger tile.
+// tiles that move the fewest operand bytes per flop, 256x256 and 256x192, are preferred whenever
+// one divides the shape and its (split) grid has at least BIG_TILE_MIN_WG workgroups: measured on
+// MI355X they beat a smaller tile that fills every CU. Between the two, and otherwise among all
+// candidates that divide the shape, workgroup-starved grids are split along K (split_for) and the
+// cost of a candidate is the number of CU waves its (split) grid needs times the work of one
+// workgroup: ceil(wg * S / CUS) * units / S. The cheapest wins; ties go to the earlier (larger)
+// tile.
 namespace {
 struct Cand {
     TileChoice tc;
     int units;
 };
-const Cand kCands[] = {{{256, 256, 4, 4}, 4}, {{128, 384, 4, 3}, 3}, {{128, 256, 2, 4}, 2},
-                       {{128, 128, 2, 2}, 1}};
+const Cand kCands[] = {{{256, 256, 4, 4}, 4}, {{256, 192, 4, 3}, 3}, {{128, 384, 4, 3}, 3},
+                       {{128, 256, 2, 4}, 2}, {{128, 128, 2, 2}, 1}};
+constexpr int N_BIG = 2;  // kCands[0 .. N_BIG) are the big tiles
 
 // K segments for a tile on (M, N, Kp): a grid that fills at most half the CUs is split into
 // S = floor(CUS / base_wg) segments (the split grid still fits one CU wave), each at least
@@ -54,16 +56,29 @@ int split_for(const TileChoice& tc, int M, int N, int Kp) {
 TileChoice route(int M, int N, int Kp) {
     TileChoice best = {128, 128, 2, 2};
     double best_cost = -1;
-    if (M <= 0 || N <= 0 || Kp <= 0) return best;
-    const TileChoice& big = kCands[0].tc;
-    if (M % big.MT == 0 && N % big.NT == 0 &&
-        (long)(M / big.MT) * (N / big.NT) * split_for(big, M, N, Kp) >= BIG_TILE_MIN_WG)
-        return big;
-    for (const Cand& c : kCands) {
-        if (M % c.tc.MT != 0 || N % c.tc.NT != 0) continue;
+    // shapes gemm() rejects (M, N multiples of 128, Kp of K_TILE) get the smallest tile, no split
+    if (M <= 0 || N <= 0 || Kp <= 0 || M % 128 != 0 || N % 128 != 0 || Kp % K_TILE != 0)
+        return best;
+    auto cost_of = [&](const Cand& c) {
         const long wg = (long)(M / c.tc.MT) * (N / c.tc.NT);
         const int S = split_for(c.tc, M, N, Kp);
-        const double cost = (double)((wg * S + CUS - 1) / CUS) * c.units / S;
+        return (double)((wg * S + CUS - 1) / CUS) * c.units / S;
+    };
+    for (int i = 0; i < N_BIG; i++) {
+        const Cand& c = kCands[i];
+        if (M % c.tc.MT != 0 || N % c.tc.NT != 0) continue;
+        if ((long)(M / c.tc.MT) * (N / c.tc.NT) * split_for(c.tc, M, N, Kp) < BIG_TILE_MIN_WG)
+            continue;
+        const double cost = cost_of(c);
+        if (best_cost < 0 || cost < best_cost - 1e-9) {
+            best = c.tc;
+            best_cost = cost;
+        }
+    }
+    if (best_cost >= 0) return best;
+    for (const Cand& c : kCands) {
+        if (M % c.tc.MT != 0 || N % c.tc.NT != 0) continue;
+        const double cost = cost_of(c);
         if (best_cost < 0 || cost < best_cost - 1e-9) {
             best = c.tc;
             best_cost = cost;
@@ -96,14 +111,15 @@ size_t plan_bytes(int M, int N, int Kp, int S, bool repack) {
 }
 
 bool route_repacks(int M, int N, int Kp) {
-    if (M <= 0 || N <= 0 || Kp <= 0) return false;
+    if (M <= 0 || N <= 0 || Kp <= 0 || M % 128 != 0 || N % 128 != 0 || Kp % K_TILE != 0)
+        return false;
     const TileChoice tc = route(M, N, Kp);
     if (M % tc.MT != 0 || N % tc.NT != 0) return false;
     return repack_for(tc, M, N, Kp);
 }
 
 int splitk_segments(int M, int N, int Kp) {
-    if (M <= 0 || N <= 0 || Kp <= 0) return 1;
+    if (M <= 0 || N <= 0 || Kp <= 0 || M % 128 != 0 || N % 128 != 0 || Kp % K_TILE != 0) return 1;
     const TileChoice tc = route(M, N, Kp);
     if (M % tc.MT != 0 || N % tc.NT != 0) return 1;
     return split_for(tc, M, N, Kp);

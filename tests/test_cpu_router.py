@@ -16,7 +16,8 @@ GOLD = os.path.join(os.path.dirname(__file__), "golden")
 with open(os.path.join(GOLD, "ref_routing.json")) as f:
     REF = json.load(f)
 
-IMPLEMENTED = {(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3), (256, 256, 4, 4)}
+IMPLEMENTED = {(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3), (256, 256, 4, 4),
+               (256, 192, 4, 3)}
 
 
 def _kpad(K):
@@ -89,12 +90,12 @@ def test_router_degenerate_shapes_do_not_trap(mx):
 
 
 def test_router_benchmark_shapes(mx):
-    # the MI355X routing of the five benchmark workloads (256x256 whenever its grid has >= 64
-    # workgroups, else cost: CU waves x workgroup work, ties to the larger tile)
+    # the MI355X routing of the five benchmark workloads (256x256 or 256x192 whenever the grid has
+    # >= 64 workgroups, else cost: CU waves x workgroup work, ties to the larger tile)
     want = {
         (256, 256, 1024): ((128, 128, 2, 2), 1),
         (8192, 8192, 8192): ((256, 256, 4, 4), 1),
-        (2048, 6144, 16128): ((256, 256, 4, 4), 1),
+        (2048, 6144, 16128): ((256, 192, 4, 3), 1),
         (2048, 1024, 105728): None,
         (2048, 5120, 105728): ((256, 256, 4, 4), 1),
     }

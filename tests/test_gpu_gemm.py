@@ -47,7 +47,8 @@ def test_routed_small_shapes(g, orc, out_type, M, N, K):
 
 
 @pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
-                                  (256, 256, 4, 4), (256, 256, 2, 4)])
+                                  (256, 256, 4, 4), (256, 256, 2, 4),
+                                  (256, 192, 4, 3)])
 @pytest.mark.parametrize("out_type", [0, 1, 2])
 def test_forced_tiles(g, orc, tile, out_type):
     M, N, K = 256, 768, 960  # K-tail: kpad(960) = 1152
@@ -58,7 +59,8 @@ def test_forced_tiles(g, orc, tile, out_type):
 
 
 @pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
-                                  (256, 256, 4, 4), (256, 256, 2, 4)])
+                                  (256, 256, 4, 4), (256, 256, 2, 4),
+                                  (256, 192, 4, 3)])
 def test_pipelined_kernel_bitwise_equals_direct(g, tile):
     """Both kernels add the same MFMA results in the same K order, so FP32 outputs are equal
     bit for bit (covers every wave block, slab and stage of the pipelined kernel)."""
@@ -85,7 +87,8 @@ def test_pipelined_split_bitwise_equals_direct_split(g):
 # ---- A repacked into the preshuffled layout ------------------------------------------------------
 
 @pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
-                                  (256, 256, 4, 4), (256, 256, 2, 4)])
+                                  (256, 256, 4, 4), (256, 256, 2, 4),
+                                  (256, 192, 4, 3)])
 def test_repacked_a_bitwise_equals_direct(g, tile):
     """The kernel reading the repacked A multiplies the same operands in the same order."""
     M, N, K = 512, 768, 2112
