@@ -38,18 +38,29 @@ const Cand kCands[] = {{{256, 256, 4, 4}, 4}, {{256, 192, 4, 3}, 3}, {{128, 384,
                        {{128, 256, 2, 4}, 2}, {{128, 128, 2, 2}, 1}};
 constexpr int N_BIG = 2;  // kCands[0 .. N_BIG) are the big tiles
 
-// K segments for a tile on (M, N, Kp): a grid that fills at most half the CUs is split into
-// S = floor(CUS / base_wg) segments (the split grid still fits one CU wave), each at least
-// MIN_TILES_PER_SEG K-tiles long so the per-segment prologue and the FP32 round trip of the
-// partials stay small against the segment's MFMA work.
+// K segments for a tile on (M, N, Kp), from a time model: a (split) grid of wg * S workgroups
+// takes ceil(wg * S / CUS) CU waves of t_tile / S each (t_tile: one workgroup over all of K at
+// CU_RATE), and every segment adds one FP32 write and read of an M x N partial at PARTIAL_BW.
+// S runs up to MAX_SPLITS with at least MIN_TILES_PER_SEG K-tiles per segment; a split must beat
+// S = 1 by SPLIT_MIN_GAIN. Measured at 2048x5120x105728 (160 workgroups of 256x256): S = 1, 3, 4,
+// 6, 8 take 792, 688, 746, 734, 763 us, and the model picks S = 3; 2048x1024x105728 gets S = 8.
 int split_for(const TileChoice& tc, int M, int N, int Kp) {
-    const long base_wg = (long)(M / tc.MT) * (N / tc.NT);
+    const long wg = (long)(M / tc.MT) * (N / tc.NT);
     const int k_tiles = Kp / K_TILE;
-    if (base_wg <= 0 || 2 * base_wg > CUS) return 1;
-    long S = CUS / base_wg;
-    const long s_cap = k_tiles / MIN_TILES_PER_SEG;
-    if (S > s_cap) S = s_cap;
-    return S < 2 ? 1 : (int)S;
+    if (wg <= 0) return 1;
+    const double t_tile = (double)k_tiles * 2.0 * tc.MT * tc.NT * K_TILE / CU_RATE;
+    const double t_part = 2.0 * M * N * sizeof(float) / PARTIAL_BW;
+    const double base = (double)((wg + CUS - 1) / CUS) * t_tile;
+    int best = 1;
+    double best_cost = base * (1.0 - SPLIT_MIN_GAIN);
+    for (int S = 2; S <= MAX_SPLITS && k_tiles / S >= MIN_TILES_PER_SEG; S++) {
+        const double cost = (double)((wg * S + CUS - 1) / CUS) * t_tile / S + S * t_part;
+        if (cost < best_cost) {
+            best = S;
+            best_cost = cost;
+        }
+    }
+    return best;
 }
 }  // namespace
 

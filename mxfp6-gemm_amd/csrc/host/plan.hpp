@@ -10,8 +10,14 @@ namespace plan {
 
 // MI355X: 256 compute units (8 XCDs x 32 CUs).
 constexpr int CUS = 256;
-// Shortest K segment of a split, in K-tiles of 192.
+// Split-K model (see split_for): shortest segment in K-tiles of 192, most segments, the dense
+// MXFP6 rate of one CU under full load (MI355X at its power limit: ~3.35 PF / 256 CUs), the
+// bandwidth of the partials' round trip, and the least gain a split must promise.
 constexpr int MIN_TILES_PER_SEG = 8;
+constexpr int MAX_SPLITS = 16;
+constexpr double CU_RATE = 13e12;
+constexpr double PARTIAL_BW = 5e12;
+constexpr double SPLIT_MIN_GAIN = 0.05;
 // Smallest (split) grid for which the 256x256 tile is taken without comparing costs.
 constexpr long BIG_TILE_MIN_WG = 64;
 // Tile columns (N / NT) from which A is repacked to the preshuffled layout first.
