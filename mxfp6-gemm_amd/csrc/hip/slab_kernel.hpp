@@ -18,14 +18,16 @@
 // instructions (waves with nothing to copy in a partial instruction copy into a dummy LDS area
 // instead of branching), spread over the slab's MFMAs, so that:
 //   * the in-order issue of MFMAs never stalls behind a burst of copies or LDS reads;
-//   * NS - 1 slabs are in flight ahead of the one being multiplied;
-//   * a wave waits only for its own copies of the next slab: vmcnt((NS - 2) * D) is exact.
+//   * NS - 2 slabs are in flight ahead of the one being multiplied;
+//   * a wave waits only for its own copies of the next slab: vmcnt((NS - 3) * D) is exact.
 // Schedule of slab q (registers R[q%2] hold slab q, read during slab q-1):
 //     wait (own copies of slab q+1) | barrier | MFMAs of slab q, interleaved with the copy of
-//     slab q+NS into stage q%NS and the reads of slab q+1 into R[(q+1)%2]
-// The barrier certifies slab q+1 (every wave's copies landed) and frees stage q%NS (every wave
-// finished reading slab q: its LDS reads completed before the barrier). The steady-state loop
-// body is branch-free; the last NS+1 slabs run a tail step with runtime conditions.
+//     slab q+NS-1 into stage (q-1)%NS and the reads of slab q+1 into R[(q+1)%2]
+// The barrier certifies slab q+1 (every wave's copies landed) and frees stage (q-1)%NS: every
+// wave has issued the MFMAs of slab q-1, so its reads of that stage have completed. The reads of
+// slab q, issued during slab q-1, may still be in flight at the barrier; nothing waits for them
+// before the MFMAs that use them. The steady-state loop body is branch-free; the last NS slabs
+// run a tail step with runtime conditions.
 // Workgroup order: with XG > 0 the linear workgroup id is remapped so the workgroups running at
 // the same time on one XCD cover an XG-row band of output tiles (shared A and B lines in that
 // XCD's L2). Epilogue: lane l of block (mi, ni) holds column l%32 and rows 8g + 4(l/32) + r;
@@ -53,6 +55,10 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Workgroup barrier without the LDS fence of __syncthreads (which waits for every outstanding LDS
+// read of the wave). The memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 template <int MT, int NT, int WM, int WN, int NS>
 struct SlabGeom {
     static constexpr int MPW = MT / 32 / WM, NPW = NT / 32 / WN;
@@ -70,7 +76,7 @@ struct SlabGeom {
     static constexpr int LDS = NS * STAGE + 1024;              // + dummy sink
     static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole-wave chunks");
     static_assert(STAGE % 16 == 0, "16-byte aligned stages");
-    static_assert((NS - 2) * D <= 63, "vmcnt range");
+    static_assert(NS >= 4 && (NS - 2) * D <= 63, "vmcnt range");
 };
 
 template <int MT, int NT, int WM, int WN, int NS, int XG, typename OutT, bool SPLIT, bool ASH>
@@ -157,7 +163,9 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
         }
     };
 
-    // operand reads (offsets hidden per operand so reads of different operands are not fused)
+    // Operand reads. Per slab every operand kind gets one base address (hidden from the compiler,
+    // so it neither re-derives it per read nor fuses reads of different kinds); the blocks of a
+    // kind are immediate offsets from it.
     const lds_cptr lds3 = (lds_cptr)lds;
     const int a_off = ASH ? wm * MPW * OPBLK_BYTES + lane * 16
                           : (wm * MPW * 32 + (lane & 31)) * SLAB_BYTES + (lane >> 5) * 24;
@@ -168,13 +176,27 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
         v8i a[MPW], b[NPW];
         int sa, sb;
     };
+    struct Bases {
+        uint32_t a16, a8, b16, b8, sa, sb;
+    };
+    // the preshuffled blocks: lane t reads 16 bytes at 16t and 8 bytes at 1024 + 8t
+    auto slab_bases = [&](uint32_t base) {
+        Bases r;
+        r.a16 = opaque_v(base + a_off);
+        r.a8 = ASH ? opaque_v(base + a_off + 1024 - 8 * lane) : 0u;
+        r.b16 = opaque_v(base + b_off);
+        r.b8 = opaque_v(base + b_off + 1024 - 8 * lane);
+        r.sa = opaque_v(base + sa_off);
+        r.sb = opaque_v(base + sb_off);
+        return r;
+    };
     // Operand reads of one slab as items: item 0 = both scale dwords, then the A and B operands in
     // the order the slab's MFMAs first use them (MFMA k multiplies a[k % MPW] by b[k / MPW]).
     constexpr int ITEMS = 1 + MPW + NPW;
-    auto read_item = [&](int item, uint32_t base, Slab& R) {
+    auto read_item = [&](int item, const Bases& bs, Slab& R) {
         if (item == 0) {
-            R.sa = *reinterpret_cast<const __attribute__((address_space(3))) int*>(lds3 + base + sa_off);
-            R.sb = *reinterpret_cast<const __attribute__((address_space(3))) int*>(lds3 + base + sb_off);
+            R.sa = *reinterpret_cast<const __attribute__((address_space(3))) int*>(lds3 + bs.sa);
+            R.sb = *reinterpret_cast<const __attribute__((address_space(3))) int*>(lds3 + bs.sb);
             return;
         }
         // items: 1 = A0, 2 = B0, 3 .. MPW+1 = A1 .. A(MPW-1), MPW+2 .. = B1 .. B(NPW-1)
@@ -189,26 +211,25 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
             kind_b = 1, idx = item - 1 - MPW;
         }
         if (!kind_b && ASH) {
-            const uint32_t o = opaque_v(base + a_off + idx * OPBLK_BYTES);
-            const v4i y0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(lds3 + o);
-            const v2i y1 = *reinterpret_cast<const __attribute__((address_space(3))) v2i*>(lds3 + o + (1024 - 8 * lane));
+            const v4i y0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(lds3 + bs.a16 + idx * OPBLK_BYTES);
+            const v2i y1 = *reinterpret_cast<const __attribute__((address_space(3))) v2i*>(lds3 + bs.a8 + idx * OPBLK_BYTES);
             const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
             R.a[idx] = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
         } else if (!kind_b) {
-            const uint32_t o = opaque_v(base + a_off + idx * 32 * SLAB_BYTES);
+            const uint32_t o = opaque_v(bs.a16 + idx * 32 * SLAB_BYTES);
             const v6i_a8 x = *reinterpret_cast<const __attribute__((address_space(3))) v6i_a8*>(lds3 + o);
             R.a[idx] = __builtin_shufflevector(x, x, 0, 1, 2, 3, 4, 5, -1, -1);
         } else {
-            const uint32_t o = opaque_v(base + b_off + idx * OPBLK_BYTES);
-            const v4i y0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(lds3 + o);
-            const v2i y1 = *reinterpret_cast<const __attribute__((address_space(3))) v2i*>(lds3 + o + (1024 - 8 * lane));
+            const v4i y0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(lds3 + bs.b16 + idx * OPBLK_BYTES);
+            const v2i y1 = *reinterpret_cast<const __attribute__((address_space(3))) v2i*>(lds3 + bs.b8 + idx * OPBLK_BYTES);
             const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
             R.b[idx] = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
         }
     };
     auto read_slab = [&](int st, Slab& R) {
+        const Bases bs = slab_bases(st * STAGE);
 #pragma unroll
-        for (int i = 0; i < ITEMS; i++) read_item(i, st * STAGE, R);
+        for (int i = 0; i < ITEMS; i++) read_item(i, bs, R);
     };
 
     v16f acc[MPW][NPW];
@@ -232,8 +253,8 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
 
     Slab R0, R1;
     // Steady-state slab q: multiply Rc (slab q) while reading slab q+1 into Rn and copying slab
-    // q+NS into stage q%NS. Every wave has issued D copies per slab, so after the copies of slab
-    // q+1 exactly NS-2 newer slabs are in flight: vmcnt((NS-2)*D) leaves only them pending.
+    // q+NS-1 into stage (q-1)%NS. Every wave has issued D copies per slab, so after the copies of
+    // slab q+1 exactly NS-3 newer slabs are in flight: vmcnt((NS-3)*D) leaves only them pending.
     // Placement in the MFMA sequence: the copies spread over the first half of the slab's MFMAs
     // (copy j after MFMA j * (NMF/2) / D), the operand reads over the second half (item i after
     // MFMA NMF/2 + i * (NMF/2) / ITEMS). No wave issues a burst of LDS or vector-memory
@@ -241,50 +262,55 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
     // and the copies' LDS writes and the operand reads do not compete for the LDS at the same time
     // (measured at 8192^3: 810 cycles per slab against 890 with both spread over the whole slab).
     auto slab_step = [&](int q, Slab& Rc, Slab& Rn) {
-        const int st = q % NS;
-        wait_vmcnt<(NS - 2) * G::D>();
-        __syncthreads();  // slab q+1 landed for every wave; every wave is done reading stage st
+        const int st = (q + NS - 1) % NS;
+        wait_vmcnt<(NS - 3) * G::D>();
+        ring_barrier();  // slab q+1 landed for every wave; every wave is done reading stage st
         const uint32_t rbase = ((q + 1) % NS) * STAGE;
+        Bases bs;
 #pragma unroll
         for (int k = 0; k < NMF; k++) {
             mfma_one(Rc, k);
+            if (k == NMF / 2) bs = slab_bases(rbase);
 #pragma unroll
             for (int i = 0; i < ITEMS; i++)
-                if (NMF / 2 + i * (NMF / 2) / ITEMS == k) read_item(i, rbase, Rn);
+                if (NMF / 2 + i * (NMF / 2) / ITEMS == k) read_item(i, bs, Rn);
 #pragma unroll
             for (int j = 0; j < G::D; j++)
-                if (j * (NMF / 2) / G::D == k) dma_op(j, q0 + q + NS, st);
+                if (j * (NMF / 2) / G::D == k) dma_op(j, q0 + q + NS - 1, st);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    // Tail slab q (the last NS+1 slabs): the same with runtime conditions, full waits and the
+    // Tail slab q (the last NS slabs): the same with runtime conditions, full waits and the
     // remaining copies issued in one block.
     auto tail_step = [&](int q, Slab& Rc, Slab& Rn) {
         if (q + 1 < nq) {
             wait_vmcnt0();
-            __syncthreads();
+            ring_barrier();
             read_slab((q + 1) % NS, Rn);
-            if (q + NS < nq) {
+            if (q + NS - 1 < nq) {
 #pragma unroll
-                for (int j = 0; j < G::D; j++) dma_op(j, q0 + q + NS, q % NS);
+                for (int j = 0; j < G::D; j++) dma_op(j, q0 + q + NS - 1, (q + NS - 1) % NS);
             }
         }
 #pragma unroll
         for (int k = 0; k < NMF; k++) mfma_one(Rc, k);
     };
 
-    // prologue: slabs 0..min(NS, nq)-1 in flight, slab 0 resident and read
-    const int pro = nq < NS ? nq : NS;
+    // prologue: slabs 0..min(NS-1, nq)-1 in flight, slab 0 resident and read
+    const int pro = nq < NS - 1 ? nq : NS - 1;
     for (int q = 0; q < pro; q++)
 #pragma unroll
         for (int j = 0; j < G::D; j++) dma_op(j, q0 + q, q);
-    wait_vmcnt0();
-    __syncthreads();
+    if (pro == NS - 1)
+        wait_vmcnt<(NS - 2) * G::D>();
+    else
+        wait_vmcnt0();
+    ring_barrier();
     read_slab(0, R0);
 
     int q = 0;
     // two slabs per iteration keep the register roles static; the body is branch-free
-    for (; q + 1 + NS < nq; q += 2) {
+    for (; q + NS < nq; q += 2) {
         slab_step(q, R0, R1);
         slab_step(q + 1, R1, R0);
     }
