@@ -146,6 +146,43 @@ int mxfp6_preshuffle_b(const uint8_t* packed, int N, int K, int row_bytes, uint8
 size_t mxfp6_tile_scale_bytes(int dim, int K, int group, int subs);
 int mxfp6_tile_scale(const uint8_t* pscale, int dim, int K, int group, int subs, uint8_t* out);
 
+/* ---- the same formats produced on the device (one HBM pass over float operands) ------------
+ * The reference has host loops only; these are their device counterparts, bit-identical to them.
+ * Inputs and outputs are device pointers; the calls are asynchronous on `stream`. */
+
+/* quantize_to_mxfp6 (preprocess.hpp:51-97) of row-major float d_x[rows][cols] (cols % 32 == 0,
+ * d_x 16-byte aligned): row r's 3*cols/4 code bytes at d_packed + r * packed_row_bytes (>= 3*cols/4,
+ * a multiple of 4; the bytes past the codes are set to 0), scales at d_scales[r * scale_cols + c]
+ * (scale_cols >= cols/32; columns past cols/32 set to 127, as pad_scales_k, :32-38, does). */
+int mxfp6_quantize_async(const float* d_x, int rows, int cols, void* d_packed,
+                         size_t packed_row_bytes, uint8_t* d_scales, int scale_cols, void* stream);
+
+/* A operand ready for mxfp6_gemm: quantize_to_mxfp6 of d_A[M][K] (K % 32 == 0) into rows of
+ * a_row_bytes (>= 3*K/4, a multiple of 4; bytes past the codes zero: a_row_bytes = 3*kpad(K)/4
+ * gives padded rows with a zero K-tail), and the scales padded to kpad(K) and tiled as
+ * tile_scale(preprocess_scale(pad_scales_k(..)), group, 3) (:32-38, :136-162, :216-233) with
+ * group = the tile's MPW; M % (32 * group) == 0. d_tiled holds mxfp6_tiled_scale_bytes(M, K,
+ * group) bytes. */
+int mxfp6_prepare_a_async(const float* d_A, int M, int K, int group, void* d_packed,
+                          size_t a_row_bytes, uint8_t* d_tiled, void* stream);
+
+/* B operand ready for mxfp6_gemm from row-major float d_B[K][N]: preprocess_B (:112-118), K
+ * padded to kpad(K) with zero codes, preshuffle_B (:182-207) into d_bsh
+ * (mxfp6_preshuffled_bytes(N, K) bytes, 16-byte aligned), and the scales tiled as for A with
+ * group = the tile's NPW; N % (32 * group) == 0. */
+int mxfp6_prepare_b_async(const float* d_B, int K, int N, int group, void* d_bsh,
+                          uint8_t* d_tiled, void* stream);
+
+/* Scales already quantised: d_scales[dim][ld] (K/32 valid columns) -> padded to kpad(K) and
+ * tiled (group) as above. */
+int mxfp6_tile_scales_async(const uint8_t* d_scales, int dim, int K, int ld, int group,
+                            uint8_t* d_tiled, void* stream);
+
+/* Sizes of the device layouts at kpad(K): preshuffled operand (dim/32 * kpad(K)/64 * 1536) and
+ * tiled scales (tile_scale(.., group, 3)). 0 for shapes the layouts cannot hold. */
+size_t mxfp6_preshuffled_bytes(int dim, int K);
+size_t mxfp6_tiled_scale_bytes(int dim, int K, int group);
+
 /* ---- synthetic operands (the benchmark workloads) ----------------------------------------- */
 
 /* Distributions of mxfp6_gen_operand. */

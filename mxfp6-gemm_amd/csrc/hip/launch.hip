@@ -1,7 +1,10 @@
 // HIP launch layer: maps a host plan (mxfp6_launch_desc) onto kernel instantiations, grids and
 // a stream. This file and the kernels it includes are the only HIP code in the library.
+#include <algorithm>
+
 #include "../hip_layer.h"
 #include "direct_kernel.hpp"
+#include "prep_kernel.hpp"
 #include "reduce_kernel.hpp"
 #include "slab_kernel.hpp"
 
@@ -82,4 +85,36 @@ extern "C" int mxfp6_hip_repack(const void* src, int row_bytes, int rows, int Kp
 
 extern "C" int mxfp6_hip_has_tile(int MT, int NT, int mpw, int npw) {
     return tile_supported(MT, NT, mpw, npw) ? 1 : 0;
+}
+
+extern "C" int mxfp6_hip_quantize_rows(const float* x, int rows, int cols, int nblk, void* packed,
+                                       size_t row_bytes, uint8_t* scales, int scale_mode,
+                                       int ncols, int group, int Kp, void* stream) {
+    const int per_wg = PREP_BLKS_PER_WAVE * (PREP_THREADS / 64);
+    const unsigned chunks = (unsigned)((nblk + per_wg - 1) / per_wg);
+    const ScaleOut so{scales, scale_mode, ncols, group, Kp / 192};
+    prep_rows_kernel<<<dim3(chunks * (unsigned)rows), dim3(PREP_THREADS), 0,
+                       static_cast<hipStream_t>(stream)>>>(x, cols, nblk,
+                                                           static_cast<uint8_t*>(packed),
+                                                           row_bytes, so, (int)chunks);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+extern "C" int mxfp6_hip_prepare_b(const float* B, int K, int N, int Kp, int group, void* bsh,
+                                   uint8_t* tiled, void* stream) {
+    const unsigned nchunks = (unsigned)((N + 63) / 64), kchunks = (unsigned)((Kp / 32 + 3) / 4);
+    prep_b_kernel<<<dim3(nchunks * kchunks), dim3(PREP_THREADS), 0,
+                    static_cast<hipStream_t>(stream)>>>(B, K, N, Kp, group,
+                                                        static_cast<uint8_t*>(bsh), tiled,
+                                                        (int)nchunks);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+extern "C" int mxfp6_hip_tile_scales(const uint8_t* s, int dim, int vblk, int ld, int Kp,
+                                     int group, uint8_t* tiled, void* stream) {
+    const size_t total = (size_t)dim * (Kp / 32);
+    const unsigned blocks = (unsigned)std::min<size_t>((total + PREP_THREADS - 1) / PREP_THREADS, 65536);
+    tile_scales_kernel<<<dim3(blocks), dim3(PREP_THREADS), 0, static_cast<hipStream_t>(stream)>>>(
+        s, dim, vblk, ld, Kp, group, tiled);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
 }

@@ -1,0 +1,219 @@
+// Quantisation and layout kernels: float operands -> the GEMM's device formats in one HBM pass.
+//
+// The GEMM consumes three formats (reference include/mxfp6/preprocess.hpp):
+//   packed rows   FP6 E2M3 codes, 4 codes in 3 bytes LSB-first (types.hpp:97-117), one E8M0
+//                 scale per 32 consecutive values of a row (quantize_to_mxfp6, :51-97);
+//   preshuffled B B^T quantised (preprocess_B, :112-118), padded to Kp with zero codes and cut into
+//                 1536-byte tiles per (32 columns, 64-wide K slab) in MFMA operand order
+//                 (preshuffle_B, :182-207): lane t = 32h + i holds column i's 32-block 2q + h,
+//                 its first 16 packed bytes at 16t, the last 8 at 1024 + 8t;
+//   tiled scales  scales padded to Kp with code 127 (pad_scales_k, :32-38), put in MFMA lane
+//                 order (preprocess_scale, :136-162) and grouped (tile_scale(group, 3), :216-233):
+//                 the scale of (row r, 32-block c) sits at byte
+//                 ((((g * ktn + kt) * 64 + lane) * 3 + sub) * gp + j), with t = r / 32,
+//                 lane = r % 32 + 32 * (c % 2), q = c / 2, g = t / group, j = t % group,
+//                 kt = q / 3, sub = q % 3, ktn = Kp / 192, gp = group rounded up to 4 (the
+//                 gp - group pad bytes of every dword are zero).
+//
+// Quantisation rule (quantize_to_mxfp6): per 32-block amax = max |x|; a zero block gets code 127;
+// otherwise need = amax / 7.5 (FP32 division) and the scale is the smallest power of two >= need,
+// code = clamp(log2(scale) + 127, 0, 254). Every value is divided by the scale (here multiplied
+// by its reciprocal, a power of two in [2^-126, 2^127]: the same correctly rounded quotient) and
+// encoded by float_to_fp6_e2m3 (types.hpp:26-72): magnitude saturated at 7.5, round to nearest
+// E2M3 with ties to the even code, sign from x < 0 (so a negative value that rounds to zero keeps
+// code 0x20, and -0.0 gives 0x00).
+//
+// Kernels (all HBM-bound; algorithmic bytes = 4 per value read + 0.75 per value and 1/32 per
+// scale written):
+//   prep_rows_kernel  row-major float [rows][cols] -> packed rows (+ zero tail up to row_bytes) and
+//                     scales, raw [rows][scale_cols] (tail columns 127) or tiled at Kp. A wave
+//                     takes 64 consecutive 32-blocks of one row: coalesced float4 loads into LDS,
+//                     then lane l quantises block l and writes its 24 bytes (consecutive lanes,
+//                     consecutive bytes).
+//   prep_b_kernel     row-major float B [K][N] -> preshuffled B^T at Kp + tiled scales. Lane n of
+//                     a wave takes column n and one 32-block: 32 loads each coalesced across the
+//                     wave's 64 consecutive columns; its 24 bytes land at 16t / 1024 + 8t of the
+//                     column's tile, so the wave's stores are contiguous too.
+//   tile_scales_kernel raw scales [dim][ld] (K/32 valid columns) -> tiled at Kp.
+#pragma once
+#include "device_common.hpp"
+
+namespace mxfp6_dev {
+
+// float_to_fp6_e2m3 (types.hpp:26-72) for a finite input.
+__device__ __forceinline__ uint32_t e2m3_code(float v) {
+    const uint32_t sign = v < 0.0f ? 0x20u : 0u;
+    const float a = fminf(fabsf(v), 7.5f);
+    // binade [0,1) -> 0 (step 1/8), [1,2) -> 1, [2,4) -> 2, [4,7.5] -> 3; offset in steps is exact
+    const int b = a < 1.0f ? 0 : a < 2.0f ? 1 : a < 4.0f ? 2 : 3;
+    const float steps = b == 0 ? a * 8.0f : (__builtin_ldexpf(a, 1 - b) - 1.0f) * 8.0f;
+    const int code = min((b << 3) + (int)__builtin_rintf(steps), 31);  // rint: ties to even
+    return sign | (uint32_t)code;
+}
+
+// Scale code of a 32-block from its amax (quantize_to_mxfp6, preprocess.hpp:62-94).
+__device__ __forceinline__ int mx_scale_code(float amax) {
+    if (amax == 0.0f) return 127;
+    const float need = amax / 7.5f;
+    int e;
+    const float sig = __builtin_frexpf(need, &e);  // need = sig * 2^e, sig in [0.5, 1)
+    if (sig == 0.5f) e -= 1;                       // an exact power of two is its own scale
+    return min(max(e + 127, 0), 254);
+}
+
+// 1 / 2^(code - 127) for codes 0..253 (a normal float; code 254 needs amax > FLT_MAX).
+__device__ __forceinline__ float inv_scale(int code) {
+    return __uint_as_float((uint32_t)(254 - code) << 23);
+}
+
+// 32 codes -> 24 bytes (6 dwords): code i at bits 6i .. 6i+5 of the little-endian stream.
+__device__ __forceinline__ void pack32(const uint32_t (&c)[32], uint32_t (&w)[6]) {
+#pragma unroll
+    for (int d = 0; d < 6; d++) w[d] = 0;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const int lo = 6 * i, d = lo >> 5, sh = lo & 31;
+        w[d] |= c[i] << sh;
+        if (sh > 26) w[d + 1] |= c[i] >> (32 - sh);
+    }
+}
+
+// Quantise 32 values into 6 packed dwords; returns the scale code.
+__device__ __forceinline__ int quant32(const float (&v)[32], uint32_t (&w)[6]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    const int code = mx_scale_code(amax);
+    const float inv = inv_scale(code);
+    uint32_t c[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) c[i] = e2m3_code(v[i] * inv);
+    pack32(c, w);
+    return code;
+}
+
+// Byte offset of the tiled scale of (row r, 32-block c); see the file comment.
+__device__ __forceinline__ size_t tiled_scale_off(int r, int c, int group, int gp, int ktn) {
+    const int t = r >> 5, lane = (r & 31) + ((c & 1) << 5), q = c >> 1;
+    const int g = t / group, j = t - g * group, kt = q / 3, sub = q - kt * 3;
+    return ((((size_t)g * ktn + kt) * 64 + lane) * 3 + sub) * gp + j;
+}
+
+// Store one tiled scale byte; the last row block of a group also clears the dword's pad bytes.
+__device__ __forceinline__ void put_tiled_scale(uint8_t* tiled, int r, int c, int group, int ktn,
+                                                int code) {
+    const int gp = (group + 3) & ~3;
+    const size_t o = tiled_scale_off(r, c, group, gp, ktn);
+    tiled[o] = (uint8_t)code;
+    if (((r >> 5) % group) == group - 1)
+        for (int j = 1; j < gp - group + 1; j++) tiled[o + j] = 0;
+}
+
+constexpr int PREP_THREADS = 256;
+constexpr int PREP_BLKS_PER_WAVE = 64;
+
+// Scale output of prep_rows_kernel: raw [rows][ncols] or tiled (group, ktn) with ncols = Kp / 32.
+struct ScaleOut {
+    uint8_t* p;
+    int tiled;       // 0 raw, 1 tiled
+    int ncols;       // scale columns written per row (raw: also the row stride)
+    int group, ktn;  // tiled
+};
+
+// grid: rows * chunks workgroups, chunks = ceil(nblk / 256) (4 waves of 64 blocks) per row, row
+// major. Block c of row r (c < nblk) writes
+// the codes of values 32c .. 32c+31 (c < cols/32) or zero bytes, cut at row_bytes, and the scale
+// column c if c < so.ncols (127 beyond cols/32).
+__global__ void __launch_bounds__(PREP_THREADS)
+    prep_rows_kernel(const float* __restrict__ x, int cols, int nblk, uint8_t* __restrict__ packed,
+                     size_t row_bytes, ScaleOut so, int chunks) {
+    __shared__ float stage[PREP_THREADS / 64][PREP_BLKS_PER_WAVE * 33];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = (int)(blockIdx.x / chunks), chunk = (int)(blockIdx.x - (unsigned)r * chunks);
+    const int blk0 = (chunk * (PREP_THREADS / 64) + wave) * PREP_BLKS_PER_WAVE;
+    const int vblk = cols / 32;  // blocks holding values
+    const float* xr = x + (size_t)r * cols;
+    float* st = stage[wave];
+    // coalesced loads of the wave's 2048 values (float4 per lane per step), block-padded in LDS
+    if (blk0 < vblk) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int p = 4 * (lane + 64 * j);  // value index within the wave's range
+            const int b = p >> 5, i = p & 31;
+            v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (blk0 + b < vblk) v = *reinterpret_cast<const v4f*>(xr + (size_t)(blk0 + b) * 32 + i);
+            st[b * 33 + i] = v[0];
+            st[b * 33 + i + 1] = v[1];
+            st[b * 33 + i + 2] = v[2];
+            st[b * 33 + i + 3] = v[3];
+        }
+    }
+    __syncthreads();
+    const int c = blk0 + lane;
+    if (c >= nblk) return;
+    uint32_t w[6] = {0, 0, 0, 0, 0, 0};
+    int code = 127;
+    if (c < vblk) {
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = st[lane * 33 + i];
+        code = quant32(v, w);
+    }
+    // packed bytes [24c, 24c + 24) of the row, cut at row_bytes (row_bytes % 4 == 0)
+    const size_t o = (size_t)24 * c;
+    if (o < row_bytes) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(packed + (size_t)r * row_bytes + o);
+        const int nd = (int)min((size_t)6, (row_bytes - o) / 4);
+#pragma unroll
+        for (int d = 0; d < 6; d++)
+            if (d < nd) dst[d] = w[d];
+    }
+    if (c < so.ncols) {
+        if (so.tiled)
+            put_tiled_scale(so.p, r, c, so.group, so.ktn, code);
+        else
+            so.p[(size_t)r * so.ncols + c] = (uint8_t)code;
+    }
+}
+
+// grid: ceil(N / 64) * kchunks workgroups, kchunks = ceil(Kp/32 / 4): workgroup (nb, kc) = one
+// wave per 64 columns and 4 consecutive 32-blocks of K (one per wave), K-chunk major.
+__global__ void __launch_bounds__(PREP_THREADS)
+    prep_b_kernel(const float* __restrict__ B, int K, int N, int Kp, int group,
+                  uint8_t* __restrict__ bsh, uint8_t* __restrict__ tiled, int nchunks) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int kc = (int)(blockIdx.x / nchunks), nb = (int)(blockIdx.x - (unsigned)kc * nchunks);
+    const int n = nb * 64 + lane;
+    const int c = kc * (PREP_THREADS / 64) + wave;
+    if (c >= Kp / 32 || n >= N) return;
+    uint32_t w[6] = {0, 0, 0, 0, 0, 0};
+    int code = 127;
+    if (32 * c < K) {
+        float v[32];
+        const float* src = B + (size_t)32 * c * N + n;
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = src[(size_t)i * N];
+        code = quant32(v, w);
+    }
+    const int k64n = Kp / 64, t = (n & 31) + ((c & 1) << 5);
+    uint8_t* tile = bsh + ((size_t)(n >> 5) * k64n + (c >> 1)) * OPBLK_BYTES;
+    *reinterpret_cast<v4i*>(tile + 16 * t) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    *reinterpret_cast<v2i*>(tile + 1024 + 8 * t) = v2i{(int)w[4], (int)w[5]};
+    put_tiled_scale(tiled, n, c, group, Kp / 192, code);
+}
+
+// grid-stride over dim * Kp/32 (row-major over (r, c)).
+__global__ void __launch_bounds__(PREP_THREADS)
+    tile_scales_kernel(const uint8_t* __restrict__ s, int dim, int vblk, int ld, int Kp, int group,
+                       uint8_t* __restrict__ tiled) {
+    const int nb = Kp / 32;
+    const size_t total = (size_t)dim * nb;
+    for (size_t e = (size_t)blockIdx.x * PREP_THREADS + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * PREP_THREADS) {
+        const int r = (int)(e / nb), c = (int)(e - (size_t)r * nb);
+        const int code = c < vblk ? s[(size_t)r * ld + c] : 127;
+        put_tiled_scale(tiled, r, c, group, Kp / 192, code);
+    }
+}
+
+}  // namespace mxfp6_dev

@@ -52,6 +52,13 @@ SIGNATURES = {
     "mxfp6_gemm_repacks_a": (C.c_int, [C.c_int, C.c_int, C.c_int]),
     "mxfp6_plan_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "mxfp6_preshuffle_rows_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "mxfp6_quantize_async": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_size_t, _vp, C.c_int, _vp]),
+    "mxfp6_prepare_a_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp,
+                                        _vp]),
+    "mxfp6_prepare_b_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]),
+    "mxfp6_tile_scales_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "mxfp6_preshuffled_bytes": (C.c_size_t, [C.c_int, C.c_int]),
+    "mxfp6_tiled_scale_bytes": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     "mxfp6_gemm_direct": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp,
                                     _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp, C.c_size_t, _vp]),
     "mxfp6_fp6_e2m3_to_float": (C.c_float, [C.c_uint8]),
@@ -178,6 +185,36 @@ def plan_workspace_size(M, N, Kp, splits, a_repack):
 def preshuffle_rows(src, row_bytes, rows, Kp, dst, stream=None):
     """On-device preshuffle of row-major packed rows (device pointers), preshuffle_B's layout."""
     return lib().mxfp6_preshuffle_rows_async(src, row_bytes, rows, Kp, dst, stream)
+
+
+def quantize_dev(dx, rows, cols, dpacked, packed_row_bytes, dscales, scale_cols, stream=None):
+    """quantize_to_mxfp6 on the device (device pointers); returns the status."""
+    return lib().mxfp6_quantize_async(dx, rows, cols, dpacked, packed_row_bytes, dscales,
+                                      scale_cols, stream)
+
+
+def prepare_a_dev(dA, M, K, group, dpacked, a_row_bytes, dtiled, stream=None):
+    """float A[M][K] -> packed rows + tiled scales at kpad(K) on the device; returns the status."""
+    return lib().mxfp6_prepare_a_async(dA, M, K, group, dpacked, a_row_bytes, dtiled, stream)
+
+
+def prepare_b_dev(dB, K, N, group, dbsh, dtiled, stream=None):
+    """float B[K][N] -> preshuffled B^T + tiled scales at kpad(K) on the device; returns the
+    status."""
+    return lib().mxfp6_prepare_b_async(dB, K, N, group, dbsh, dtiled, stream)
+
+
+def tile_scales_dev(dscales, dim, K, ld, group, dtiled, stream=None):
+    """Raw scales [dim][ld] -> tiled at kpad(K) on the device; returns the status."""
+    return lib().mxfp6_tile_scales_async(dscales, dim, K, ld, group, dtiled, stream)
+
+
+def preshuffled_bytes(dim, K):
+    return lib().mxfp6_preshuffled_bytes(dim, K)
+
+
+def tiled_scale_bytes(dim, K, group):
+    return lib().mxfp6_tiled_scale_bytes(dim, K, group)
 
 
 def gemm_direct(out_type, M, N, Kp, mpw, npw, dA, dBsh, dsA, dsB, dD, A_row_bytes, splits=1,
