@@ -17,6 +17,7 @@ typedef int v6i_a8 __attribute__((__vector_size__(24), __aligned__(8)));
 // 12 bytes, 4-byte aligned (one ds_read_b96)
 typedef int v3i_a4 __attribute__((__vector_size__(12), __aligned__(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned v6u __attribute__((ext_vector_type(6)));
 
 // Bytes of one packed 64-element K slab of a row (64 codes * 6 bits).
 constexpr int SLAB_BYTES = 48;

@@ -90,13 +90,13 @@ extern "C" int mxfp6_hip_has_tile(int MT, int NT, int mpw, int npw) {
 extern "C" int mxfp6_hip_quantize_rows(const float* x, int rows, int cols, int nblk, void* packed,
                                        size_t row_bytes, uint8_t* scales, int scale_mode,
                                        int ncols, int group, int Kp, void* stream) {
-    const int per_wg = PREP_BLKS_PER_WAVE * (PREP_THREADS / 64);
-    const unsigned chunks = (unsigned)((nblk + per_wg - 1) / per_wg);
+    const int chunks = (nblk + PREP_BLKS_PER_WAVE - 1) / PREP_BLKS_PER_WAVE;
+    const size_t tasks = (size_t)rows * chunks, per_wg = PREP_THREADS / 64;
     const ScaleOut so{scales, scale_mode, ncols, group, Kp / 192};
-    prep_rows_kernel<<<dim3(chunks * (unsigned)rows), dim3(PREP_THREADS), 0,
+    prep_rows_kernel<<<dim3((unsigned)((tasks + per_wg - 1) / per_wg)), dim3(PREP_THREADS), 0,
                        static_cast<hipStream_t>(stream)>>>(x, cols, nblk,
                                                            static_cast<uint8_t*>(packed),
-                                                           row_bytes, so, (int)chunks);
+                                                           row_bytes, so, chunks, rows);
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

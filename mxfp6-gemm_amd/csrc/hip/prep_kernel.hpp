@@ -20,8 +20,8 @@
 // code = clamp(log2(scale) + 127, 0, 254). Every value is divided by the scale (here multiplied
 // by its reciprocal, a power of two in [2^-126, 2^127]: the same correctly rounded quotient) and
 // encoded by float_to_fp6_e2m3 (types.hpp:26-72): magnitude saturated at 7.5, round to nearest
-// E2M3 with ties to the even code, sign from x < 0 (so a negative value that rounds to zero keeps
-// code 0x20, and -0.0 gives 0x00).
+// E2M3 with ties to the even code, sign from q < 0 (so a negative quotient that rounds to zero
+// keeps code 0x20, and a zero quotient gives 0x00).
 //
 // Kernels (all HBM-bound; algorithmic bytes = 4 per value read + 0.75 per value and 1/32 per
 // scale written):
@@ -40,17 +40,6 @@
 
 namespace mxfp6_dev {
 
-// float_to_fp6_e2m3 (types.hpp:26-72) for a finite input.
-__device__ __forceinline__ uint32_t e2m3_code(float v) {
-    const uint32_t sign = v < 0.0f ? 0x20u : 0u;
-    const float a = fminf(fabsf(v), 7.5f);
-    // binade [0,1) -> 0 (step 1/8), [1,2) -> 1, [2,4) -> 2, [4,7.5] -> 3; offset in steps is exact
-    const int b = a < 1.0f ? 0 : a < 2.0f ? 1 : a < 4.0f ? 2 : 3;
-    const float steps = b == 0 ? a * 8.0f : (__builtin_ldexpf(a, 1 - b) - 1.0f) * 8.0f;
-    const int code = min((b << 3) + (int)__builtin_rintf(steps), 31);  // rint: ties to even
-    return sign | (uint32_t)code;
-}
-
 // Scale code of a 32-block from its amax (quantize_to_mxfp6, preprocess.hpp:62-94).
 __device__ __forceinline__ int mx_scale_code(float amax) {
     if (amax == 0.0f) return 127;
@@ -66,29 +55,35 @@ __device__ __forceinline__ float inv_scale(int code) {
     return __uint_as_float((uint32_t)(254 - code) << 23);
 }
 
-// 32 codes -> 24 bytes (6 dwords): code i at bits 6i .. 6i+5 of the little-endian stream.
-__device__ __forceinline__ void pack32(const uint32_t (&c)[32], uint32_t (&w)[6]) {
-#pragma unroll
-    for (int d = 0; d < 6; d++) w[d] = 0;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-        const int lo = 6 * i, d = lo >> 5, sh = lo & 31;
-        w[d] |= c[i] << sh;
-        if (sh > 26) w[d + 1] |= c[i] >> (32 - sh);
-    }
+// The quotient x / scale as the reference forms it, with -0.0 turned into +0.0: the reference
+// takes the sign from q < 0, so a zero quotient always encodes as code 0x00, while the hardware
+// conversion keeps the sign bit of -0.0. A nonzero quotient is unchanged by + 0.0, and the
+// product is not contracted into an FMA (which would keep the sign of an underflowing product).
+__device__ __forceinline__ float scaled_quotient(float x, float inv) {
+#pragma clang fp contract(off)
+    return x * inv + 0.0f;
 }
 
-// Quantise 32 values into 6 packed dwords; returns the scale code.
+// Quantise 32 values into 6 packed dwords (code i at bits 6i .. 6i+5, LSB-first); returns the
+// scale code. The E2M3 encoding is v_cvt_scalef32_2xpk16_fp6_f32 (scale 1.0) on the quotients:
+// round to nearest with ties to even, magnitude saturated at 7.5, the sign kept for a value that
+// rounds to zero -- float_to_fp6_e2m3 (types.hpp:26-72) exactly; the instruction interleaves its
+// two 16-value sources (output i comes from source i % 2, element i / 2).
 __device__ __forceinline__ int quant32(const float (&v)[32], uint32_t (&w)[6]) {
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
     const int code = mx_scale_code(amax);
     const float inv = inv_scale(code);
-    uint32_t c[32];
+    v16f even, odd;
 #pragma unroll
-    for (int i = 0; i < 32; i++) c[i] = e2m3_code(v[i] * inv);
-    pack32(c, w);
+    for (int i = 0; i < 16; i++) {
+        even[i] = scaled_quotient(v[2 * i], inv);
+        odd[i] = scaled_quotient(v[2 * i + 1], inv);
+    }
+    const v6u h = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(even, odd, 1.0f);
+#pragma unroll
+    for (int d = 0; d < 6; d++) w[d] = h[d];
     return code;
 }
 
@@ -120,22 +115,25 @@ struct ScaleOut {
     int group, ktn;  // tiled
 };
 
-// grid: rows * chunks workgroups, chunks = ceil(nblk / 256) (4 waves of 64 blocks) per row, row
-// major. Block c of row r (c < nblk) writes
+// Wave tasks: (row r, chunk) for chunk < chunks = ceil(nblk / 64), row-major, 4 per workgroup
+// (grid = ceil(rows * chunks / 4)); a task covers blocks 64 * chunk .. +63 of its row. Block c of
+// row r (c < nblk) writes
 // the codes of values 32c .. 32c+31 (c < cols/32) or zero bytes, cut at row_bytes, and the scale
 // column c if c < so.ncols (127 beyond cols/32).
 __global__ void __launch_bounds__(PREP_THREADS)
     prep_rows_kernel(const float* __restrict__ x, int cols, int nblk, uint8_t* __restrict__ packed,
-                     size_t row_bytes, ScaleOut so, int chunks) {
+                     size_t row_bytes, ScaleOut so, int chunks, int rows) {
     __shared__ float stage[PREP_THREADS / 64][PREP_BLKS_PER_WAVE * 33];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r = (int)(blockIdx.x / chunks), chunk = (int)(blockIdx.x - (unsigned)r * chunks);
-    const int blk0 = (chunk * (PREP_THREADS / 64) + wave) * PREP_BLKS_PER_WAVE;
+    const size_t task = (size_t)blockIdx.x * (PREP_THREADS / 64) + wave;
+    const int r = (int)(task / chunks), chunk = (int)(task - (size_t)r * chunks);
+    const bool live = r < rows;
+    const int blk0 = chunk * PREP_BLKS_PER_WAVE;
     const int vblk = cols / 32;  // blocks holding values
     const float* xr = x + (size_t)r * cols;
     float* st = stage[wave];
     // coalesced loads of the wave's 2048 values (float4 per lane per step), block-padded in LDS
-    if (blk0 < vblk) {
+    if (live && blk0 < vblk) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int p = 4 * (lane + 64 * j);  // value index within the wave's range
@@ -150,7 +148,7 @@ __global__ void __launch_bounds__(PREP_THREADS)
     }
     __syncthreads();
     const int c = blk0 + lane;
-    if (c >= nblk) return;
+    if (!live || c >= nblk) return;
     uint32_t w[6] = {0, 0, 0, 0, 0, 0};
     int code = 127;
     if (c < vblk) {
