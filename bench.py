@@ -7,6 +7,7 @@ over operands already resident in HBM. Default workload: M = N = K = 8192, FP16 
 drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX rule.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--all] [--no-cpu]
+  python bench.py --prep      (device operand preparation: float -> MXFP6 device layouts, GB/s)
 
 Prints one JSON line per workload (only the default one unless --all). Besides the contract
 fields it reports:
@@ -246,6 +247,73 @@ def run_config(name, steps, warmup, with_cpu):
     return out
 
 
+def run_prep(steps, warmup):
+    """Operand preparation on the device at the default workload's size: float A[8192][8192] ->
+    packed rows + tiled scales (prepare_a), float B[8192][8192] -> preshuffled B^T + tiled scales
+    (prepare_b), one step = both calls. Algorithmic bytes per value: 4 read, 0.75 + 1/32 written
+    (padded to kpad(K) = 8256)."""
+    import torch
+
+    M = N = K = 8192
+    Kp = mx.kpad(K)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(SEED)
+    A = torch.randn(M, K, device=dev, generator=g)
+    B = torch.randn(K, N, device=dev, generator=g)
+    rb = Kp // 4 * 3
+    pa = torch.empty(M * rb, dtype=torch.uint8, device=dev)
+    ta = torch.empty(mx.tiled_scale_bytes(M, K, 4), dtype=torch.uint8, device=dev)
+    pb = torch.empty(mx.preshuffled_bytes(N, K), dtype=torch.uint8, device=dev)
+    tb = torch.empty(mx.tiled_scale_bytes(N, K, 4), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    calls = {
+        "prep_rows_kernel": lambda: mx.prepare_a_dev(A.data_ptr(), M, K, 4, pa.data_ptr(), rb,
+                                                     ta.data_ptr(), sp),
+        "prep_b_kernel": lambda: mx.prepare_b_dev(B.data_ptr(), K, N, 4, pb.data_ptr(),
+                                                  tb.data_ptr(), sp),
+    }
+    for _ in range(warmup):
+        for c in calls.values():
+            assert c() == 0
+    torch.cuda.synchronize()
+    evs = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(steps)] for k in calls}
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        for k, c in calls.items():
+            evs[k][i][0].record(stream)
+            if c() != 0:
+                raise RuntimeError(f"{k} failed")
+            evs[k][i][1].record(stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    k_ms = {k: sum(a.elapsed_time(b) for a, b in v) / steps for k, v in evs.items()}
+    per_op = M * K * 4 + M * Kp * 3 // 4 + M * Kp // 32  # A and B have the same shape
+    gbs = 2 * per_op / (ms * 1e-3) / 1e9
+    dom = max(k_ms, key=k_ms.get)
+    achieved = per_op / (k_ms[dom] * 1e-3) / 1e9
+    workload = f"mxfp6_prepare_{M}x{K}"
+    log(f"[bench] prepare: {ms * 1e3:.1f} us/step; " +
+        ", ".join(f"{k} {v * 1e3:.1f} us ({per_op / (v * 1e-3) / 1e9:.0f} GB/s)"
+                  for k, v in k_ms.items()))
+    return {
+        "metric": "MXFP6 operand preparation (quantize + device layouts) GB/s, 1xMI355X",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 -> mxfp6_e2m3", "data": "synthetic",
+        "config": {"workload": workload, "A": [M, K], "B": [K, N], "Kp": Kp, "group": 4,
+                   "inputs": "N(0,1) float32", "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic(workload, dom), "kernel": dom,
+                     "kernel_ms": round(k_ms[dom], 6)},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -259,6 +327,8 @@ def main():
     ap.add_argument("--no-clock", action="store_true", help=argparse.SUPPRESS)  # accepted, no-op
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run the 256 MiB copy kernel that calibrates the HBM byte counters")
+    ap.add_argument("--prep", action="store_true",
+                    help="time the device operand preparation (quantize + layouts) instead")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on exactly one GPU; --gpus {a.gpus} is not supported (the MXFP6 "
@@ -267,6 +337,9 @@ def main():
         sys.exit(2)
     if a.copy_calibration:
         copy_calibration()
+        return
+    if a.prep:
+        print(json.dumps(run_prep(a.steps, a.warmup)), flush=True)
         return
     names = sorted(CONFIGS) if a.all else [a.config]
     for n in names:
