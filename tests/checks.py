@@ -66,3 +66,46 @@ def check(D, R, absdot, out_type):
     if out_type == 0:
         return check_f32(D, R, absdot)
     return check_lowp(D, R, "f16" if out_type == 1 else "bf16")
+
+
+# ---- whole-output checksums (full-size workloads) ------------------------------------------------
+
+# half an ulp of each output format relative to |D| (normal range), and its subnormal step
+HALF_ULP = {0: (0.0, 0.0), 1: (2.0 ** -11, 2.0 ** -24), 2: (2.0 ** -8, 2.0 ** -133)}
+
+
+def _gemv64(X32, v64, chunk=1024):
+    """X (float32 [R][K]) @ v (float64 [K]) in float64, a block of rows at a time."""
+    out = np.empty(X32.shape[0], dtype=np.float64)
+    for r in range(0, X32.shape[0], chunk):
+        out[r:r + chunk] = X32[r:r + chunk].astype(np.float64) @ v64
+    return out
+
+
+def check_checksums(col_sum, row_sum, col_abs, row_abs, total, Af, Bf, out_type):
+    """Row and column sums of D (float64 sums of the output values, and of their magnitudes)
+    against FP64 GEMVs of the exactly dequantised operands Af [M][K] and Bf = B^T [N][K]:
+    column sums = (1^T A) B, row sums = A (B 1), total = 1^T A B 1. Each row or column may differ
+    by the sum of its elements' bars: 1e-5 * sum|ab| for the FP32 accumulation, half an ulp of
+    the output format per element and the format's smallest subnormal step. Returns the largest
+    error / bound ratio over columns and rows."""
+    M, N = Af.shape[0], Bf.shape[0]
+    sA = Af.sum(axis=0, dtype=np.float64)
+    sB = Bf.sum(axis=0, dtype=np.float64)
+    col_pred = _gemv64(Bf, sA)
+    row_pred = _gemv64(Af, sB)
+    col_ab = _gemv64(np.abs(Bf), np.abs(Af).sum(axis=0, dtype=np.float64))
+    row_ab = _gemv64(np.abs(Af), np.abs(Bf).sum(axis=0, dtype=np.float64))
+    rel, sub = HALF_ULP[out_type]
+    col_bound = F32_RTOL * col_ab + rel * np.asarray(col_abs) + sub * M
+    row_bound = F32_RTOL * row_ab + rel * np.asarray(row_abs) + sub * N
+    col_err = np.abs(np.asarray(col_sum) - col_pred)
+    row_err = np.abs(np.asarray(row_sum) - row_pred)
+    assert (col_err <= col_bound).all(), (
+        f"{(col_err > col_bound).sum()} column sums off; worst column "
+        f"{int(np.argmax(col_err - col_bound))}")
+    assert (row_err <= row_bound).all(), (
+        f"{(row_err > row_bound).sum()} row sums off; worst row {int(np.argmax(row_err - row_bound))}")
+    tot_pred = float(sA @ sB)
+    assert abs(total - tot_pred) <= col_bound.sum(), f"total {total} vs {tot_pred}"
+    return float((col_err / col_bound).max()), float((row_err / row_bound).max())

@@ -121,3 +121,34 @@ def test_checks_catch_planted_mistakes(mx, orc):
     checks.check_lowp(b16, R, "bf16")
     with pytest.raises(AssertionError):
         checks.check_lowp(-b16 + 1e-3, R, "bf16")
+
+
+@pytest.mark.parametrize("out_type", [0, 1, 2])
+def test_checksums_catch_planted_mistakes(mx, orc, out_type):
+    """The whole-output checksums of the full-size GPU tests pass on the oracle's own D (rounded
+    to the output format) and fail on a zeroed 32x32 block, two swapped 128-column tiles, one
+    row scaled by 2 (a wrong scale), and a doubled K segment in one 32x32 block."""
+    M, N, K = 256, 384, 1024
+    p = mx.make_problem(M, N, K, seed=11 + out_type)
+    R, _ = orc.problem_f64(p)
+    r32 = R.astype(np.float32)
+    D = {0: r32, 1: r32.astype(np.float16).astype(np.float32),
+         2: checks.round_bf16(r32)}[out_type].astype(np.float64)
+    Af = orc.dequant_f32(p.a_packed, p.a_row_bytes, p.a_scales, M, K)
+    Bf = orc.dequant_f32(p.b_packed, p.b_row_bytes, p.b_scales, N, K)
+
+    def run(d):
+        return checks.check_checksums(d.sum(0), d.sum(1), np.abs(d).sum(0), np.abs(d).sum(1),
+                                      float(d.sum()), Af, Bf, out_type)
+
+    run(D)
+    half = orc.gemm_f64(p.a_packed, p.a_row_bytes, p.a_scales, p.b_packed, p.b_row_bytes,
+                        p.b_scales, M, N, K // 2)[0]
+    planted = []
+    z = D.copy(); z[64:96, 32:64] = 0; planted.append(z)                 # block never written
+    s = D.copy(); s[:, 0:128], s[:, 128:256] = D[:, 128:256], D[:, 0:128]; planted.append(s)
+    w = D.copy(); w[100] *= 2; planted.append(w)                          # wrong scale on a row
+    dk = D.copy(); dk[0:32, 0:32] += half[0:32, 0:32]; planted.append(dk)  # K half counted twice
+    for bad in planted:
+        with pytest.raises(AssertionError):
+            run(bad)
