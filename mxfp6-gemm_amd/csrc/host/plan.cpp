@@ -2,6 +2,7 @@
 // points (C++ API of include/mxfp6/gemm.hpp and the GEMM part of the C ABI in
 // include/mxfp6_gemm.h). Plain C++17 with no HIP header: every device action goes through the
 // thin launch layer declared in hip_layer.h.
+#include <algorithm>
 #include <cstdio>
 
 #include "../hip_layer.h"
@@ -14,98 +15,83 @@ namespace plan {
 
 // ---- router ------------------------------------------------------------------------------
 //
-// Candidate tiles (each an instantiation of the pipelined kernel, 4 waves per workgroup, one
-// workgroup per CU):
-//   256x256, waves 2x2, each wave 128x128 -> MPW 4, NPW 4   (work 4 units of 128x128)
-//   256x192, waves 2x2, each wave 128x96  -> MPW 4, NPW 3   (3 units)
-//   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3   (3 units)
-//   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4   (2 units)
-//   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (1 unit)
-// The kernel is bound by the per-CU global->LDS copy rate (64 B/clk per CU on MI355X), so the
-// tiles that move the fewest operand bytes per flop, 256x256 and 256x192, are preferred whenever
-// one divides the shape and its (split) grid has at least BIG_TILE_MIN_WG workgroups: measured on
-// MI355X they beat a smaller tile that fills every CU. Between the two, and otherwise among all
-// candidates that divide the shape, workgroup-starved grids are split along K (split_for) and the
-// cost of a candidate is the number of CU waves its (split) grid needs times the work of one
-// workgroup: ceil(wg * S / CUS) * units / S. The cheapest wins; ties go to the earlier (larger)
-// tile.
+// Candidate tiles (each an instantiation of the pipelined kernel, 4 waves per workgroup):
+//   256x256, waves 2x2, each wave 128x128 -> MPW 4, NPW 4   (16 MFMAs per wave per 64-wide slab)
+//   256x192, waves 2x2, each wave 128x96  -> MPW 4, NPW 3   (12)
+//   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3   (12)
+//   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4   (8)
+//   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (4; two workgroups fit a CU's LDS)
+// A plan is (tile, K segments S, A repacked or not); the router takes the plan with the least
+// predicted time. The time model (microseconds, MI355X) follows the kernel's structure:
+//   waves    = ceil(wg * S / (CUS * occupancy)) rounds of workgroups;
+//   t_slab   = max(T_SLAB_MIN, per_cu * (T_MFMA * mfmas + T_COPY_KB * copied KiB)) per 64-wide K
+//              slab: a latency floor (the ring keeps four slabs in flight), else the CU's MFMA and
+//              global->LDS copy work, shared by the workgroups resident on it; a row-major A slab
+//              costs A_ROWS_COST more per byte than a preshuffled one (a copy touches ~3 cache
+//              lines per 128 bytes instead of 1);
+//   t_wg     = T_WG + slabs * t_slab + T_OUT_KB * output KiB * per_cu;
+//   t        = T_LAUNCH + waves * t_wg, plus for a repack T_LAUNCH + its bytes (A read and written)
+//              at BYTES_PER_US, and for a split T_LAUNCH + the partials written and read back.
+// The constants are a least-squares fit (log time) to every plan of 46 shapes measured on one
+// MI355X (M, N from 128 to 8192, K from 1024 to 105728): the plan the model picks is within
+// 1.2% of the measured best on average, 11% at worst (the previous fixed rules were up to 2x
+// off on small-K grids), and it is the measured best on the five benchmark workloads.
 namespace {
-struct Cand {
+struct Plan {
     TileChoice tc;
-    int units;
+    int S;
+    bool repack;
 };
-const Cand kCands[] = {{{256, 256, 4, 4}, 4}, {{256, 192, 4, 3}, 3}, {{128, 384, 4, 3}, 3},
-                       {{128, 256, 2, 4}, 2}, {{128, 128, 2, 2}, 1}};
-constexpr int N_BIG = 2;  // kCands[0 .. N_BIG) are the big tiles
+const TileChoice kCands[] = {{256, 256, 4, 4}, {256, 192, 4, 3}, {128, 384, 4, 3},
+                             {128, 256, 2, 4}, {128, 128, 2, 2}};
 
-// K segments for a tile on (M, N, Kp), from a time model: a (split) grid of wg * S workgroups
-// takes ceil(wg * S / CUS) CU waves of t_tile / S each (t_tile: one workgroup over all of K at
-// CU_RATE), and every segment adds one FP32 write and read of an M x N partial at PARTIAL_BW.
-// S runs up to MAX_SPLITS with at least MIN_TILES_PER_SEG K-tiles per segment; a split must beat
-// S = 1 by SPLIT_MIN_GAIN. Measured at 2048x5120x105728 (160 workgroups of 256x256): S = 1, 3, 4,
-// 6, 8 take 792, 688, 746, 734, 763 us, and the model picks S = 3; 2048x1024x105728 gets S = 8.
-int split_for(const TileChoice& tc, int M, int N, int Kp) {
-    const long wg = (long)(M / tc.MT) * (N / tc.NT);
+double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repack) {
+    const long wg = (long)(M / tc.MT) * (N / tc.NT) * S;
+    const int occ = (tc.MT == 128 && tc.NT == 128) ? 2 : 1;  // workgroups per CU (LDS)
+    const long cap = (long)CUS * occ;
+    const long waves = (wg + cap - 1) / cap;
+    const double per_cu = std::max(1.0, (double)std::min(wg, cap) / CUS);
+    const int mfmas = (tc.MT / 64) * (tc.NT / 64);
+    const double slabs = (double)(Kp / 64) / S;
+    const double copy_kb =
+        (tc.MT * 48.0 * (repack ? 1.0 : 1.0 + A_ROWS_COST) + tc.NT / 32 * 1536.0) / 1024.0;
+    const double t_slab = std::max(T_SLAB_MIN, per_cu * (T_MFMA * mfmas + T_COPY_KB * copy_kb));
+    const double out_kb = tc.MT * tc.NT * (S > 1 ? 4.0 : 2.0) / 1024.0;
+    const double t_wg = T_WG + slabs * t_slab + T_OUT_KB * out_kb * per_cu;
+    double t = T_LAUNCH + (double)waves * t_wg;
+    if (repack) t += T_LAUNCH + 2.0 * M * (Kp / 4 * 3.0) / BYTES_PER_US;
+    if (S > 1) t += T_LAUNCH + (4.0 * S * M * N + 2.0 * M * N) / BYTES_PER_US;
+    return t;
+}
+
+bool shape_ok(int M, int N, int Kp) {
+    return M > 0 && N > 0 && Kp > 0 && M % 128 == 0 && N % 128 == 0 && Kp % K_TILE == 0;
+}
+
+// The least-time plan. Candidates are visited from the simplest (no split, no repack) and a
+// plan needs a PLAN_MIN_GAIN lead to displace an earlier one, so near-ties keep the plan with
+// fewer launches and less workspace. Shapes gemm() rejects get the trivial plan.
+Plan best_plan(int M, int N, int Kp) {
+    Plan best = {{128, 128, 2, 2}, 1, false};
+    if (!shape_ok(M, N, Kp)) return best;
+    double best_t = -1.0;
     const int k_tiles = Kp / K_TILE;
-    if (wg <= 0) return 1;
-    const double t_tile = (double)k_tiles * 2.0 * tc.MT * tc.NT * K_TILE / CU_RATE;
-    const double t_part = 2.0 * M * N * sizeof(float) / PARTIAL_BW;
-    const double base = (double)((wg + CUS - 1) / CUS) * t_tile;
-    int best = 1;
-    double best_cost = base * (1.0 - SPLIT_MIN_GAIN);
-    for (int S = 2; S <= MAX_SPLITS && k_tiles / S >= MIN_TILES_PER_SEG; S++) {
-        const double cost = (double)((wg * S + CUS - 1) / CUS) * t_tile / S + S * t_part;
-        if (cost < best_cost) {
-            best = S;
-            best_cost = cost;
-        }
-    }
+    for (int rp = 0; rp < 2; rp++)
+        for (int S = 1; S <= MAX_SPLITS && S <= k_tiles; S++)
+            for (const TileChoice& tc : kCands) {
+                if (M % tc.MT != 0 || N % tc.NT != 0) continue;
+                const double t = plan_time_us(tc, M, N, Kp, S, rp != 0);
+                if (best_t < 0 || t < best_t * (1.0 - PLAN_MIN_GAIN)) {
+                    best = {tc, S, rp != 0};
+                    best_t = t;
+                }
+            }
     return best;
 }
 }  // namespace
 
 TileChoice route(int M, int N, int Kp) {
-    TileChoice best = {128, 128, 2, 2};
-    double best_cost = -1;
-    // shapes gemm() rejects (M, N multiples of 128, Kp of K_TILE) get the smallest tile, no split
-    if (M <= 0 || N <= 0 || Kp <= 0 || M % 128 != 0 || N % 128 != 0 || Kp % K_TILE != 0)
-        return best;
-    auto cost_of = [&](const Cand& c) {
-        const long wg = (long)(M / c.tc.MT) * (N / c.tc.NT);
-        const int S = split_for(c.tc, M, N, Kp);
-        return (double)((wg * S + CUS - 1) / CUS) * c.units / S;
-    };
-    for (int i = 0; i < N_BIG; i++) {
-        const Cand& c = kCands[i];
-        if (M % c.tc.MT != 0 || N % c.tc.NT != 0) continue;
-        if ((long)(M / c.tc.MT) * (N / c.tc.NT) * split_for(c.tc, M, N, Kp) < BIG_TILE_MIN_WG)
-            continue;
-        const double cost = cost_of(c);
-        if (best_cost < 0 || cost < best_cost - 1e-9) {
-            best = c.tc;
-            best_cost = cost;
-        }
-    }
-    if (best_cost >= 0) return best;
-    for (const Cand& c : kCands) {
-        if (M % c.tc.MT != 0 || N % c.tc.NT != 0) continue;
-        const double cost = cost_of(c);
-        if (best_cost < 0 || cost < best_cost - 1e-9) {
-            best = c.tc;
-            best_cost = cost;
-        }
-    }
-    return best;
-}
-
-// Whether A is first repacked into the preshuffled operand layout (an HBM-bound pass over A).
-// A row-major A costs the tile kernel's copies one 128-byte cache line per 48 useful bytes of a
-// row and slab; repacked, every copy is a contiguous 1 KiB. The pass pays when the kernel re-reads
-// each A row band many times, i.e. when the output has many tile columns.
-bool repack_for(const TileChoice& tc, int M, int N, int Kp) {
-    (void)M;
-    (void)Kp;
-    return N / tc.NT >= REPACK_MIN_TILE_COLS;
+    return best_plan(M, N, Kp).tc;
 }
 
 size_t split_bytes(int M, int N, int S) {
@@ -122,18 +108,11 @@ size_t plan_bytes(int M, int N, int Kp, int S, bool repack) {
 }
 
 bool route_repacks(int M, int N, int Kp) {
-    if (M <= 0 || N <= 0 || Kp <= 0 || M % 128 != 0 || N % 128 != 0 || Kp % K_TILE != 0)
-        return false;
-    const TileChoice tc = route(M, N, Kp);
-    if (M % tc.MT != 0 || N % tc.NT != 0) return false;
-    return repack_for(tc, M, N, Kp);
+    return shape_ok(M, N, Kp) && best_plan(M, N, Kp).repack;
 }
 
 int splitk_segments(int M, int N, int Kp) {
-    if (M <= 0 || N <= 0 || Kp <= 0 || M % 128 != 0 || N % 128 != 0 || Kp % K_TILE != 0) return 1;
-    const TileChoice tc = route(M, N, Kp);
-    if (M % tc.MT != 0 || N % tc.NT != 0) return 1;
-    return split_for(tc, M, N, Kp);
+    return shape_ok(M, N, Kp) ? best_plan(M, N, Kp).S : 1;
 }
 
 size_t workspace_bytes(int M, int N, int Kp) {
@@ -215,10 +194,11 @@ int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void*
                  size_t ws_bytes, void* stream) {
     const int st = check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
     if (st != MXFP6_OK) return st;
-    const TileChoice tc = route(M, N, Kp);
+    const Plan pl = best_plan(M, N, Kp);
+    const TileChoice tc = pl.tc;
     if (N % tc.NT != 0 || M % tc.MT != 0) return MXFP6_ERR_TILE;
-    int S = split_for(tc, M, N, Kp);
-    bool rp = repack_for(tc, M, N, Kp);
+    int S = pl.S;
+    bool rp = pl.repack;
     const int kernel = kernel_for(tc);
     if (kernel != MXFP6_KERNEL_TILE) rp = false;
     if (ws == nullptr) ws_bytes = 0;

@@ -10,18 +10,17 @@ namespace plan {
 
 // MI355X: 256 compute units (8 XCDs x 32 CUs).
 constexpr int CUS = 256;
-// Split-K model (see split_for): shortest segment in K-tiles of 192, most segments, the dense
-// MXFP6 rate of one CU under full load (MI355X at its power limit: ~3.35 PF / 256 CUs), the
-// bandwidth of the partials' round trip, and the least gain a split must promise.
-constexpr int MIN_TILES_PER_SEG = 8;
-constexpr int MAX_SPLITS = 16;
-constexpr double CU_RATE = 13e12;
-constexpr double PARTIAL_BW = 5e12;
-constexpr double SPLIT_MIN_GAIN = 0.05;
-// Smallest (split) grid for which the 256x256 tile is taken without comparing costs.
-constexpr long BIG_TILE_MIN_WG = 64;
-// Tile columns (N / NT) from which A is repacked to the preshuffled layout first.
-constexpr int REPACK_MIN_TILE_COLS = 8;
+// Plan-time model of the router (plan.cpp): least-squares fit on MI355X, microseconds.
+constexpr int MAX_SPLITS = 16;             // K segments considered
+constexpr double T_LAUNCH = 3.737;         // one kernel launch (and its ramp), back to back
+constexpr double T_WG = 0.394;             // fixed cost of one workgroup
+constexpr double T_SLAB_MIN = 0.2447;      // latency floor of one 64-wide K slab
+constexpr double T_MFMA = 0.010511;        // per MFMA per wave per slab, per resident workgroup
+constexpr double T_COPY_KB = 0.01375;      // per KiB copied global->LDS per slab, per workgroup
+constexpr double T_OUT_KB = 0.010544;      // per KiB of output (FP16 tile or FP32 partial) per workgroup
+constexpr double BYTES_PER_US = 3.873e6;   // repack and split-K partial traffic
+constexpr double A_ROWS_COST = 0.76725;    // extra copy cost per byte of a row-major A slab
+constexpr double PLAN_MIN_GAIN = 0.01;     // lead a more complex plan needs over a simpler one
 
 TileChoice route(int M, int N, int Kp);
 int splitk_segments(int M, int N, int Kp);

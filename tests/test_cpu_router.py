@@ -77,7 +77,7 @@ def test_workspace_matches_split(mx):
                 assert ws == want, (M, N, K, S, rp, ws)
                 assert mx.plan_workspace_size(M, N, Kp, S, rp) == want
                 if S > 1:
-                    assert Kp // 192 // S >= 8 and S <= 16  # every segment >= 8 K-tiles
+                    assert Kp // 192 >= S and S <= 16  # every segment holds >= 1 K-tile
 
 
 def test_router_degenerate_shapes_do_not_trap(mx):
@@ -87,10 +87,8 @@ def test_router_degenerate_shapes_do_not_trap(mx):
 
 
 def test_router_benchmark_shapes(mx):
-    # the MI355X routing of the five benchmark workloads (256x256 or 256x192 whenever the grid has
-    # >= 64 workgroups, else cost: CU waves x workgroup work, ties to the larger tile). Split counts
-    # follow the CU-wave time model: 160 workgroups over 551 K-tiles take 3 segments (480
-    # workgroups, two waves of a third of K each: 2/3 of the unsplit time), 32 workgroups take 8.
+    # The plan-time model's picks for the five benchmark workloads; each is the fastest of all
+    # plans (tile x 1..16 segments x A layout) measured on MI355X for that shape.
     want = {
         (256, 256, 1024): ((128, 128, 2, 2), 1),
         (8192, 8192, 8192): ((256, 256, 4, 4), 1),
@@ -102,8 +100,27 @@ def test_router_benchmark_shapes(mx):
         t = mx.choose_tile(M, N, _kpad(K))
         S = mx.splitk_segments(M, N, _kpad(K))
         assert (tuple(t), S) == exp, (M, N, K, t, S)
-    # A is repacked where the output has >= 8 tile columns
+    # A is repacked where the kernel is long enough to amortise the extra pass and launch
     for (M, N, K), rp in {(8192, 8192, 8192): True, (2048, 6144, 16128): True,
                           (2048, 1024, 105728): False, (2048, 5120, 105728): True,
                           (256, 256, 1024): False}.items():
         assert mx.repacks_a(M, N, _kpad(K)) == rp, (M, N, K)
+
+
+def test_router_small_k_plans(mx):
+    """Shapes whose measured best plan (MI355X, every tile x split x A layout) differs from the
+    large-K habit of 256x256 tiles with a repacked A: short K favours more, smaller workgroups
+    and no extra launch for the repack; the router's model reproduces the measured winners."""
+    want = {  # (M, N, K): (tile, S, repack) measured fastest
+        (2048, 2048, 2048): ((128, 128, 2, 2), 1, False),   # 14.5 us vs 29.2 for 256x256 + repack
+        (2048, 1024, 1024): ((128, 128, 2, 2), 1, False),   # 9.1 us vs 14.1 with a repack
+        (4096, 4096, 1024): ((256, 256, 4, 4), 1, False),   # 22.9 us vs 27.7 with a repack
+        (2048, 4096, 1024): ((128, 256, 2, 4), 1, False),   # 14.3 us vs 24.6 for 256x256
+        (512, 1024, 16384): ((128, 128, 2, 2), 8, False),   # 21.8 us: 64 workgroups x 8 segments
+        (8192, 8192, 2048): ((256, 256, 4, 4), 1, True),    # 114.4 us vs 120.4 unrepacked
+    }
+    for (M, N, K), (tile, S, rp) in want.items():
+        Kp = _kpad(K)
+        got = (tuple(mx.choose_tile(M, N, Kp)), mx.splitk_segments(M, N, Kp),
+               mx.repacks_a(M, N, Kp))
+        assert got == (tile, S, rp), (M, N, K, got)
