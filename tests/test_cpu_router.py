@@ -124,3 +124,28 @@ def test_router_small_k_plans(mx):
         got = (tuple(mx.choose_tile(M, N, Kp)), mx.splitk_segments(M, N, Kp),
                mx.repacks_a(M, N, Kp))
         assert got == (tile, S, rp), (M, N, K, got)
+
+
+def test_router_equals_the_tuning_model(mx):
+    """The Python model in mxfp6-gemm_amd/tune (the one the constants are fitted with) and the
+    library's router make the same choice on every shape of the recorded plan measurements and
+    on a grid of other shapes; and with the committed constants its picks are within 2% of the
+    measured best on average."""
+    import math
+    import os
+    import sys
+    tune = os.path.join(os.path.dirname(mx.LIB_PATH), "..", "tune")
+    sys.path.insert(0, tune)
+    import plan_model as pm
+    recs = pm.load([os.path.join(tune, "plans_mi355x.jsonl")])
+    shapes = [tuple(r["shape"]) for r in recs]
+    shapes += [(M, N, K) for M in (128, 512, 2048, 8192) for N in (128, 768, 3072, 12288)
+               for K in (192, 2048, 30000, 105728)]
+    for M, N, K in shapes:
+        Kp = _kpad(K)
+        tile, S, rp = pm.best_plan(pm.CONSTANTS, M, N, Kp)
+        got = (tuple(mx.choose_tile(M, N, Kp)), mx.splitk_segments(M, N, Kp), mx.repacks_a(M, N, Kp))
+        assert got == (tile, S, rp), (M, N, K, got, (tile, S, rp))
+    ev = pm.evaluate(pm.CONSTANTS, recs)
+    gm = math.exp(sum(math.log(g) for _, g in ev) / len(ev))
+    assert len(ev) >= 40 and gm < 1.02, (len(ev), gm)
