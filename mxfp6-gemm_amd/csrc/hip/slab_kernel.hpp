@@ -64,17 +64,20 @@ struct SlabGeom {
     static constexpr int MPW = MT / 32 / WM, NPW = NT / 32 / WN;
     static constexpr int NWAVES = WM * WN, THREADS = 64 * NWAVES;
     static constexpr int A_BYTES = MT * SLAB_BYTES;           // A rows of one slab
+    // the stage's A area rounded up to whole 1 KiB wave copies (a 32-row tile has 1.5 KiB; the
+    // last wave's extra chunks land in the padding)
+    static constexpr int A_STAGE = (A_BYTES + 1023) / 1024 * 1024;
     static constexpr int B_BYTES = NT / 32 * OPBLK_BYTES;      // B blocks of one slab
     static constexpr int SC_GROUPS = WM + WN;                  // scale groups of the workgroup
     static constexpr int SC_BYTES = SC_GROUPS * 256;           // one dword per lane per group
-    static constexpr int STAGE = A_BYTES + B_BYTES + SC_BYTES;
+    static constexpr int STAGE = A_STAGE + B_BYTES + SC_BYTES;
     static constexpr int A_CHUNKS = A_BYTES / 16, B_CHUNKS = B_BYTES / 16;
-    static constexpr int A_ISS = (A_CHUNKS + THREADS - 1) / THREADS;
+    static constexpr int A_ISS = (A_STAGE / 16 + THREADS - 1) / THREADS;
     static constexpr int B_ISS = (B_CHUNKS + THREADS - 1) / THREADS;
     static constexpr int SC_ISS = (SC_GROUPS + NWAVES - 1) / NWAVES;
     static constexpr int D = A_ISS + B_ISS + SC_ISS;           // copy instructions per wave per slab
     static constexpr int LDS = NS * STAGE + 1024;              // + dummy sink
-    static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole-wave chunks");
+    static_assert(B_BYTES % 1024 == 0, "whole-wave chunks");
     static_assert(STAGE % 16 == 0, "16-byte aligned stages");
     static_assert(NS >= 4 && (NS - 2) * D <= 63, "vmcnt range");
 };
@@ -139,7 +142,7 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
     }
     const uint32_t lds0 = lds_u32(lds);
     const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds0 + wave * 1024);
-    const uint32_t lds_sc_wave = __builtin_amdgcn_readfirstlane(lds0 + G::A_BYTES + G::B_BYTES + wave * 256);
+    const uint32_t lds_sc_wave = __builtin_amdgcn_readfirstlane(lds0 + G::A_STAGE + G::B_BYTES + wave * 256);
     const uint32_t lds_dummy = __builtin_amdgcn_readfirstlane(lds0 + NS * STAGE);
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
@@ -147,13 +150,13 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
     auto dma_op = [&](int j, int q, int st) {
         const uint32_t so = st * STAGE;
         if (j < G::A_ISS) {
-            const bool live = G::A_CHUNKS % THREADS == 0 || j * THREADS + wave_u * 64 < G::A_CHUNKS;
+            const bool live = (G::A_STAGE / 16) % THREADS == 0 || j * THREADS + wave_u * 64 < G::A_STAGE / 16;
             dma16(live ? lds_wave + so + j * THREADS * 16 : lds_dummy,
                   a_base + (size_t)q * (ASH ? OPBLK_BYTES : SLAB_BYTES), a_voff[j]);
         } else if (j < G::A_ISS + G::B_ISS) {
             const int i = j - G::A_ISS;
             const bool live = G::B_CHUNKS % THREADS == 0 || i * THREADS + wave_u * 64 < G::B_CHUNKS;
-            dma16(live ? lds_wave + so + G::A_BYTES + i * THREADS * 16 : lds_dummy,
+            dma16(live ? lds_wave + so + G::A_STAGE + i * THREADS * 16 : lds_dummy,
                   b_base + (size_t)q * OPBLK_BYTES, b_voff[i]);
         } else {
             const int i = j - G::A_ISS - G::B_ISS;
@@ -169,9 +172,9 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
     const lds_cptr lds3 = (lds_cptr)lds;
     const int a_off = ASH ? wm * MPW * OPBLK_BYTES + lane * 16
                           : (wm * MPW * 32 + (lane & 31)) * SLAB_BYTES + (lane >> 5) * 24;
-    const int b_off = G::A_BYTES + wn * NPW * OPBLK_BYTES + lane * 16;
-    const int sa_off = G::A_BYTES + G::B_BYTES + wm * 256 + lane * 4;
-    const int sb_off = G::A_BYTES + G::B_BYTES + (WM + wn) * 256 + lane * 4;
+    const int b_off = G::A_STAGE + wn * NPW * OPBLK_BYTES + lane * 16;
+    const int sa_off = G::A_STAGE + G::B_BYTES + wm * 256 + lane * 4;
+    const int sb_off = G::A_STAGE + G::B_BYTES + (WM + wn) * 256 + lane * 4;
     struct Slab {
         v8i a[MPW], b[NPW];
         int sa, sb;
@@ -344,7 +347,11 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
 // (MT, NT, MPW, NPW) -> wave grid: the scale grouping fixes how many 32-blocks one wave holds,
 // so it also selects between the 4-wave and 8-wave instantiation of a tile.
 inline bool tile_supported(int MT, int NT, int mpw, int npw) {
-    return (MT == 128 && NT == 128 && mpw == 2 && npw == 2) ||
+    return (MT == 32 && NT == 128 && mpw == 1 && npw == 1) ||
+           (MT == 32 && NT == 256 && mpw == 1 && npw == 2) ||
+           (MT == 64 && NT == 128 && mpw == 2 && npw == 1) ||
+           (MT == 64 && NT == 256 && mpw == 2 && npw == 2) ||
+           (MT == 128 && NT == 128 && mpw == 2 && npw == 2) ||
            (MT == 128 && NT == 256 && mpw == 2 && npw == 4) ||
            (MT == 128 && NT == 384 && mpw == 4 && npw == 3) ||
            (MT == 256 && NT == 256 && mpw == 4 && npw == 4) ||
@@ -387,6 +394,11 @@ int slab_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
 template <typename OutT>
 int slab_launch(const mxfp6_launch_desc* d, hipStream_t st) {
     if (!tile_supported(d->MT, d->NT, d->mpw, d->npw)) return 1;
+    // skinny tiles (M not a multiple of 128): one wave row, four wave columns, a deeper ring
+    if (d->MT == 32 && d->NT == 128) return slab_launch_t<32, 128, 1, 4, 4, 8, OutT>(d, st);
+    if (d->MT == 32 && d->NT == 256) return slab_launch_t<32, 256, 1, 4, 4, 8, OutT>(d, st);
+    if (d->MT == 64 && d->NT == 128) return slab_launch_t<64, 128, 1, 4, 4, 8, OutT>(d, st);
+    if (d->MT == 64 && d->NT == 256) return slab_launch_t<64, 256, 1, 4, 4, 8, OutT>(d, st);
     if (d->MT == 128 && d->NT == 128) return slab_launch_t<128, 128, 2, 2, 4, 6, OutT>(d, st);
     if (d->MT == 128 && d->NT == 256) return slab_launch_t<128, 256, 2, 2, 4, 8, OutT>(d, st);
     if (d->MT == 128 && d->NT == 384) return slab_launch_t<128, 384, 1, 4, 4, 6, OutT>(d, st);

@@ -21,6 +21,8 @@ namespace plan {
 //   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3   (12)
 //   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4   (8)
 //   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (4; two workgroups fit a CU's LDS)
+// and, for M not a multiple of 128 (M a multiple of 32), the skinny tiles (waves 1x4):
+//   64x256 (MPW 2, NPW 2), 32x256 (1, 2), 64x128 (2, 1), 32x128 (1, 1; two per CU)
 // A plan is (tile, K segments S, A repacked or not); the router takes the plan with the least
 // predicted time. The time model (microseconds, MI355X) follows the kernel's structure:
 //   waves    = ceil(wg * S / (CUS * occupancy)) rounds of workgroups;
@@ -44,14 +46,15 @@ struct Plan {
 };
 const TileChoice kCands[] = {{256, 256, 4, 4}, {256, 192, 4, 3}, {128, 384, 4, 3},
                              {128, 256, 2, 4}, {128, 128, 2, 2}};
+const TileChoice kSkinny[] = {{64, 256, 2, 2}, {32, 256, 1, 2}, {64, 128, 2, 1}, {32, 128, 1, 1}};
 
 double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repack) {
     const long wg = (long)(M / tc.MT) * (N / tc.NT) * S;
-    const int occ = (tc.MT == 128 && tc.NT == 128) ? 2 : 1;  // workgroups per CU (LDS)
+    const int occ = (tc.NT == 128 && (tc.MT == 128 || tc.MT == 32)) ? 2 : 1;  // per CU (LDS)
     const long cap = (long)CUS * occ;
     const long waves = (wg + cap - 1) / cap;
     const double per_cu = std::max(1.0, (double)std::min(wg, cap) / CUS);
-    const int mfmas = (tc.MT / 64) * (tc.NT / 64);
+    const int mfmas = tc.MPW * tc.NPW;  // per wave per slab
     const double slabs = (double)(Kp / 64) / S;
     const double copy_kb =
         (tc.MT * 48.0 * (repack ? 1.0 : 1.0 + A_ROWS_COST) + tc.NT / 32 * 1536.0) / 1024.0;
@@ -65,7 +68,7 @@ double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repa
 }
 
 bool shape_ok(int M, int N, int Kp) {
-    return M > 0 && N > 0 && Kp > 0 && M % 128 == 0 && N % 128 == 0 && Kp % K_TILE == 0;
+    return M > 0 && N > 0 && Kp > 0 && M % 32 == 0 && N % 128 == 0 && Kp % K_TILE == 0;
 }
 
 // The least-time plan. Candidates are visited from the simplest (no split, no repack) and a
@@ -76,9 +79,14 @@ Plan best_plan(int M, int N, int Kp) {
     if (!shape_ok(M, N, Kp)) return best;
     double best_t = -1.0;
     const int k_tiles = Kp / K_TILE;
+    const bool skinny = M % 128 != 0;
+    const TileChoice* cands = skinny ? kSkinny : kCands;
+    const int n_cands = skinny ? (int)(sizeof(kSkinny) / sizeof(kSkinny[0]))
+                               : (int)(sizeof(kCands) / sizeof(kCands[0]));
     for (int rp = 0; rp < 2; rp++)
         for (int S = 1; S <= MAX_SPLITS && S <= k_tiles; S++)
-            for (const TileChoice& tc : kCands) {
+            for (int ci = 0; ci < n_cands; ci++) {
+                const TileChoice& tc = cands[ci];
                 if (M % tc.MT != 0 || N % tc.NT != 0) continue;
                 const double t = plan_time_us(tc, M, N, Kp, S, rp != 0);
                 if (best_t < 0 || t < best_t * (1.0 - PLAN_MIN_GAIN)) {
@@ -127,7 +135,7 @@ int check_common(int out_type, int M, int N, int Kp, const void* dA, const void*
                  const void* dsA, const void* dsB, const void* dD, int A_row_bytes) {
     if (out_type < 0 || out_type > 2) return MXFP6_ERR_OUT_TYPE;
     if (!dA || !dBsh || !dsA || !dsB || !dD) return MXFP6_ERR_NULL;
-    if (M <= 0 || N <= 0 || M % 128 != 0 || N % 128 != 0) return MXFP6_ERR_SHAPE;
+    if (M <= 0 || N <= 0 || M % 32 != 0 || N % 128 != 0) return MXFP6_ERR_SHAPE;
     if (Kp <= 0 || Kp % K_TILE != 0) return MXFP6_ERR_SHAPE;
     // A rows are read for packed(Kp) bytes from row * A_row_bytes; a compact row (packed(K),
     // K > Kp - K_TILE) is at most packed(K_TILE - 32) = 120 bytes shorter than packed(Kp).
@@ -141,7 +149,7 @@ const char* status_text(int st) {
     switch (st) {
         case MXFP6_OK: return "ok";
         case MXFP6_ERR_NULL: return "null pointer argument";
-        case MXFP6_ERR_SHAPE: return "unsupported shape (M, N multiples of 128; Kp multiple of 192; A_row_bytes)";
+        case MXFP6_ERR_SHAPE: return "unsupported shape (M multiple of 32, N of 128; Kp multiple of 192; A_row_bytes)";
         case MXFP6_ERR_OUT_TYPE: return "out_type must be F32, F16 or BF16";
         case MXFP6_ERR_TILE: return "tile not implemented or does not divide the shape";
         case MXFP6_ERR_ARG: return "invalid argument";
@@ -201,6 +209,7 @@ int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void*
     bool rp = pl.repack;
     const int kernel = kernel_for(tc);
     if (kernel != MXFP6_KERNEL_TILE) rp = false;
+    if (kernel != MXFP6_KERNEL_TILE && M % 64 != 0) return MXFP6_ERR_TILE;
     if (ws == nullptr) ws_bytes = 0;
     // A workspace too small for the repacked A drops the repack (a pure speed choice); one too
     // small for the split-K partials as well runs unsplit, with the reference's warning.
@@ -344,6 +353,7 @@ extern "C" int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, in
                                  void* ws, size_t ws_bytes, void* stream) {
     const int st = plan::check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
     if (st != MXFP6_OK) return st;
+    if (M % 64 != 0) return MXFP6_ERR_SHAPE;  // the direct kernel's workgroups are 64x64
     if (mpw < 1 || mpw > 4 || npw < 1 || npw > 4 || (M / 32) % mpw != 0 || (N / 32) % npw != 0)
         return MXFP6_ERR_ARG;
     if (splits < 1 || splits > Kp / K_TILE) return MXFP6_ERR_ARG;

@@ -17,6 +17,7 @@ CUS = 256
 K_TILE = 192
 MAX_SPLITS = 16
 TILES = [(256, 256, 4, 4), (256, 192, 4, 3), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2)]
+SKINNY = [(64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)]  # M % 128 != 0
 NAMES = ["T_LAUNCH", "T_WG", "T_SLAB_MIN", "T_MFMA", "T_COPY_KB", "T_OUT_KB", "BYTES_PER_US",
          "A_ROWS_COST"]
 CONSTANTS = {"T_LAUNCH": 3.737, "T_WG": 0.394, "T_SLAB_MIN": 0.2447, "T_MFMA": 0.010511,
@@ -28,11 +29,11 @@ PLAN_MIN_GAIN = 0.01
 def plan_time_us(c, tile, M, N, Kp, S, repack):
     MT, NT = tile[0], tile[1]
     wg = (M // MT) * (N // NT) * S
-    occ = 2 if (MT, NT) == (128, 128) else 1
+    occ = 2 if (MT, NT) in ((128, 128), (32, 128)) else 1
     cap = CUS * occ
     waves = (wg + cap - 1) // cap
     per_cu = max(1.0, min(wg, cap) / CUS)
-    mfmas = (MT // 64) * (NT // 64)
+    mfmas = tile[2] * tile[3]
     slabs = (Kp // 64) / S
     copy_kb = (MT * 48.0 * (1.0 if repack else 1.0 + c["A_ROWS_COST"]) + NT // 32 * 1536.0) / 1024.0
     t_slab = max(c["T_SLAB_MIN"], per_cu * (c["T_MFMA"] * mfmas + c["T_COPY_KB"] * copy_kb))
@@ -53,7 +54,7 @@ def best_plan(c, M, N, Kp):
     kt = Kp // K_TILE
     for rp in (False, True):
         for S in range(1, min(MAX_SPLITS, kt) + 1):
-            for tile in TILES:
+            for tile in (SKINNY if M % 128 else TILES):
                 if M % tile[0] or N % tile[1]:
                     continue
                 t = plan_time_us(c, tile, M, N, Kp, S, rp)
@@ -106,14 +107,19 @@ def evaluate(c, recs):
 def main():
     paths = sys.argv[1:] or [os.path.join(HERE, "plans_mi355x.jsonl")]
     recs = load(paths)
-    c, l = fit(recs, CONSTANTS)
-    print("fitted constants (log-time loss %.3f over %d shapes):" % (l, len(recs)))
+    # the constants are fitted on the shapes with M % 128 == 0 (the skinny tiles reuse them)
+    fit_recs = [r for r in recs if r["shape"][0] % 128 == 0]
+    c, l = fit(fit_recs, CONSTANTS)
+    print("fitted constants (log-time loss %.3f over %d shapes):" % (l, len(fit_recs)))
     for n in NAMES:
         print(f"  {n:14s} {c[n]:.6g}")
-    ev = evaluate(c, recs)
-    gm = math.exp(sum(math.log(g) for _, g in ev) / len(ev))
-    print(f"picks measured for {len(ev)} shapes: geomean {gm:.3f}x of the best, worst "
-          f"{max(g for _, g in ev):.3f}x")
+    for label, sel in (("M % 128 == 0", lambda s: s[0] % 128 == 0),
+                       ("skinny M", lambda s: s[0] % 128 != 0)):
+        ev = [(s, g) for s, g in evaluate(c, recs) if sel(s)]
+        if ev:
+            gm = math.exp(sum(math.log(g) for _, g in ev) / len(ev))
+            print(f"{label}: picks measured for {len(ev)} shapes: geomean {gm:.3f}x of the best, "
+                  f"worst {max(g for _, g in ev):.3f}x")
 
 
 if __name__ == "__main__":

@@ -17,7 +17,7 @@ import torch  # noqa: E402
 
 import mxfp6_amd as mx  # noqa: E402
 
-TILES = [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3), (256, 256, 4, 4), (256, 192, 4, 3)]
+TILES = [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3), (256, 256, 4, 4), (256, 192, 4, 3), (64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)]
 SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
 
 
@@ -44,7 +44,8 @@ def sweep(M, N, K):
     D = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
     res = []
     for t in TILES:
-        if M % t[0] or N % t[1]:
+        # the router offers the skinny tiles (fewer than 128 rows) exactly when M % 128 != 0
+        if M % t[0] or N % t[1] or (t[0] < 128) != (M % 128 != 0):
             continue
         bsh, sa, sb = p.layouts(t)
         dB, dsa, dsb = (torch.from_numpy(x).cuda() for x in (bsh, sa, sb))

@@ -86,6 +86,39 @@ def test_pipelined_split_bitwise_equals_direct_split(g):
     assert np.array_equal(Dr.view(np.uint32), Dd.view(np.uint32))
 
 
+# ---- M not a multiple of 128: the skinny tiles ------------------------------------------------
+
+SKINNY = [(32, 128, 1, 1), (32, 256, 1, 2), (64, 128, 2, 1), (64, 256, 2, 2)]
+
+
+@pytest.mark.parametrize("out_type", [0, 1, 2])
+@pytest.mark.parametrize("M,N,K", [(32, 128, 192), (64, 256, 1024), (96, 384, 960),
+                                   (160, 256, 2048), (224, 512, 4096), (32, 4096, 8192)])
+def test_routed_skinny_m(g, orc, out_type, M, N, K):
+    p = mx.make_problem(M, N, K, seed=M * 5 + N + K)
+    t = mx.choose_tile(M, N, p.Kp)
+    assert tuple(t) in SKINNY
+    D = g.run_routed(g.DevProblem(p, t), out_type)
+    R, ab = _oracle(orc, p)
+    checks.check(D, R, ab, out_type)
+
+
+@pytest.mark.parametrize("tile", SKINNY)
+def test_skinny_tiles_bitwise_equal_direct(g, tile):
+    """Every skinny tile, row-major and repacked A, unsplit and split: the same MFMAs in the same
+    K order as the direct kernel, so FP32 outputs are equal bit for bit."""
+    M, N, K = 192, 512, 2112  # 11 K-tiles: odd count, ring wrap, peeled tail
+    p = mx.make_problem(M, N, K, seed=91)
+    dp = g.DevProblem(p, tile)
+    Dd = g.run_direct(dp, mx.OUT_F32)
+    for a_layout in (0, 1):
+        Dt = g.run_explicit(dp, mx.OUT_F32, a_layout=a_layout)
+        assert np.array_equal(Dt.view(np.uint32), Dd.view(np.uint32)), a_layout
+    Dds = g.run_direct(dp, mx.OUT_F32, splits=5)
+    Dts = g.run_explicit(dp, mx.OUT_F32, splits=5, a_layout=1)
+    assert np.array_equal(Dts.view(np.uint32), Dds.view(np.uint32))
+
+
 # ---- A repacked into the preshuffled layout ------------------------------------------------------
 
 @pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
