@@ -52,7 +52,9 @@ size_t mxfp6_gemm_workspace_size(int M, int N, int Kp);
 int mxfp6_splitk_segments(int M, int N, int Kp);
 
 /* gemm(ot, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, B_row_bytes, ws, ws_bytes) on the
- * null stream. Same arguments and semantics as gemm.hpp:63-64 / gemm.cpp:65-83, plus a status:
+ * null stream. Same arguments and semantics as gemm.hpp:63-64 / gemm.cpp:65-83, and shapes:
+ * N a multiple of 128; M a multiple of 128, or (beyond the reference) of 32, routed to 32- and
+ * 64-row tiles (the scales tiled with the MPW choose_tile returns for that M). Plus a status:
  * a shape that would split with a NULL or short workspace runs unsplit (stderr warning, status
  * MXFP6_OK), as the reference does. A workspace too short for the repacked A (but long enough
  * for the partials) only skips the repack: same result, slower. */
