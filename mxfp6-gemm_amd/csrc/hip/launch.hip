@@ -1,12 +1,14 @@
 // HIP launch layer: maps a host plan (mxfp6_launch_desc) onto kernel instantiations, grids and
-// a stream. This file and the kernels it includes are the only HIP code in the library.
+// a stream. This file, the tile kernel's instantiation units (slab_*.hip) and the kernels they
+// include are the only HIP code in the library.
 #include <algorithm>
 
 #include "../hip_layer.h"
 #include "direct_kernel.hpp"
 #include "prep_kernel.hpp"
 #include "reduce_kernel.hpp"
-#include "slab_kernel.hpp"
+#include "repack_kernel.hpp"
+#include "slab_run.hpp"
 
 using namespace mxfp6_dev;
 
@@ -15,9 +17,13 @@ namespace {
 template <typename OutT>
 int launch_reduce(const mxfp6_launch_desc* d, hipStream_t st) {
     const size_t total = (size_t)d->M * d->N;
-    const unsigned blocks = (unsigned)((total / 4 + 255) / 256);
-    reduce_splitk_kernel<OutT><<<dim3(blocks), dim3(256), 0, st>>>(d->ws, static_cast<OutT*>(d->D),
-                                                                  total, d->splits);
+    OutT* D = static_cast<OutT*>(d->D);
+    if (total % 4 == 0)
+        reduce_splitk_kernel<OutT, 4><<<dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0, st>>>(
+            d->ws, D, total, d->splits);
+    else
+        reduce_splitk_kernel<OutT, 1><<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st>>>(
+            d->ws, D, total, d->splits);
     return 0;
 }
 
@@ -45,9 +51,9 @@ int launch_typed(const mxfp6_launch_desc* d, hipStream_t st) {
         case MXFP6_KERNEL_DIRECT:
             return launch_direct<OutT>(d, st);
         case MXFP6_KERNEL_TILE: {
-            const int rc = slab_launch<OutT>(d, st);
-            if (rc != 0 || d->splits <= 1) return rc;
-            return launch_reduce<OutT>(d, st);
+            if (d->splits <= 1) return slab_run<OutT, false>(d, st);
+            const int rc = slab_run<float, true>(d, st);
+            return rc != 0 ? rc : launch_reduce<OutT>(d, st);
         }
         default:
             return 1;
@@ -87,24 +93,36 @@ extern "C" int mxfp6_hip_has_tile(int MT, int NT, int mpw, int npw) {
     return tile_supported(MT, NT, mpw, npw) ? 1 : 0;
 }
 
+// Rows of the tiled scale layout: dim rounded up to whole groups of 32 * group rows.
+static int rows_in_groups(int dim, int group) {
+    return (dim + 32 * group - 1) / (32 * group) * (32 * group);
+}
+
 extern "C" int mxfp6_hip_quantize_rows(const float* x, int rows, int cols, int nblk, void* packed,
                                        size_t row_bytes, uint8_t* scales, int scale_mode,
                                        int ncols, int group, int Kp, void* stream) {
     const int chunks = (nblk + PREP_BLKS_PER_WAVE - 1) / PREP_BLKS_PER_WAVE;
-    const size_t tasks = (size_t)rows * chunks, per_wg = PREP_THREADS / 64;
+    const int rows_out = scale_mode ? rows_in_groups(rows, group) : rows;
+    const size_t tasks = (size_t)rows_out * chunks, per_wg = PREP_THREADS / 64;
     const ScaleOut so{scales, scale_mode, ncols, group, Kp / 192};
-    prep_rows_kernel<<<dim3((unsigned)((tasks + per_wg - 1) / per_wg)), dim3(PREP_THREADS), 0,
-                       static_cast<hipStream_t>(stream)>>>(x, cols, nblk,
-                                                           static_cast<uint8_t*>(packed),
-                                                           row_bytes, so, chunks, rows);
+    const dim3 grid((unsigned)((tasks + per_wg - 1) / per_wg));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint8_t* pk = static_cast<uint8_t*>(packed);
+    if (cols % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0)
+        prep_rows_kernel<true><<<grid, dim3(PREP_THREADS), 0, st>>>(x, cols, nblk, pk, row_bytes,
+                                                                    so, chunks, rows, rows_out);
+    else
+        prep_rows_kernel<false><<<grid, dim3(PREP_THREADS), 0, st>>>(x, cols, nblk, pk, row_bytes,
+                                                                     so, chunks, rows, rows_out);
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
 extern "C" int mxfp6_hip_prepare_b(const float* B, int K, int N, int Kp, int group, void* bsh,
                                    uint8_t* tiled, void* stream) {
-    const unsigned nchunks = (unsigned)((N + 63) / 64), kchunks = (unsigned)((Kp / 32 + 3) / 4);
+    const int NG = rows_in_groups(N, group);
+    const unsigned nchunks = (unsigned)((NG + 63) / 64), kchunks = (unsigned)((Kp / 32 + 3) / 4);
     prep_b_kernel<<<dim3(nchunks * kchunks), dim3(PREP_THREADS), 0,
-                    static_cast<hipStream_t>(stream)>>>(B, K, N, Kp, group,
+                    static_cast<hipStream_t>(stream)>>>(B, K, N, NG, Kp, group,
                                                         static_cast<uint8_t*>(bsh), tiled,
                                                         (int)nchunks);
     return hipGetLastError() == hipSuccess ? 0 : 2;
@@ -112,9 +130,10 @@ extern "C" int mxfp6_hip_prepare_b(const float* B, int K, int N, int Kp, int gro
 
 extern "C" int mxfp6_hip_tile_scales(const uint8_t* s, int dim, int vblk, int ld, int Kp,
                                      int group, uint8_t* tiled, void* stream) {
-    const size_t total = (size_t)dim * (Kp / 32);
+    const int dim_out = rows_in_groups(dim, group);
+    const size_t total = (size_t)dim_out * (Kp / 32);
     const unsigned blocks = (unsigned)std::min<size_t>((total + PREP_THREADS - 1) / PREP_THREADS, 65536);
     tile_scales_kernel<<<dim3(blocks), dim3(PREP_THREADS), 0, static_cast<hipStream_t>(stream)>>>(
-        s, dim, vblk, ld, Kp, group, tiled);
+        s, dim, dim_out, vblk, ld, Kp, group, tiled);
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }

@@ -115,35 +115,46 @@ struct ScaleOut {
     int group, ktn;  // tiled
 };
 
-// Wave tasks: (row r, chunk) for chunk < chunks = ceil(nblk / 64), row-major, 4 per workgroup
-// (grid = ceil(rows * chunks / 4)); a task covers blocks 64 * chunk .. +63 of its row. Block c of
-// row r (c < nblk) writes
-// the codes of values 32c .. 32c+31 (c < cols/32) or zero bytes, cut at row_bytes, and the scale
-// column c if c < so.ncols (127 beyond cols/32).
+// Wave tasks: (row r, chunk) for r < rows_out and chunk < chunks = ceil(nblk / 64), row-major,
+// 4 per workgroup (grid = ceil(rows_out * chunks / 4)); a task covers blocks 64 * chunk .. +63 of
+// its row. Rows rows .. rows_out-1 are zero rows that complete the last scale group of a tiled
+// output (no packed bytes). Block c of row r (c < nblk) writes the codes of values 32c .. 32c+31
+// (zero past cols; zero bytes for a block past the values), cut at row_bytes, and the scale
+// column c if c < so.ncols (127 for a block without values). V4: cols % 4 == 0 and x 16-byte
+// aligned (float4 loads); otherwise one float per lane per load.
+template <bool V4>
 __global__ void __launch_bounds__(PREP_THREADS)
     prep_rows_kernel(const float* __restrict__ x, int cols, int nblk, uint8_t* __restrict__ packed,
-                     size_t row_bytes, ScaleOut so, int chunks, int rows) {
+                     size_t row_bytes, ScaleOut so, int chunks, int rows, int rows_out) {
     __shared__ float stage[PREP_THREADS / 64][PREP_BLKS_PER_WAVE * 33];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const size_t task = (size_t)blockIdx.x * (PREP_THREADS / 64) + wave;
     const int r = (int)(task / chunks), chunk = (int)(task - (size_t)r * chunks);
-    const bool live = r < rows;
+    const bool live = r < rows_out, data = r < rows;
     const int blk0 = chunk * PREP_BLKS_PER_WAVE;
-    const int vblk = cols / 32;  // blocks holding values
+    const int vblk = (cols + 31) / 32;  // blocks holding values
     const float* xr = x + (size_t)r * cols;
     float* st = stage[wave];
-    // coalesced loads of the wave's 2048 values (float4 per lane per step), block-padded in LDS
-    if (live && blk0 < vblk) {
+    // coalesced loads of the wave's 2048 values, block-padded in LDS
+    if (data && blk0 < vblk) {
+        if constexpr (V4) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int p = 4 * (lane + 64 * j);  // value index within the wave's range
-            const int b = p >> 5, i = p & 31;
-            v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (blk0 + b < vblk) v = *reinterpret_cast<const v4f*>(xr + (size_t)(blk0 + b) * 32 + i);
-            st[b * 33 + i] = v[0];
-            st[b * 33 + i + 1] = v[1];
-            st[b * 33 + i + 2] = v[2];
-            st[b * 33 + i + 3] = v[3];
+            for (int j = 0; j < 8; j++) {
+                const int p = 4 * (lane + 64 * j);  // value index within the wave's range
+                const int b = p >> 5, i = p & 31, e = blk0 * 32 + p;
+                v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (e < cols) v = *reinterpret_cast<const v4f*>(xr + e);
+                st[b * 33 + i] = v[0];
+                st[b * 33 + i + 1] = v[1];
+                st[b * 33 + i + 2] = v[2];
+                st[b * 33 + i + 3] = v[3];
+            }
+        } else {
+#pragma unroll 8
+            for (int j = 0; j < 32; j++) {
+                const int p = lane + 64 * j, e = blk0 * 32 + p;
+                st[(p >> 5) * 33 + (p & 31)] = e < cols ? xr[e] : 0.0f;
+            }
         }
     }
     __syncthreads();
@@ -151,7 +162,7 @@ __global__ void __launch_bounds__(PREP_THREADS)
     if (!live || c >= nblk) return;
     uint32_t w[6] = {0, 0, 0, 0, 0, 0};
     int code = 127;
-    if (c < vblk) {
+    if (data && c < vblk) {
         float v[32];
 #pragma unroll
         for (int i = 0; i < 32; i++) v[i] = st[lane * 33 + i];
@@ -159,7 +170,7 @@ __global__ void __launch_bounds__(PREP_THREADS)
     }
     // packed bytes [24c, 24c + 24) of the row, cut at row_bytes (row_bytes % 4 == 0)
     const size_t o = (size_t)24 * c;
-    if (o < row_bytes) {
+    if (data && o < row_bytes) {
         uint32_t* dst = reinterpret_cast<uint32_t*>(packed + (size_t)r * row_bytes + o);
         const int nd = (int)min((size_t)6, (row_bytes - o) / 4);
 #pragma unroll
@@ -174,42 +185,49 @@ __global__ void __launch_bounds__(PREP_THREADS)
     }
 }
 
-// grid: ceil(N / 64) * kchunks workgroups, kchunks = ceil(Kp/32 / 4): workgroup (nb, kc) = one
-// wave per 64 columns and 4 consecutive 32-blocks of K (one per wave), K-chunk major.
+// grid: nchunks * kchunks workgroups, nchunks = ceil(NG / 64), kchunks = ceil(Kp/32 / 4):
+// workgroup (nb, kc) = one wave per 64 columns and 4 consecutive 32-blocks of K (one per wave),
+// K-chunk major. Columns N .. NG-1 (NG = N rounded up to whole scale groups of 32 * group
+// columns) are zero columns: they complete the last 32-column tile of bsh and the last scale
+// group. Values past K in the last 32-block are zero.
 __global__ void __launch_bounds__(PREP_THREADS)
-    prep_b_kernel(const float* __restrict__ B, int K, int N, int Kp, int group,
+    prep_b_kernel(const float* __restrict__ B, int K, int N, int NG, int Kp, int group,
                   uint8_t* __restrict__ bsh, uint8_t* __restrict__ tiled, int nchunks) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int kc = (int)(blockIdx.x / nchunks), nb = (int)(blockIdx.x - (unsigned)kc * nchunks);
     const int n = nb * 64 + lane;
     const int c = kc * (PREP_THREADS / 64) + wave;
-    if (c >= Kp / 32 || n >= N) return;
+    if (c >= Kp / 32 || n >= NG) return;
     uint32_t w[6] = {0, 0, 0, 0, 0, 0};
     int code = 127;
-    if (32 * c < K) {
+    if (n < N && 32 * c < K) {
         float v[32];
         const float* src = B + (size_t)32 * c * N + n;
+        const int kv = min(32, K - 32 * c);  // values of this block
 #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = src[(size_t)i * N];
+        for (int i = 0; i < 32; i++) v[i] = i < kv ? src[(size_t)i * N] : 0.0f;
         code = quant32(v, w);
     }
-    const int k64n = Kp / 64, t = (n & 31) + ((c & 1) << 5);
-    uint8_t* tile = bsh + ((size_t)(n >> 5) * k64n + (c >> 1)) * OPBLK_BYTES;
-    *reinterpret_cast<v4i*>(tile + 16 * t) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-    *reinterpret_cast<v2i*>(tile + 1024 + 8 * t) = v2i{(int)w[4], (int)w[5]};
+    if (n < (N + 31) / 32 * 32) {
+        const int k64n = Kp / 64, t = (n & 31) + ((c & 1) << 5);
+        uint8_t* tile = bsh + ((size_t)(n >> 5) * k64n + (c >> 1)) * OPBLK_BYTES;
+        *reinterpret_cast<v4i*>(tile + 16 * t) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        *reinterpret_cast<v2i*>(tile + 1024 + 8 * t) = v2i{(int)w[4], (int)w[5]};
+    }
     put_tiled_scale(tiled, n, c, group, Kp / 192, code);
 }
 
-// grid-stride over dim * Kp/32 (row-major over (r, c)).
+// grid-stride over dim_out * Kp/32 (row-major over (r, c)); rows dim .. dim_out-1 complete the
+// last scale group (code 127, zero values).
 __global__ void __launch_bounds__(PREP_THREADS)
-    tile_scales_kernel(const uint8_t* __restrict__ s, int dim, int vblk, int ld, int Kp, int group,
-                       uint8_t* __restrict__ tiled) {
+    tile_scales_kernel(const uint8_t* __restrict__ s, int dim, int dim_out, int vblk, int ld,
+                       int Kp, int group, uint8_t* __restrict__ tiled) {
     const int nb = Kp / 32;
-    const size_t total = (size_t)dim * nb;
+    const size_t total = (size_t)dim_out * nb;
     for (size_t e = (size_t)blockIdx.x * PREP_THREADS + threadIdx.x; e < total;
          e += (size_t)gridDim.x * PREP_THREADS) {
         const int r = (int)(e / nb), c = (int)(e - (size_t)r * nb);
-        const int code = c < vblk ? s[(size_t)r * ld + c] : 127;
+        const int code = (r < dim && c < vblk) ? s[(size_t)r * ld + c] : 127;
         put_tiled_scale(tiled, r, c, group, Kp / 192, code);
     }
 }

@@ -1,26 +1,33 @@
 // Split-K second stage: D[i] = (OutT)(((0 + P[0][i]) + P[1][i]) + ... + P[S-1][i]) over the FP32
 // partial layers P[s] = ws + s*total, in fixed segment order (bit-reproducible, and the same
 // summation order as the reference's reduce_splitk, src/kernel.hpp:305-313).
-// HBM-bound: reads S*total*4 bytes and writes total*sizeof(OutT) bytes. Each thread handles
-// 4 consecutive elements with 16-byte loads; total must be a multiple of 4.
+// HBM-bound: reads S*total*4 bytes and writes total*sizeof(OutT) bytes. With VEC = 4 each thread
+// handles 4 consecutive elements with 16-byte loads (total a multiple of 4); VEC = 1 (a ragged
+// M x N) one element per thread.
 #pragma once
 #include "device_common.hpp"
 
 namespace mxfp6_dev {
 
-template <typename OutT>
+template <typename OutT, int VEC>
 __global__ void __launch_bounds__(256)
     reduce_splitk_kernel(const float* __restrict__ ws, OutT* __restrict__ D, size_t total, int S) {
-    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * VEC;
     if (i >= total) return;
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < S; s++) acc += *reinterpret_cast<const v4f*>(ws + (size_t)s * total + i);
-    if constexpr (sizeof(OutT) == 4) {
-        *reinterpret_cast<v4f*>(D + i) = acc;
+    if constexpr (VEC == 1) {
+        float acc = 0.f;
+        for (int s = 0; s < S; s++) acc += ws[(size_t)s * total + i];
+        D[i] = cvt_out<OutT>(acc);
     } else {
-        OutT o[4] = {cvt_out<OutT>(acc.x), cvt_out<OutT>(acc.y), cvt_out<OutT>(acc.z),
-                     cvt_out<OutT>(acc.w)};
-        *reinterpret_cast<v2i*>(D + i) = *reinterpret_cast<const v2i*>(o);
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < S; s++) acc += *reinterpret_cast<const v4f*>(ws + (size_t)s * total + i);
+        if constexpr (sizeof(OutT) == 4) {
+            *reinterpret_cast<v4f*>(D + i) = acc;
+        } else {
+            OutT o[4] = {cvt_out<OutT>(acc.x), cvt_out<OutT>(acc.y), cvt_out<OutT>(acc.z),
+                         cvt_out<OutT>(acc.w)};
+            *reinterpret_cast<v2i*>(D + i) = *reinterpret_cast<const v2i*>(o);
+        }
     }
 }
 

@@ -3,7 +3,8 @@
 // Source: `rows` rows of packed FP6 codes, row r at src + r * row_bytes, read for packed(Kp) =
 // 48 * k64n bytes (a compact row shorter than that is over-read into the next row or the
 // buffer's end pad, exactly as the GEMM kernels read it; those bytes meet B's zero K-tail).
-// Destination: for each 32-row block mb and 64-wide K slab kk, one 1536-byte tile at
+// Destination: ceil(rows / 32) row blocks (rows past `rows` in the last block are zero codes);
+// for each 32-row block mb and 64-wide K slab kk, one 1536-byte tile at
 // (mb * k64n + kk) * 1536 holding the slab in MFMA operand order: lane t = 32h + i (row 32mb + i,
 // K-half h) owns the row's bytes 48kk + 24h .. +23, the first 16 at 16t, the last 8 at
 // 1024 + 8t. This is the layout preshuffle_B gives B^T, so a repacked A is read by the same
@@ -25,7 +26,7 @@ constexpr int REPACK_SEG = 48 * REPACK_KK;  // bytes of one row segment (768)
 
 template <int VEC>
 __global__ void __launch_bounds__(REPACK_THREADS)
-    repack_rows_kernel(const uint8_t* __restrict__ src, int row_bytes, int k64n,
+    repack_rows_kernel(const uint8_t* __restrict__ src, int row_bytes, int rows, int k64n,
                        uint8_t* __restrict__ dst) {
     __shared__ __attribute__((aligned(16))) uint8_t seg[32 * REPACK_SEG];
     const int mb = blockIdx.y;
@@ -33,6 +34,7 @@ __global__ void __launch_bounds__(REPACK_THREADS)
     const int nkk = min(REPACK_KK, k64n - kk0);
     const int seg_bytes = nkk * SLAB_BYTES;
     const uint8_t* rows0 = src + (size_t)mb * 32 * row_bytes + (size_t)kk0 * SLAB_BYTES;
+    const int nrows = min(32, rows - mb * 32);  // rows of this block that exist
 
     // phase 1: 32 row segments -> LDS (row-major, REPACK_SEG bytes per row)
     const int per_row = seg_bytes / VEC;
@@ -40,6 +42,10 @@ __global__ void __launch_bounds__(REPACK_THREADS)
         const int i = c / per_row, o = (c - i * per_row) * VEC;
         const uint8_t* s = rows0 + (size_t)i * row_bytes + o;
         uint8_t* d = seg + i * REPACK_SEG + o;
+        if (i >= nrows) {
+            for (int b = 0; b < VEC; b += 4) *reinterpret_cast<int*>(d + b) = 0;
+            continue;
+        }
         if constexpr (VEC == 16)
             *reinterpret_cast<v4i*>(d) = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(s));
         else if constexpr (VEC == 8)
@@ -73,14 +79,14 @@ __global__ void __launch_bounds__(REPACK_THREADS)
 // Launch: the widest load the source rows' alignment allows.
 inline void repack_rows_launch(const uint8_t* src, int row_bytes, int rows, int k64n,
                                uint8_t* dst, hipStream_t st) {
-    const dim3 grid((unsigned)((k64n + REPACK_KK - 1) / REPACK_KK), (unsigned)(rows / 32));
+    const dim3 grid((unsigned)((k64n + REPACK_KK - 1) / REPACK_KK), (unsigned)((rows + 31) / 32));
     const uintptr_t align = reinterpret_cast<uintptr_t>(src) | (uintptr_t)row_bytes;
     if (align % 16 == 0)
-        repack_rows_kernel<16><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, k64n, dst);
+        repack_rows_kernel<16><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, rows, k64n, dst);
     else if (align % 8 == 0)
-        repack_rows_kernel<8><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, k64n, dst);
+        repack_rows_kernel<8><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, rows, k64n, dst);
     else
-        repack_rows_kernel<4><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, k64n, dst);
+        repack_rows_kernel<4><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, rows, k64n, dst);
 }
 
 }  // namespace mxfp6_dev

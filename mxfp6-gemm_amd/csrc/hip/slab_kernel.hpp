@@ -32,12 +32,19 @@
 // the same time on one XCD cover an XG-row band of output tiles (shared A and B lines in that
 // XCD's L2). Epilogue: lane l of block (mi, ni) holds column l%32 and rows 8g + 4(l/32) + r;
 // D row-major; with SPLIT, FP32 partials of K segment blockIdx.z go to ws[z][M][N].
+// Ragged shapes (MASK: MT does not divide M or NT does not divide N): the grid is
+// ceil(M/MT) x ceil(N/NT), and the operand layouts hold ceil(M/32) and ceil(N/32) 32-row blocks
+// (scale groups: ceil over MPW / NPW blocks). The last tile row and column copy clamped sources
+// (a block, row or scale group past the end reads the last one that exists), so every copy stays
+// inside the operands; the epilogue stores only rows < M and columns < N. The clamping sits in
+// the per-workgroup copy offsets, so the K loop is the same as for a dividing tile.
 #pragma once
 
 #include "../hip_layer.h"
 #include "device_common.hpp"
 #include "lds_dma.hpp"
 #include "repack_kernel.hpp"
+#include "slab_run.hpp"
 
 namespace mxfp6_dev {
 
@@ -82,7 +89,8 @@ struct SlabGeom {
     static_assert(NS >= 4 && (NS - 2) * D <= 63, "vmcnt range");
 };
 
-template <int MT, int NT, int WM, int WN, int NS, int XG, typename OutT, bool SPLIT, bool ASH>
+template <int MT, int NT, int WM, int WN, int NS, int XG, typename OutT, bool SPLIT, bool ASH,
+          bool MASK>
 __global__ void __launch_bounds__(64 * WM * WN, 1)
     slab_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
@@ -111,6 +119,13 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
     const uint8_t* a_base = ASH ? A + (size_t)wg_m * (MT / 32) * k64n * OPBLK_BYTES
                                 : A + (size_t)wg_m * MT * A_row_bytes;
     const uint8_t* b_base = Bsh + (size_t)wg_n * (NT / 32) * k64n * OPBLK_BYTES;
+    // MASK: the last row / block / scale group of the operands that this tile may read (relative
+    // to the tile's first); past them the copies repeat the last one (never stored)
+    const int a_row_last = M - 1 - wg_m * MT;
+    const int a_blk_last = (M + 31) / 32 - 1 - wg_m * (MT / 32);
+    const int b_blk_last = (N + 31) / 32 - 1 - wg_n * (NT / 32);
+    const int sa_grp_last = ((M + 31) / 32 + MPW - 1) / MPW - 1;
+    const int sb_grp_last = ((N + 31) / 32 + NPW - 1) / NPW - 1;
 
     // per-thread copy sources (offsets from the slab's base, constant across slabs)
     uint32_t a_voff[G::A_ISS], b_voff[G::B_ISS];
@@ -118,16 +133,21 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
     for (int i = 0; i < G::A_ISS; i++) {
         const int c = (i * THREADS + tid) % G::A_CHUNKS;
         if (ASH) {
-            const int blk = c / 96, r = c - blk * 96;
+            int blk = c / 96;
+            const int r = c - blk * 96;
+            if (MASK) blk = min(blk, a_blk_last);
             a_voff[i] = (uint32_t)(blk * k64n * OPBLK_BYTES + r * 16);
         } else {
-            const int row = c / 3, part = c - row * 3;
+            int row = c / 3;
+            const int part = c - row * 3;
+            if (MASK) row = min(row, a_row_last);
             a_voff[i] = (uint32_t)(row * A_row_bytes + part * 16);
         }
     }
 #pragma unroll
     for (int i = 0; i < G::B_ISS; i++) {
-        const int c = (i * THREADS + tid) % G::B_CHUNKS, blk = c / 96, r = c - blk * 96;
+        const int c = (i * THREADS + tid) % G::B_CHUNKS, b = c / 96, r = c - b * 96;
+        const int blk = MASK ? min(b, b_blk_last) : b;
         b_voff[i] = (uint32_t)(blk * k64n * OPBLK_BYTES + r * 16);
     }
     // scale gather: wave w copies group i*NWAVES + w of [A groups | B groups]; lane l's dword of
@@ -137,7 +157,8 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
     for (int i = 0; i < G::SC_ISS; i++) {
         int grp = i * G::NWAVES + wave;
         if (grp >= G::SC_GROUPS) grp = G::SC_GROUPS - 1;  // dummy copy: valid source
-        const int g = grp < WM ? wg_m * WM + grp : wg_n * WN + (grp - WM);
+        int g = grp < WM ? wg_m * WM + grp : wg_n * WN + (grp - WM);
+        if (MASK) g = min(g, grp < WM ? sa_grp_last : sb_grp_last);
         sc_src[i] = (grp < WM ? sA : sB) + ((size_t)g * k_tiles * 64 + lane) * 12;
     }
     const uint32_t lds0 = lds_u32(lds);
@@ -334,7 +355,9 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
             for (int g = 0; g < 4; g++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const size_t idx = (size_t)(m_w + mi * 32 + 8 * g + r) * N + n_w + ni * 32;
+                    const int m = m_w + mi * 32 + 8 * g + r, n = n_w + ni * 32;
+                    if (MASK && (m >= M || n >= N)) continue;
+                    const size_t idx = (size_t)m * N + n;
                     if (SPLIT)
                         ws[(size_t)blockIdx.z * M * N + idx] = acc[mi][ni][4 * g + r];
                     else
@@ -342,69 +365,62 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
                 }
 }
 
-// ---- instantiations and launch -------------------------------------------------------------------
+// ---- launch ----------------------------------------------------------------------------------
 
-// (MT, NT, MPW, NPW) -> wave grid: the scale grouping fixes how many 32-blocks one wave holds,
-// so it also selects between the 4-wave and 8-wave instantiation of a tile.
-inline bool tile_supported(int MT, int NT, int mpw, int npw) {
-    return (MT == 32 && NT == 128 && mpw == 1 && npw == 1) ||
-           (MT == 32 && NT == 256 && mpw == 1 && npw == 2) ||
-           (MT == 64 && NT == 128 && mpw == 2 && npw == 1) ||
-           (MT == 64 && NT == 256 && mpw == 2 && npw == 2) ||
-           (MT == 128 && NT == 128 && mpw == 2 && npw == 2) ||
-           (MT == 128 && NT == 256 && mpw == 2 && npw == 4) ||
-           (MT == 128 && NT == 384 && mpw == 4 && npw == 3) ||
-           (MT == 256 && NT == 256 && mpw == 4 && npw == 4) ||
-           (MT == 256 && NT == 192 && mpw == 4 && npw == 3) ||
-           (MT == 256 && NT == 256 && mpw == 2 && npw == 4);
+// One launch of the tile kernel; KT is the kernel's output type (float for the split-K partials).
+template <int MT, int NT, int WM, int WN, int XG, int NS, typename KT, bool SPLIT, bool ASH,
+          bool MASK>
+void slab_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipStream_t st) {
+    const dim3 grid((unsigned)((d->M + MT - 1) / MT), (unsigned)((d->N + NT - 1) / NT),
+                    (unsigned)d->splits);
+    slab_kernel<MT, NT, WM, WN, NS, XG, KT, SPLIT, ASH, MASK><<<grid, dim3(64 * WM * WN), 0, st>>>(
+        A, static_cast<const uint8_t*>(d->Bsh), d->sA, d->sB,
+        SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr, d->M, d->N, d->Kp,
+        d->A_row_bytes, SPLIT ? d->splits : 1);
 }
 
-// Ring depth per tile: as many slabs as fit 160 KiB of LDS (128 x 128: half of it, two
-// workgroups per CU).
-template <int MT, int NT, int WM, int WN, int XG, int NS, typename OutT, bool ASH>
-void slab_launch_a(const mxfp6_launch_desc* d, const uint8_t* A, hipStream_t st) {
-    const dim3 grid((unsigned)(d->M / MT), (unsigned)(d->N / NT), (unsigned)d->splits);
-    const dim3 block(64 * WM * WN);
-    const uint8_t* B = static_cast<const uint8_t*>(d->Bsh);
-    if (d->splits > 1)
-        slab_kernel<MT, NT, WM, WN, NS, XG, float, true, ASH><<<grid, block, 0, st>>>(
-            A, B, d->sA, d->sB, nullptr, d->ws, d->M, d->N, d->Kp, d->A_row_bytes, d->splits);
-    else
-        slab_kernel<MT, NT, WM, WN, NS, XG, OutT, false, ASH><<<grid, block, 0, st>>>(
-            A, B, d->sA, d->sB, static_cast<OutT*>(d->D), nullptr, d->M, d->N, d->Kp,
-            d->A_row_bytes, 1);
-}
-
-template <int MT, int NT, int WM, int WN, int XG, int NS, typename OutT>
+// Ring depth per tile: as many slabs as fit 160 KiB of LDS (128 x 128 and 32 x 128: half of it,
+// two workgroups per CU). MASK when the tile does not divide M x N.
+template <int MT, int NT, int WM, int WN, int XG, int NS, typename KT, bool SPLIT>
 int slab_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     static_assert(SlabGeom<MT, NT, WM, WN, NS>::LDS <= 160 * 1024, "LDS budget");
+    const bool mask = d->M % MT != 0 || d->N % NT != 0;
+    const uint8_t* A = static_cast<const uint8_t*>(d->A);
     if (d->a_layout == MXFP6_A_REPACK) {
         // repack A into the preshuffled layout, then run the kernel on it
-        repack_rows_launch(static_cast<const uint8_t*>(d->A), d->A_row_bytes, d->M, d->Kp / 64,
-                           static_cast<uint8_t*>(d->Ash), st);
-        slab_launch_a<MT, NT, WM, WN, XG, NS, OutT, true>(d, static_cast<const uint8_t*>(d->Ash), st);
-    } else if (d->a_layout == MXFP6_A_PRESHUFFLED) {
-        slab_launch_a<MT, NT, WM, WN, XG, NS, OutT, true>(d, static_cast<const uint8_t*>(d->A), st);
+        repack_rows_launch(A, d->A_row_bytes, d->M, d->Kp / 64, static_cast<uint8_t*>(d->Ash), st);
+        A = static_cast<const uint8_t*>(d->Ash);
+    }
+    if (d->a_layout == MXFP6_A_ROWS) {
+        if (mask)
+            slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, false, true>(d, A, st);
+        else
+            slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, false, false>(d, A, st);
     } else {
-        slab_launch_a<MT, NT, WM, WN, XG, NS, OutT, false>(d, static_cast<const uint8_t*>(d->A), st);
+        if (mask)
+            slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, true, true>(d, A, st);
+        else
+            slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, true, false>(d, A, st);
     }
     return 0;
 }
 
-template <typename OutT>
-int slab_launch(const mxfp6_launch_desc* d, hipStream_t st) {
+// Tile dispatch (declared in slab_run.hpp; instantiated once per (KT, SPLIT) in its own
+// translation unit: slab_split.hip, slab_f32.hip, slab_f16.hip, slab_bf16.hip).
+template <typename KT, bool SPLIT>
+int slab_run(const mxfp6_launch_desc* d, hipStream_t st) {
     if (!tile_supported(d->MT, d->NT, d->mpw, d->npw)) return 1;
-    // skinny tiles (M not a multiple of 128): one wave row, four wave columns, a deeper ring
-    if (d->MT == 32 && d->NT == 128) return slab_launch_t<32, 128, 1, 4, 4, 8, OutT>(d, st);
-    if (d->MT == 32 && d->NT == 256) return slab_launch_t<32, 256, 1, 4, 4, 8, OutT>(d, st);
-    if (d->MT == 64 && d->NT == 128) return slab_launch_t<64, 128, 1, 4, 4, 8, OutT>(d, st);
-    if (d->MT == 64 && d->NT == 256) return slab_launch_t<64, 256, 1, 4, 4, 8, OutT>(d, st);
-    if (d->MT == 128 && d->NT == 128) return slab_launch_t<128, 128, 2, 2, 4, 6, OutT>(d, st);
-    if (d->MT == 128 && d->NT == 256) return slab_launch_t<128, 256, 2, 2, 4, 8, OutT>(d, st);
-    if (d->MT == 128 && d->NT == 384) return slab_launch_t<128, 384, 1, 4, 4, 6, OutT>(d, st);
-    if (d->MT == 256 && d->NT == 192) return slab_launch_t<256, 192, 2, 2, 4, 6, OutT>(d, st);
-    if (d->mpw == 2) return slab_launch_t<256, 256, 4, 2, 4, 6, OutT>(d, st);
-    return slab_launch_t<256, 256, 2, 2, 4, 6, OutT>(d, st);
+    // skinny tiles: one wave row, four wave columns, a deeper ring
+    if (d->MT == 32 && d->NT == 128) return slab_launch_t<32, 128, 1, 4, 4, 8, KT, SPLIT>(d, st);
+    if (d->MT == 32 && d->NT == 256) return slab_launch_t<32, 256, 1, 4, 4, 8, KT, SPLIT>(d, st);
+    if (d->MT == 64 && d->NT == 128) return slab_launch_t<64, 128, 1, 4, 4, 8, KT, SPLIT>(d, st);
+    if (d->MT == 64 && d->NT == 256) return slab_launch_t<64, 256, 1, 4, 4, 8, KT, SPLIT>(d, st);
+    if (d->MT == 128 && d->NT == 128) return slab_launch_t<128, 128, 2, 2, 4, 6, KT, SPLIT>(d, st);
+    if (d->MT == 128 && d->NT == 256) return slab_launch_t<128, 256, 2, 2, 4, 8, KT, SPLIT>(d, st);
+    if (d->MT == 128 && d->NT == 384) return slab_launch_t<128, 384, 1, 4, 4, 6, KT, SPLIT>(d, st);
+    if (d->MT == 256 && d->NT == 192) return slab_launch_t<256, 192, 2, 2, 4, 6, KT, SPLIT>(d, st);
+    if (d->mpw == 2) return slab_launch_t<256, 256, 4, 2, 4, 6, KT, SPLIT>(d, st);
+    return slab_launch_t<256, 256, 2, 2, 4, 6, KT, SPLIT>(d, st);
 }
 
 }  // namespace mxfp6_dev

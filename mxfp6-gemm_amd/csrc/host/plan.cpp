@@ -23,9 +23,13 @@ namespace plan {
 //   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (4; two workgroups fit a CU's LDS)
 // and, for M not a multiple of 128 (M a multiple of 32), the skinny tiles (waves 1x4):
 //   64x256 (MPW 2, NPW 2), 32x256 (1, 2), 64x128 (2, 1), 32x128 (1, 1; two per CU)
+// Ragged shapes (M not a multiple of 32 or N not a multiple of 128) take any of the nine tiles,
+// the last tile row and column masked (wg counts the partial tiles).
 // A plan is (tile, K segments S, A repacked or not); the router takes the plan with the least
 // predicted time. The time model (microseconds, MI355X) follows the kernel's structure:
+//   wg       = ceil(M / MT) * ceil(N / NT) workgroups per K segment;
 //   waves    = ceil(wg * S / (CUS * occupancy)) rounds of workgroups;
+//   per_cu   = ceil(min(wg * S, CUS * occupancy) / CUS) workgroups on the busiest CU;
 //   t_slab   = max(T_SLAB_MIN, per_cu * (T_MFMA * mfmas + T_COPY_KB * copied KiB)) per 64-wide K
 //              slab: a latency floor (the ring keeps four slabs in flight), else the CU's MFMA and
 //              global->LDS copy work, shared by the workgroups resident on it; a row-major A slab
@@ -34,10 +38,12 @@ namespace plan {
 //   t_wg     = T_WG + slabs * t_slab + T_OUT_KB * output KiB * per_cu;
 //   t        = T_LAUNCH + waves * t_wg, plus for a repack T_LAUNCH + its bytes (A read and written)
 //              at BYTES_PER_US, and for a split T_LAUNCH + the partials written and read back.
-// The constants are a least-squares fit (log time) to every plan of 46 shapes measured on one
-// MI355X (M, N from 128 to 8192, K from 1024 to 105728): the plan the model picks is within
-// 1.2% of the measured best on average, 11% at worst (the previous fixed rules were up to 2x
-// off on small-K grids), and it is the measured best on the five benchmark workloads.
+// The constants are a least-squares fit (log time) to every plan of the 56 measured shapes with
+// M % 128 == 0 (one MI355X; M from 128 to 8192, N from 256 to 102272, K from 1024 to 105728,
+// masked N included): the plan the model picks is within 1.1% of the measured best on average,
+// 14% at worst (fixed rules were up to 2x off on small-K grids), and it is the measured best on
+// the five benchmark workloads. On the 14 skinny-M and 6 ragged shapes measured, the same
+// constants pick within 16% and 7% of the best.
 namespace {
 struct Plan {
     TileChoice tc;
@@ -49,51 +55,68 @@ const TileChoice kCands[] = {{256, 256, 4, 4}, {256, 192, 4, 3}, {128, 384, 4, 3
 const TileChoice kSkinny[] = {{64, 256, 2, 2}, {32, 256, 1, 2}, {64, 128, 2, 1}, {32, 128, 1, 1}};
 
 double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repack) {
-    const long wg = (long)(M / tc.MT) * (N / tc.NT) * S;
+    const long wg = (long)((M + tc.MT - 1) / tc.MT) * ((N + tc.NT - 1) / tc.NT) * S;
     const int occ = (tc.NT == 128 && (tc.MT == 128 || tc.MT == 32)) ? 2 : 1;  // per CU (LDS)
     const long cap = (long)CUS * occ;
     const long waves = (wg + cap - 1) / cap;
-    const double per_cu = std::max(1.0, (double)std::min(wg, cap) / CUS);
+    const long per_cu = std::max(1L, (std::min(wg, cap) + CUS - 1) / CUS);  // on the busiest CU
     const int mfmas = tc.MPW * tc.NPW;  // per wave per slab
     const double slabs = (double)(Kp / 64) / S;
     const double copy_kb =
         (tc.MT * 48.0 * (repack ? 1.0 : 1.0 + A_ROWS_COST) + tc.NT / 32 * 1536.0) / 1024.0;
-    const double t_slab = std::max(T_SLAB_MIN, per_cu * (T_MFMA * mfmas + T_COPY_KB * copy_kb));
+    const double t_slab =
+        std::max(T_SLAB_MIN, (double)per_cu * (T_MFMA * mfmas + T_COPY_KB * copy_kb));
     const double out_kb = tc.MT * tc.NT * (S > 1 ? 4.0 : 2.0) / 1024.0;
     const double t_wg = T_WG + slabs * t_slab + T_OUT_KB * out_kb * per_cu;
     double t = T_LAUNCH + (double)waves * t_wg;
-    if (repack) t += T_LAUNCH + 2.0 * M * (Kp / 4 * 3.0) / BYTES_PER_US;
+    if (repack) t += T_LAUNCH + 2.0 * ((M + 31) / 32 * 32) * (Kp / 4 * 3.0) / BYTES_PER_US;
     if (S > 1) t += T_LAUNCH + (4.0 * S * M * N + 2.0 * M * N) / BYTES_PER_US;
     return t;
 }
 
 bool shape_ok(int M, int N, int Kp) {
-    return M > 0 && N > 0 && Kp > 0 && M % 32 == 0 && N % 128 == 0 && Kp % K_TILE == 0;
+    return M > 0 && N > 0 && Kp > 0 && Kp % K_TILE == 0;
 }
+
+// M x N tiled by whole 32-row and 128-column blocks (the reference's shapes and the skinny-M
+// ones); other shapes are ragged and run masked tiles.
+bool regular(int M, int N) {
+    return M % 32 == 0 && N % 128 == 0;
+}
+
+const int kNCands = (int)(sizeof(kCands) / sizeof(kCands[0]));
+const int kNSkinny = (int)(sizeof(kSkinny) / sizeof(kSkinny[0]));
 
 // The least-time plan. Candidates are visited from the simplest (no split, no repack) and a
 // plan needs a PLAN_MIN_GAIN lead to displace an earlier one, so near-ties keep the plan with
-// fewer launches and less workspace. Shapes gemm() rejects get the trivial plan.
+// fewer launches and less workspace. Regular shapes take the tiles whose MT divides M (the
+// skinny ones when M is not a multiple of 128), with the last tile column masked when NT does
+// not divide N (the reference's NMASK route, src/kernel.hpp:144-154, for any tile: N = 102272
+// runs 256x256 over ceil(N/256) columns instead of 128x128); ragged shapes any of the nine, big
+// tiles first. Shapes gemm() rejects get the trivial plan.
 Plan best_plan(int M, int N, int Kp) {
     Plan best = {{128, 128, 2, 2}, 1, false};
     if (!shape_ok(M, N, Kp)) return best;
     double best_t = -1.0;
     const int k_tiles = Kp / K_TILE;
+    const bool reg = regular(M, N);
     const bool skinny = M % 128 != 0;
-    const TileChoice* cands = skinny ? kSkinny : kCands;
-    const int n_cands = skinny ? (int)(sizeof(kSkinny) / sizeof(kSkinny[0]))
-                               : (int)(sizeof(kCands) / sizeof(kCands[0]));
-    for (int rp = 0; rp < 2; rp++)
-        for (int S = 1; S <= MAX_SPLITS && S <= k_tiles; S++)
-            for (int ci = 0; ci < n_cands; ci++) {
-                const TileChoice& tc = cands[ci];
-                if (M % tc.MT != 0 || N % tc.NT != 0) continue;
-                const double t = plan_time_us(tc, M, N, Kp, S, rp != 0);
-                if (best_t < 0 || t < best_t * (1.0 - PLAN_MIN_GAIN)) {
-                    best = {tc, S, rp != 0};
-                    best_t = t;
+    const int n_cands = reg ? (skinny ? kNSkinny : kNCands) : kNCands + kNSkinny;
+    // regular shapes: the dividing tiles first, then (pass 1) the N-masked ones
+    for (int pass = 0; pass < (reg ? 2 : 1); pass++)
+        for (int rp = 0; rp < 2; rp++)
+            for (int S = 1; S <= MAX_SPLITS && S <= k_tiles; S++)
+                for (int ci = 0; ci < n_cands; ci++) {
+                    const TileChoice& tc =
+                        reg ? (skinny ? kSkinny[ci] : kCands[ci])
+                            : (ci < kNCands ? kCands[ci] : kSkinny[ci - kNCands]);
+                    if (reg && (M % tc.MT != 0 || (N % tc.NT != 0) != (pass == 1))) continue;
+                    const double t = plan_time_us(tc, M, N, Kp, S, rp != 0);
+                    if (best_t < 0 || t < best_t * (1.0 - PLAN_MIN_GAIN)) {
+                        best = {tc, S, rp != 0};
+                        best_t = t;
+                    }
                 }
-            }
     return best;
 }
 }  // namespace
@@ -106,8 +129,9 @@ size_t split_bytes(int M, int N, int S) {
     return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
+// The repacked A: ceil(M / 32) whole 32-row blocks.
 size_t repack_bytes(int M, int Kp) {
-    return (size_t)M * (size_t)(Kp / 4 * 3);
+    return (size_t)((M + 31) / 32 * 32) * (size_t)(Kp / 4 * 3);
 }
 
 size_t plan_bytes(int M, int N, int Kp, int S, bool repack) {
@@ -135,8 +159,7 @@ int check_common(int out_type, int M, int N, int Kp, const void* dA, const void*
                  const void* dsA, const void* dsB, const void* dD, int A_row_bytes) {
     if (out_type < 0 || out_type > 2) return MXFP6_ERR_OUT_TYPE;
     if (!dA || !dBsh || !dsA || !dsB || !dD) return MXFP6_ERR_NULL;
-    if (M <= 0 || N <= 0 || M % 32 != 0 || N % 128 != 0) return MXFP6_ERR_SHAPE;
-    if (Kp <= 0 || Kp % K_TILE != 0) return MXFP6_ERR_SHAPE;
+    if (M <= 0 || N <= 0 || Kp <= 0 || Kp % K_TILE != 0) return MXFP6_ERR_SHAPE;
     // A rows are read for packed(Kp) bytes from row * A_row_bytes; a compact row (packed(K),
     // K > Kp - K_TILE) is at most packed(K_TILE - 32) = 120 bytes shorter than packed(Kp).
     const long packed_kp = (long)Kp / 4 * 3;
@@ -149,7 +172,7 @@ const char* status_text(int st) {
     switch (st) {
         case MXFP6_OK: return "ok";
         case MXFP6_ERR_NULL: return "null pointer argument";
-        case MXFP6_ERR_SHAPE: return "unsupported shape (M multiple of 32, N of 128; Kp multiple of 192; A_row_bytes)";
+        case MXFP6_ERR_SHAPE: return "unsupported shape (M, N > 0; Kp a multiple of 192; A_row_bytes)";
         case MXFP6_ERR_OUT_TYPE: return "out_type must be F32, F16 or BF16";
         case MXFP6_ERR_TILE: return "tile not implemented or does not divide the shape";
         case MXFP6_ERR_ARG: return "invalid argument";
@@ -204,12 +227,11 @@ int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void*
     if (st != MXFP6_OK) return st;
     const Plan pl = best_plan(M, N, Kp);
     const TileChoice tc = pl.tc;
-    if (N % tc.NT != 0 || M % tc.MT != 0) return MXFP6_ERR_TILE;
     int S = pl.S;
     bool rp = pl.repack;
     const int kernel = kernel_for(tc);
     if (kernel != MXFP6_KERNEL_TILE) rp = false;
-    if (kernel != MXFP6_KERNEL_TILE && M % 64 != 0) return MXFP6_ERR_TILE;
+    if (kernel != MXFP6_KERNEL_TILE && (M % 64 != 0 || N % 64 != 0)) return MXFP6_ERR_TILE;
     if (ws == nullptr) ws_bytes = 0;
     // A workspace too small for the repacked A drops the repack (a pure speed choice); one too
     // small for the split-K partials as well runs unsplit, with the reference's warning.
@@ -229,6 +251,12 @@ bool tile_divides(const int tile[4], int M, int N) {
     return tile[0] > 0 && tile[1] > 0 && M % tile[0] == 0 && N % tile[1] == 0 &&
            tile[2] >= 1 && tile[2] <= 4 && tile[3] >= 1 && tile[3] <= 4 &&
            (M / 32) % tile[2] == 0 && (N / 32) % tile[3] == 0;
+}
+
+// A tile the explicit plan may run on any M x N: a partial last tile row or column is masked.
+bool tile_valid(const int tile[4]) {
+    return tile[0] > 0 && tile[1] > 0 && tile[2] >= 1 && tile[2] <= 4 && tile[3] >= 1 &&
+           tile[3] <= 4;
 }
 
 }  // namespace plan
@@ -333,7 +361,7 @@ extern "C" int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int
     if (!tile) return MXFP6_ERR_NULL;
     const int st = plan::check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
     if (st != MXFP6_OK) return st;
-    if (!plan::tile_divides(tile, M, N)) return MXFP6_ERR_TILE;
+    if (!plan::tile_valid(tile)) return MXFP6_ERR_TILE;
     const TileChoice tc = {tile[0], tile[1], tile[2], tile[3]};
     if (!mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW)) return MXFP6_ERR_TILE;
     if (splits < 1 || splits > Kp / K_TILE || a_layout < MXFP6_A_ROWS ||
@@ -353,7 +381,7 @@ extern "C" int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, in
                                  void* ws, size_t ws_bytes, void* stream) {
     const int st = plan::check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
     if (st != MXFP6_OK) return st;
-    if (M % 64 != 0) return MXFP6_ERR_SHAPE;  // the direct kernel's workgroups are 64x64
+    if (M % 64 != 0 || N % 64 != 0) return MXFP6_ERR_SHAPE;  // its workgroups are 64x64
     if (mpw < 1 || mpw > 4 || npw < 1 || npw > 4 || (M / 32) % mpw != 0 || (N / 32) % npw != 0)
         return MXFP6_ERR_ARG;
     if (splits < 1 || splits > Kp / K_TILE) return MXFP6_ERR_ARG;
@@ -377,7 +405,7 @@ extern "C" size_t mxfp6_plan_workspace_size(int M, int N, int Kp, int splits, in
 extern "C" int mxfp6_preshuffle_rows_async(const void* src, int row_bytes, int rows, int Kp,
                                            void* dst, void* stream) {
     if (!src || !dst) return MXFP6_ERR_NULL;
-    if (rows <= 0 || rows % 32 != 0 || Kp <= 0 || Kp % K_TILE != 0) return MXFP6_ERR_SHAPE;
+    if (rows <= 0 || Kp <= 0 || Kp % K_TILE != 0) return MXFP6_ERR_SHAPE;
     if (row_bytes <= 0 || row_bytes % 4 != 0 || row_bytes < Kp / 4 * 3 - 120) return MXFP6_ERR_SHAPE;
     return mxfp6_hip_repack(src, row_bytes, rows, Kp, dst, stream) == 0 ? MXFP6_OK : MXFP6_ERR_HIP;
 }

@@ -12,14 +12,14 @@ namespace plan {
 constexpr int CUS = 256;
 // Plan-time model of the router (plan.cpp): least-squares fit on MI355X, microseconds.
 constexpr int MAX_SPLITS = 16;             // K segments considered
-constexpr double T_LAUNCH = 3.737;         // one kernel launch (and its ramp), back to back
-constexpr double T_WG = 0.394;             // fixed cost of one workgroup
-constexpr double T_SLAB_MIN = 0.2447;      // latency floor of one 64-wide K slab
-constexpr double T_MFMA = 0.010511;        // per MFMA per wave per slab, per resident workgroup
-constexpr double T_COPY_KB = 0.01375;      // per KiB copied global->LDS per slab, per workgroup
-constexpr double T_OUT_KB = 0.010544;      // per KiB of output (FP16 tile or FP32 partial) per workgroup
-constexpr double BYTES_PER_US = 3.873e6;   // repack and split-K partial traffic
-constexpr double A_ROWS_COST = 0.76725;    // extra copy cost per byte of a row-major A slab
+constexpr double T_LAUNCH = 2.850807;       // one kernel launch (and its ramp), back to back
+constexpr double T_WG = 2.072229;           // fixed cost of one workgroup
+constexpr double T_SLAB_MIN = 0.25706;      // latency floor of one 64-wide K slab
+constexpr double T_MFMA = 0.011908;        // per MFMA per wave per slab, per workgroup on the busiest CU
+constexpr double T_COPY_KB = 0.011984;      // per KiB copied global->LDS per slab, per workgroup
+constexpr double T_OUT_KB = 0.017816;      // per KiB of output (FP16 tile or FP32 partial) per workgroup
+constexpr double BYTES_PER_US = 4.401662e6;   // repack and split-K partial traffic
+constexpr double A_ROWS_COST = 0.853373;    // extra copy cost per byte of a row-major A slab
 constexpr double PLAN_MIN_GAIN = 0.01;     // lead a more complex plan needs over a simpler one
 
 TileChoice route(int M, int N, int Kp);

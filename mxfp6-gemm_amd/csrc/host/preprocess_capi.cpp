@@ -295,14 +295,21 @@ extern "C" int mxfp6_gen_operand(int rows, int K, int dist, double sigma, uint64
 extern "C" int mxfp6_prepare_b(const uint8_t* packed, int N, int Kp, size_t b_row_bytes,
                                uint8_t* bsh, int nthreads) {
     if (!packed || !bsh) return MXFP6_ERR_NULL;
-    if (N <= 0 || N % 32 != 0 || Kp <= 0 || Kp % 64 != 0 || b_row_bytes < (size_t)(Kp / 4 * 3))
+    if (N <= 0 || Kp <= 0 || Kp % 64 != 0 || b_row_bytes < (size_t)(Kp / 4 * 3))
         return MXFP6_ERR_ARG;
     const size_t k64n = (size_t)(Kp / 64);
-    parallel_for((size_t)(N / 32), nthreads, [&](size_t nt) {
+    // ceil(N / 32) tiles; rows past N in the last one are zero codes
+    parallel_for((size_t)((N + 31) / 32), nthreads, [&](size_t nt) {
         for (size_t q = 0; q < k64n; q++) {
             uint8_t* tile = bsh + (nt * k64n + q) * 1536;
             for (size_t t = 0; t < 64; t++) {
-                const uint8_t* src = packed + (nt * 32 + (t & 31)) * b_row_bytes + q * 48 + (t >> 5) * 24;
+                const size_t n = nt * 32 + (t & 31);
+                if (n >= (size_t)N) {
+                    std::memset(tile + 16 * t, 0, 16);
+                    std::memset(tile + 1024 + 8 * t, 0, 8);
+                    continue;
+                }
+                const uint8_t* src = packed + n * b_row_bytes + q * 48 + (t >> 5) * 24;
                 std::memcpy(tile + 16 * t, src, 16);
                 std::memcpy(tile + 1024 + 8 * t, src + 16, 8);
             }
@@ -314,11 +321,10 @@ extern "C" int mxfp6_prepare_b(const uint8_t* packed, int N, int Kp, size_t b_ro
 extern "C" int mxfp6_prepare_scales(const uint8_t* scales, int dim, int Kp, int group,
                                     uint8_t* tiled, int nthreads) {
     if (!scales || !tiled) return MXFP6_ERR_NULL;
-    if (dim <= 0 || dim % 32 != 0 || Kp <= 0 || Kp % 192 != 0 || group < 1 || group > 4 ||
-        (dim / 32) % group != 0)
-        return MXFP6_ERR_ARG;
+    if (dim <= 0 || Kp <= 0 || Kp % 192 != 0 || group < 1 || group > 4) return MXFP6_ERR_ARG;
     const size_t sc = (size_t)(Kp / 32), k_tiles = (size_t)(Kp / 192), gp = 4;
-    parallel_for((size_t)(dim / 32 / group), nthreads, [&](size_t g) {
+    // ceil(dim / (32 * group)) groups; rows past dim are zero rows (code 127)
+    parallel_for((size_t)((dim + 32 * group - 1) / (32 * group)), nthreads, [&](size_t g) {
         for (size_t kt = 0; kt < k_tiles; kt++)
             for (size_t lane = 0; lane < 64; lane++)
                 for (size_t sub = 0; sub < 3; sub++) {
@@ -329,7 +335,9 @@ extern "C" int mxfp6_prepare_scales(const uint8_t* scales, int dim, int Kp, int 
                             continue;
                         }
                         const size_t row = (g * group + j) * 32 + (lane & 31);
-                        dst[j] = scales[row * sc + 2 * (kt * 3 + sub) + (lane >> 5)];
+                        dst[j] = row < (size_t)dim
+                                     ? scales[row * sc + 2 * (kt * 3 + sub) + (lane >> 5)]
+                                     : 127;
                     }
                 }
     });

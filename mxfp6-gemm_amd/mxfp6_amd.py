@@ -247,7 +247,8 @@ def gen_values(rows: int, K: int, dist: int, sigma: float, seed: int, stream: in
 
 
 def prepare_b(packed: np.ndarray, N: int, Kp: int, row_bytes: int, nthreads: int = 0) -> np.ndarray:
-    out = np.empty((N // 32) * (Kp // 64) * 1536, dtype=np.uint8)
+    """Preshuffled B^T: ceil(N/32) tiles of 32 columns (zero codes past N)."""
+    out = np.empty(-(-N // 32) * (Kp // 64) * 1536, dtype=np.uint8)
     _check(lib().mxfp6_prepare_b(_ptr(packed), N, Kp, row_bytes, _ptr(out), nthreads),
            "prepare_b")
     return out
@@ -256,7 +257,7 @@ def prepare_b(packed: np.ndarray, N: int, Kp: int, row_bytes: int, nthreads: int
 def prepare_scales(scales: np.ndarray, dim: int, Kp: int, group: int, nthreads: int = 0) -> np.ndarray:
     scales = np.ascontiguousarray(scales, dtype=np.uint8)
     assert scales.size == dim * (Kp // 32)
-    out = np.empty(lib().mxfp6_tile_scale_bytes(dim, Kp, group, 3), dtype=np.uint8)
+    out = np.empty(tiled_scale_bytes(dim, Kp, group), dtype=np.uint8)
     _check(lib().mxfp6_prepare_scales(_ptr(scales), dim, Kp, group, _ptr(out), nthreads),
            "prepare_scales")
     return out

@@ -20,19 +20,19 @@ TILES = [(256, 256, 4, 4), (256, 192, 4, 3), (128, 384, 4, 3), (128, 256, 2, 4),
 SKINNY = [(64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)]  # M % 128 != 0
 NAMES = ["T_LAUNCH", "T_WG", "T_SLAB_MIN", "T_MFMA", "T_COPY_KB", "T_OUT_KB", "BYTES_PER_US",
          "A_ROWS_COST"]
-CONSTANTS = {"T_LAUNCH": 3.737, "T_WG": 0.394, "T_SLAB_MIN": 0.2447, "T_MFMA": 0.010511,
-             "T_COPY_KB": 0.01375, "T_OUT_KB": 0.010544, "BYTES_PER_US": 3.873e6,
-             "A_ROWS_COST": 0.76725}
+CONSTANTS = {"T_LAUNCH": 2.850807, "T_WG": 2.072229, "T_SLAB_MIN": 0.25706, "T_MFMA": 0.011908,
+             "T_COPY_KB": 0.011984, "T_OUT_KB": 0.017816, "BYTES_PER_US": 4.401662e6,
+             "A_ROWS_COST": 0.853373}
 PLAN_MIN_GAIN = 0.01
 
 
 def plan_time_us(c, tile, M, N, Kp, S, repack):
     MT, NT = tile[0], tile[1]
-    wg = (M // MT) * (N // NT) * S
+    wg = -(-M // MT) * -(-N // NT) * S
     occ = 2 if (MT, NT) in ((128, 128), (32, 128)) else 1
     cap = CUS * occ
     waves = (wg + cap - 1) // cap
-    per_cu = max(1.0, min(wg, cap) / CUS)
+    per_cu = max(1, -(-min(wg, cap) // CUS))  # workgroups on the busiest CU
     mfmas = tile[2] * tile[3]
     slabs = (Kp // 64) / S
     copy_kb = (MT * 48.0 * (1.0 if repack else 1.0 + c["A_ROWS_COST"]) + NT // 32 * 1536.0) / 1024.0
@@ -41,7 +41,7 @@ def plan_time_us(c, tile, M, N, Kp, S, repack):
     t_wg = c["T_WG"] + slabs * t_slab + c["T_OUT_KB"] * out_kb * per_cu
     t = c["T_LAUNCH"] + waves * t_wg
     if repack:
-        t += c["T_LAUNCH"] + 2.0 * M * (Kp // 4 * 3.0) / c["BYTES_PER_US"]
+        t += c["T_LAUNCH"] + 2.0 * (-(-M // 32) * 32) * (Kp // 4 * 3.0) / c["BYTES_PER_US"]
     if S > 1:
         t += c["T_LAUNCH"] + (4.0 * S * M * N + 2.0 * M * N) / c["BYTES_PER_US"]
     return t
@@ -49,17 +49,22 @@ def plan_time_us(c, tile, M, N, Kp, S, repack):
 
 def best_plan(c, M, N, Kp):
     """(tile, S, repack) with the least predicted time, visiting plans from the simplest and
-    requiring a PLAN_MIN_GAIN lead to replace an earlier one (as plan.cpp does)."""
+    requiring a PLAN_MIN_GAIN lead to replace an earlier one (as plan.cpp does). Regular shapes
+    (M % 32 == 0, N % 128 == 0) take the tiles whose MT divides M (the last tile column masked
+    when NT does not divide N, visited after every dividing plan); ragged ones any tile, masked."""
     best, best_t = ((128, 128, 2, 2), 1, False), None
     kt = Kp // K_TILE
-    for rp in (False, True):
-        for S in range(1, min(MAX_SPLITS, kt) + 1):
-            for tile in (SKINNY if M % 128 else TILES):
-                if M % tile[0] or N % tile[1]:
-                    continue
-                t = plan_time_us(c, tile, M, N, Kp, S, rp)
-                if best_t is None or t < best_t * (1.0 - PLAN_MIN_GAIN):
-                    best, best_t = (tile, S, rp), t
+    regular = M % 32 == 0 and N % 128 == 0
+    cands = (SKINNY if M % 128 else TILES) if regular else TILES + SKINNY
+    for masked in ((False, True) if regular else (None,)):
+        for rp in (False, True):
+            for S in range(1, min(MAX_SPLITS, kt) + 1):
+                for tile in cands:
+                    if regular and (M % tile[0] or bool(N % tile[1]) != masked):
+                        continue
+                    t = plan_time_us(c, tile, M, N, Kp, S, rp)
+                    if best_t is None or t < best_t * (1.0 - PLAN_MIN_GAIN):
+                        best, best_t = (tile, S, rp), t
     return best
 
 

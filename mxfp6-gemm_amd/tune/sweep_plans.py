@@ -1,6 +1,7 @@
 """Measure every execution plan of libmxfp6gemm on the GPU, for re-fitting the router's model.
 
-A plan is (tile, K segments S, A layout: 0 row-major, 1 repacked first); each is timed through
+A plan is (tile, K segments S, A layout: 0 row-major, 1 repacked first; a tile that does not
+divide M x N runs masked); each is timed through
 mxfp6_gemm_explicit on FP16 output as the best mean of 3 x 20 back-to-back launches after 5
 warm-ups. One JSON line per shape: {"shape": [M, N, K], "plans": [[us, tile, S, a_layout], ...]}
 sorted by time.
@@ -43,14 +44,17 @@ def sweep(M, N, K):
     dA = torch.from_numpy(p.a_packed).cuda()
     D = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
     res = []
+    regular = M % 32 == 0 and N % 128 == 0
     for t in TILES:
-        # the router offers the skinny tiles (fewer than 128 rows) exactly when M % 128 != 0
-        if M % t[0] or N % t[1] or (t[0] < 128) != (M % 128 != 0):
+        # the plans the router considers: on a regular shape (M % 32 == 0, N % 128 == 0) the
+        # tiles whose MT divides M, the skinny ones (fewer than 128 rows) exactly when
+        # M % 128 != 0, N masked when NT does not divide it; on a ragged shape every tile
+        if regular and (M % t[0] or (t[0] < 128) != (M % 128 != 0)):
             continue
         bsh, sa, sb = p.layouts(t)
         dB, dsa, dsb = (torch.from_numpy(x).cuda() for x in (bsh, sa, sb))
         for S in SPLITS:
-            if S > kt or (S > 1 and (M // t[0]) * (N // t[1]) * S > 2048):
+            if S > kt or (S > 1 and -(-M // t[0]) * -(-N // t[1]) * S > 2048):
                 continue
             for rp in (0, 1):
                 wsb = mx.plan_workspace_size(M, N, p.Kp, S, rp)

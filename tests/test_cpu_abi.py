@@ -53,33 +53,44 @@ def test_argument_checks_reject_before_launch(mx):
     p = 0x1000  # never dereferenced: every call below must fail validation first
     assert mx.gemm(0, 128, 128, 192, 0, p, p, p, p, 144) == 1            # null A
     assert mx.gemm(3, 128, 128, 192, p, p, p, p, p, 144) == 3            # bad out type
-    assert mx.gemm(0, 100, 128, 192, p, p, p, p, p, 144) == 2            # M % 128
+    assert mx.gemm(0, 0, 128, 192, p, p, p, p, p, 144) == 2              # M = 0
+    assert mx.gemm(0, 128, -5, 192, p, p, p, p, p, 144) == 2             # N < 0
     assert mx.gemm(0, 128, 128, 200, p, p, p, p, p, 144) == 2            # Kp % 192
     assert mx.gemm(0, 128, 128, 192, p, p, p, p, p, 6) == 2              # A row too short
     assert mx.gemm(0, 128, 128, 192, p, p, p, p, p, 146) == 2            # A row misaligned
     assert mx.gemm_force_tile(0, 128, 128, 192, (128, 384, 4, 3), p, p, p, p, p, 144) == 4
     assert mx.gemm_force_tile(0, 256, 256, 192, (256, 128, 4, 2), p, p, p, p, p, 144) == 4  # not instantiated
+    assert mx.gemm_force_tile(0, 100, 128, 192, (128, 128, 2, 2), p, p, p, p, p, 144) == 4  # ragged
+    assert mx.gemm_explicit(0, 100, 100, 192, (256, 128, 4, 2), 1, p, p, p, p, p, 144) == 4
+    assert mx.gemm_explicit(0, 100, 100, 192, (128, 128, 2, 2), 2, p, p, p, p, p, 144) == 5  # no ws
     assert mx.gemm_direct(0, 128, 128, 192, 5, 2, p, p, p, p, p, 144) == 5
     assert mx.gemm_direct(0, 128, 128, 192, 2, 2, p, p, p, p, p, 144, splits=2) == 5
+    assert mx.gemm_direct(0, 96, 128, 192, 1, 1, p, p, p, p, p, 144) == 2   # M % 64
+    assert mx.gemm_direct(0, 128, 100, 192, 1, 1, p, p, p, p, p, 144) == 2  # N % 64
 
 
 def test_prep_argument_checks_reject_before_launch(mx):
     p = 0x1000  # 16-byte aligned, never dereferenced
     assert mx.quantize_dev(0, 4, 64, p, 48, p, 2) == 1                  # null input
-    assert mx.quantize_dev(p, 4, 48, p, 36, p, 2) == 2                  # cols % 32
+    assert mx.quantize_dev(p, 0, 48, p, 48, p, 2) == 2                  # no rows
     assert mx.quantize_dev(p, 4, 64, p, 44, p, 2) == 2                  # row shorter than codes
+    assert mx.quantize_dev(p, 4, 40, p, 44, p, 2) == 2                  # ragged K: 2 blocks
     assert mx.quantize_dev(p, 4, 64, p, 50, p, 2) == 2                  # row stride % 4
-    assert mx.quantize_dev(p, 4, 64, p, 48, p, 1) == 2                  # too few scale columns
-    assert mx.quantize_dev(p + 4, 4, 64, p, 48, p, 2) == 5              # input not 16-byte aligned
-    assert mx.prepare_a_dev(p, 96, 64, 2, p, 48, p) == 2                # M % (32 * group)
+    assert mx.quantize_dev(p, 4, 40, p, 48, p, 1) == 2                  # too few scale columns
+    assert mx.quantize_dev(p + 2, 4, 64, p, 48, p, 2) == 5              # input not 4-byte aligned
+    assert mx.prepare_a_dev(p, 0, 64, 2, p, 48, p) == 2                 # M = 0
+    assert mx.prepare_a_dev(p, 96, 40, 2, p, 44, p) == 2                # row shorter than codes
     assert mx.prepare_a_dev(p, 128, 64, 5, p, 48, p) == 5               # group
-    assert mx.prepare_b_dev(p, 64, 96, 2, p, p) == 2                    # N % (32 * group)
-    assert mx.prepare_b_dev(p, 60, 64, 2, p, p) == 2                    # K % 32
+    assert mx.prepare_b_dev(p, 64, 0, 2, p, p) == 2                     # N = 0
+    assert mx.prepare_b_dev(p, -1, 64, 2, p, p) == 2                    # K < 0
     assert mx.prepare_b_dev(p, 64, 64, 2, p + 8, p) == 5                # Bsh not 16-byte aligned
-    assert mx.tile_scales_dev(p, 64, 64, 1, 2, p) == 2                  # ld < K/32
+    assert mx.tile_scales_dev(p, 64, 64, 1, 2, p) == 2                  # ld < ceil(K/32)
+    assert mx.tile_scales_dev(p, 64, 40, 1, 2, p) == 2
     assert mx.tile_scales_dev(0, 64, 64, 2, 2, p) == 1
-    # layout sizes at kpad(K)
-    assert mx.preshuffled_bytes(64, 1000) == 0
-    assert mx.preshuffled_bytes(64, 992) == 2 * (1152 // 64) * 1536
+    # layout sizes at kpad(K); ragged dims round up to 32-row blocks and whole scale groups
+    assert mx.preshuffled_bytes(0, 64) == 0
+    assert mx.preshuffled_bytes(64, 1000) == 2 * (1152 // 64) * 1536
+    assert mx.preshuffled_bytes(50, 992) == 2 * (1152 // 64) * 1536
     assert mx.tiled_scale_bytes(96, 992, 3) == 1 * (1152 // 192) * 64 * 3 * 4
-    assert mx.tiled_scale_bytes(96, 992, 2) == 0
+    assert mx.tiled_scale_bytes(96, 992, 2) == 2 * (1152 // 192) * 64 * 3 * 4
+    assert mx.tiled_scale_bytes(1, 33, 4) == 1 * 1 * 64 * 3 * 4

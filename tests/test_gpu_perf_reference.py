@@ -35,6 +35,12 @@ WORKLOADS = {
     "s2048x1024x4096": (2048, 1024, 4096, mx.OUT_F16, (mx.DIST_NORMAL, 1.0), (mx.DIST_NORMAL, 1.0)),
     "s1024x4096x8192": (1024, 4096, 8192, mx.OUT_F16, (mx.DIST_NORMAL, 1.0), (mx.DIST_NORMAL, 1.0)),
     "s4096x4096x1024": (4096, 4096, 1024, mx.OUT_F16, (mx.DIST_NORMAL, 1.0), (mx.DIST_NORMAL, 1.0)),
+    # N a multiple of 128 but not of 256: the reference's masked 256x256 route (NMASK,
+    # src/kernel.hpp:144-154; README.md:270-279 quotes N = 102272)
+    "s8192x896x8192": (8192, 896, 8192, mx.OUT_F16, (mx.DIST_NORMAL, 1.0), (mx.DIST_NORMAL, 1.0)),
+    "s4096x2432x8192": (4096, 2432, 8192, mx.OUT_F16, (mx.DIST_NORMAL, 1.0), (mx.DIST_NORMAL, 1.0)),
+    "s2048x102272x1024": (2048, 102272, 1024, mx.OUT_F16, (mx.DIST_NORMAL, 1.0),
+                          (mx.DIST_NORMAL, 1.0)),
 }
 
 
