@@ -52,12 +52,17 @@ size_t mxfp6_gemm_workspace_size(int M, int N, int Kp);
 int mxfp6_splitk_segments(int M, int N, int Kp);
 
 /* gemm(ot, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, B_row_bytes, ws, ws_bytes) on the
- * null stream. Same arguments and semantics as gemm.hpp:63-64 / gemm.cpp:65-83, and shapes:
- * N a multiple of 128; M a multiple of 128, or (beyond the reference) of 32, routed to 32- and
- * 64-row tiles (the scales tiled with the MPW choose_tile returns for that M). Plus a status:
- * a shape that would split with a NULL or short workspace runs unsplit (stderr warning, status
- * MXFP6_OK), as the reference does. A workspace too short for the repacked A (but long enough
- * for the partials) only skips the repack: same result, slower. */
+ * null stream. Same arguments and semantics as gemm.hpp:63-64 / gemm.cpp:65-83 on the
+ * reference's shapes (M, N multiples of 128). Beyond the reference, any M, N >= 1: M a multiple
+ * of 32 routes to 32- and 64-row tiles, and a tile that does not divide M x N runs with its last
+ * tile row / column masked (the reference's NMASK, src/kernel.hpp:144-154, generalised). The
+ * operand layouts then hold ceil(dim/32) 32-row blocks and whole scale groups, completed with
+ * zero rows (codes 0, scale code 127): mxfp6_preshuffled_bytes / mxfp6_tiled_scale_bytes size
+ * them, mxfp6_prepare_* and mxfp6_prepare_b / mxfp6_prepare_scales produce them. The scales are
+ * tiled with the MPW / NPW choose_tile returns for the shape. Plus a status: a shape that would
+ * split with a NULL or short workspace runs unsplit (stderr warning, status MXFP6_OK), as the
+ * reference does. A workspace too short for the repacked A (but long enough for the partials)
+ * only skips the repack: same result, slower. */
 int mxfp6_gemm(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
                const uint8_t* dsA, const uint8_t* dsB, void* dD, int A_row_bytes, int B_row_bytes,
                void* ws, size_t ws_bytes);
@@ -69,13 +74,14 @@ int mxfp6_gemm_async(int out_type, int M, int N, int Kp, const void* dA, const v
 
 /* gemm_force_tile: run the tile {MT, NT, MPW, NPW} given by the caller instead of the router's
  * choice, unsplit. Test-only in the reference (src/gemm.cpp:85-107, not in its header); the
- * scales must be tiled with this tile's MPW/NPW. Rejects tiles the library does not implement. */
+ * scales must be tiled with this tile's MPW/NPW. Rejects tiles the library does not implement
+ * and tiles that do not divide M x N (mxfp6_gemm_explicit runs those masked). */
 int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4], const void* dA,
                           const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
                           int A_row_bytes, int B_row_bytes, void* stream);
 
-/* Run an explicit plan: the pipelined kernel with tile {MT, NT, MPW, NPW}, `splits` K segments and
- * an A layout: 0 = row-major A (A_row_bytes per row); 1 = repack row-major A into the workspace in
+/* Run an explicit plan: the pipelined kernel with tile {MT, NT, MPW, NPW} (masked when it does
+ * not divide M x N), `splits` K segments and an A layout: 0 = row-major A (A_row_bytes per row); 1 = repack row-major A into the workspace in
  * the preshuffled operand layout first, then read that; 2 = dA already holds A in the preshuffled
  * layout (mxfp6_preshuffle_rows_async output; A_row_bytes is then only checked). Needs ws of
  * mxfp6_plan_workspace_size(M, N, Kp, splits, a_layout == 1) bytes. For tuning, benchmarks and
@@ -94,17 +100,18 @@ int mxfp6_gemm_repacks_a(int M, int N, int Kp);
 /* Workspace bytes of an explicit plan (0 when splits == 1 and a_repack == 0). */
 size_t mxfp6_plan_workspace_size(int M, int N, int Kp, int splits, int a_repack);
 
-/* On-device preshuffle of `rows` (multiple of 32) row-major packed rows, each read for packed(Kp)
- * bytes from src + r * row_bytes, into dst (rows * packed(Kp) bytes) in the layout of
- * preshuffle_B (reference include/mxfp6/preprocess.hpp:182-207, which runs on the host). Used by
- * gemm() to repack A; applied to B^T it gives preshuffle_B's output on the GPU. */
+/* On-device preshuffle of `rows` row-major packed rows, each read for packed(Kp) bytes from
+ * src + r * row_bytes, into dst (ceil(rows/32) * 32 * packed(Kp) bytes; rows past `rows` in the
+ * last 32-row block are zero codes) in the layout of preshuffle_B (reference
+ * include/mxfp6/preprocess.hpp:182-207, which runs on the host). Used by gemm() to repack A;
+ * applied to B^T it gives preshuffle_B's output on the GPU. */
 int mxfp6_preshuffle_rows_async(const void* src, int row_bytes, int rows, int Kp, void* dst,
                                 void* stream);
 
 /* The direct kernel (one wave per 32x32 block, operands read straight from global memory, any
- * scale grouping mpw/npw in 1..4) with an explicit K split count. A second, independent GPU
- * implementation used to cross-check the pipelined kernels; no counterpart in the reference.
- * splits > 1 needs ws of splits*M*N*4 bytes. */
+ * scale grouping mpw/npw in 1..4) with an explicit K split count; M and N multiples of 64. A
+ * second, independent GPU implementation used to cross-check the pipelined kernels; no
+ * counterpart in the reference. splits > 1 needs ws of splits*M*N*4 bytes. */
 int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, int npw, const void* dA,
                       const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
                       int A_row_bytes, int splits, void* ws, size_t ws_bytes, void* stream);
@@ -150,38 +157,44 @@ int mxfp6_tile_scale(const uint8_t* pscale, int dim, int K, int group, int subs,
 
 /* ---- the same formats produced on the device (one HBM pass over float operands) ------------
  * The reference has host loops only; these are their device counterparts, bit-identical to them.
- * Inputs and outputs are device pointers; the calls are asynchronous on `stream`. */
+ * Inputs and outputs are device pointers; the calls are asynchronous on `stream`. Beyond the
+ * reference (which needs K % 32 == 0 and whole 32-row blocks), any sizes >= 1: a K that is not a
+ * multiple of 32 is quantised as if zero-padded to one (nb = ceil(K/32) blocks, 24 bytes each),
+ * and dims that do not fill a 32-row block or a scale group are completed with zero rows
+ * (codes 0, scale code 127) in the preshuffled and tiled outputs. Float inputs are 4-byte
+ * aligned (16-byte aligned with a row length that is a multiple of 4 reads them as float4). */
 
-/* quantize_to_mxfp6 (preprocess.hpp:51-97) of row-major float d_x[rows][cols] (cols % 32 == 0,
- * d_x 16-byte aligned): row r's 3*cols/4 code bytes at d_packed + r * packed_row_bytes (>= 3*cols/4,
- * a multiple of 4; the bytes past the codes are set to 0), scales at d_scales[r * scale_cols + c]
- * (scale_cols >= cols/32; columns past cols/32 set to 127, as pad_scales_k, :32-38, does). */
+/* quantize_to_mxfp6 (preprocess.hpp:51-97) of row-major float d_x[rows][cols]: row r's
+ * 24 * ceil(cols/32) code bytes at d_packed + r * packed_row_bytes (at least that, a multiple of 4;
+ * the bytes past the codes are set to 0), scales at d_scales[r * scale_cols + c]
+ * (scale_cols >= ceil(cols/32); columns past the values set to 127, as pad_scales_k, :32-38,
+ * does). */
 int mxfp6_quantize_async(const float* d_x, int rows, int cols, void* d_packed,
                          size_t packed_row_bytes, uint8_t* d_scales, int scale_cols, void* stream);
 
-/* A operand ready for mxfp6_gemm: quantize_to_mxfp6 of d_A[M][K] (K % 32 == 0) into rows of
- * a_row_bytes (>= 3*K/4, a multiple of 4; bytes past the codes zero: a_row_bytes = 3*kpad(K)/4
+/* A operand ready for mxfp6_gemm: quantize_to_mxfp6 of d_A[M][K] into rows of a_row_bytes
+ * (>= 24 * ceil(K/32), a multiple of 4; bytes past the codes zero: a_row_bytes = 3*kpad(K)/4
  * gives padded rows with a zero K-tail), and the scales padded to kpad(K) and tiled as
  * tile_scale(preprocess_scale(pad_scales_k(..)), group, 3) (:32-38, :136-162, :216-233) with
- * group = the tile's MPW; M % (32 * group) == 0. d_tiled holds mxfp6_tiled_scale_bytes(M, K,
- * group) bytes. */
+ * group = the tile's MPW. d_tiled holds mxfp6_tiled_scale_bytes(M, K, group) bytes. */
 int mxfp6_prepare_a_async(const float* d_A, int M, int K, int group, void* d_packed,
                           size_t a_row_bytes, uint8_t* d_tiled, void* stream);
 
 /* B operand ready for mxfp6_gemm from row-major float d_B[K][N]: preprocess_B (:112-118), K
  * padded to kpad(K) with zero codes, preshuffle_B (:182-207) into d_bsh
  * (mxfp6_preshuffled_bytes(N, K) bytes, 16-byte aligned), and the scales tiled as for A with
- * group = the tile's NPW; N % (32 * group) == 0. */
+ * group = the tile's NPW. */
 int mxfp6_prepare_b_async(const float* d_B, int K, int N, int group, void* d_bsh,
                           uint8_t* d_tiled, void* stream);
 
-/* Scales already quantised: d_scales[dim][ld] (K/32 valid columns) -> padded to kpad(K) and
- * tiled (group) as above. */
+/* Scales already quantised: d_scales[dim][ld] (ceil(K/32) valid columns) -> padded to kpad(K)
+ * and tiled (group) as above. */
 int mxfp6_tile_scales_async(const uint8_t* d_scales, int dim, int K, int ld, int group,
                             uint8_t* d_tiled, void* stream);
 
-/* Sizes of the device layouts at kpad(K): preshuffled operand (dim/32 * kpad(K)/64 * 1536) and
- * tiled scales (tile_scale(.., group, 3)). 0 for shapes the layouts cannot hold. */
+/* Sizes of the device layouts at kpad(K): preshuffled operand (ceil(dim/32) * kpad(K)/64 * 1536)
+ * and tiled scales (tile_scale(.., group, 3) over ceil(dim / (32 * group)) groups). 0 for
+ * dim, K < 1 or a group outside 1..4. */
 size_t mxfp6_preshuffled_bytes(int dim, int K);
 size_t mxfp6_tiled_scale_bytes(int dim, int K, int group);
 
@@ -209,9 +222,12 @@ int mxfp6_gen_values(int rows, int K, int dist, double sigma, uint64_t seed, uin
                      float* out, int nthreads);
 
 /* Prepare kernel-ready device-layout buffers on the host from raw packed codes and scales:
- *   B: packed B^T[N][b_row_bytes] (Kp codes per row) -> preshuffled bsh (N/32 * Kp/64 * 1536 B)
- *   scales[dim][Kp/32] -> tiled (preprocess_scale then tile_scale(group, 3)).
- * Multi-threaded versions of preshuffle_B and tile_scale(preprocess_scale(..)). */
+ *   B: packed B^T[N][b_row_bytes] (Kp codes per row) -> preshuffled bsh
+ *      (ceil(N/32) * Kp/64 * 1536 B; zero codes past N)
+ *   scales[dim][Kp/32] -> tiled (preprocess_scale then tile_scale(group, 3)) over
+ *      ceil(dim / (32 * group)) groups (code 127 past dim).
+ * Multi-threaded versions of preshuffle_B and tile_scale(preprocess_scale(..)), extended to
+ * ragged dims as the device producers are. */
 int mxfp6_prepare_b(const uint8_t* packed, int N, int Kp, size_t b_row_bytes, uint8_t* bsh,
                     int nthreads);
 int mxfp6_prepare_scales(const uint8_t* scales, int dim, int Kp, int group, uint8_t* tiled,
