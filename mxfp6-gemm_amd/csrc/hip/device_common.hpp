@@ -50,6 +50,13 @@ __device__ __forceinline__ __hip_bfloat16 cvt_out<__hip_bfloat16>(float v) {
     return __float2bfloat16(v);
 }
 
+// The 16 bits of an FP16 / BF16 value, zero-extended.
+template <typename T>
+__device__ __forceinline__ uint32_t half_bits(T h) {
+    static_assert(sizeof(T) == 2, "16-bit type");
+    return __builtin_bit_cast(uint16_t, h);
+}
+
 // First K-tile and K-tile count of split segment z when k_tiles tiles are divided into S
 // segments: the first k_tiles % S segments take one extra tile.
 __device__ __forceinline__ void split_segment(int k_tiles, int S, int z, int& kt0, int& nkt) {
