@@ -332,3 +332,28 @@ def test_reference_library_same_inputs(g, orc, ref_lib, M, N, K, out_type):
     checks.check(theirs[rows], R, ab, out_type)
     same = float((ours.view(np.uint32) == theirs.view(np.uint32)).mean())
     g.say(f"    bit-identical to the reference library: {100 * same:.2f}% of elements")
+
+
+# ---- FP16/BF16 epilogue: exactly the rounded FP32 result ------------------------------------
+
+@pytest.mark.parametrize("tile", [(256, 256, 4, 4), (256, 256, 2, 4), (256, 192, 4, 3),
+                                  (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2),
+                                  (64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1),
+                                  (32, 128, 1, 1)])
+@pytest.mark.parametrize("M,N", [(256, 768), (289, 418), (97, 419)])
+def test_lowp_output_is_rounded_f32(g, tile, M, N):
+    """Every tile, unsplit: the FP16 and BF16 outputs equal the FP32 output of the same plan
+    rounded to nearest-even on the host, bit for bit (the lane-pair exchange of the 16-bit
+    epilogue moves every value to its row and column; N odd takes the element stores)."""
+    import torch
+    K = 1056
+    p = mx.make_problem(M, N, K, dist_a=mx.DIST_STUDENT_T3, dist_b=mx.DIST_STUDENT_T3,
+                        seed=M + N)
+    dp = g.DevProblem(p, tile)
+    D32 = g.run_explicit(dp, mx.OUT_F32)
+    D16 = g.run_explicit(dp, mx.OUT_F16)
+    Db16 = g.run_explicit(dp, mx.OUT_BF16)
+    want16 = D32.astype(np.float16).astype(np.float32)
+    assert np.array_equal(D16.view(np.uint32), want16.view(np.uint32))
+    wantb = checks.round_bf16(D32)
+    assert np.array_equal(Db16.view(np.uint32), wantb.view(np.uint32))
