@@ -26,15 +26,15 @@
 // Kernels (all HBM-bound; algorithmic bytes = 4 per value read + 0.75 per value and 1/32 per
 // scale written):
 //   prep_rows_kernel  row-major float [rows][cols] -> packed rows (+ zero tail up to row_bytes) and
-//                     scales, raw [rows][scale_cols] (tail columns 127) or tiled at Kp. A wave
-//                     takes 64 consecutive 32-blocks of one row: coalesced float4 loads into LDS,
-//                     then lane l quantises block l and writes its 24 bytes (consecutive lanes,
-//                     consecutive bytes).
+//                     scales, raw [rows][scale_cols] (tail columns 127) or tiled at Kp. A
+//                     one-wave workgroup takes 64 consecutive 32-blocks of one row: coalesced
+//                     float4 loads into LDS, then lane l quantises block l and writes its 24
+//                     bytes (consecutive lanes, consecutive bytes).
 //   prep_b_kernel     row-major float B [K][N] -> preshuffled B^T at Kp + tiled scales. Lane n of
 //                     a wave takes column n and one 32-block: 32 loads each coalesced across the
 //                     wave's 64 consecutive columns; its 24 bytes land at 16t / 1024 + 8t of the
 //                     column's tile, so the wave's stores are contiguous too.
-//   tile_scales_kernel raw scales [dim][ld] (K/32 valid columns) -> tiled at Kp.
+//   tile_scales_kernel raw scales [dim][ld] (ceil(K/32) valid columns) -> tiled at Kp.
 #pragma once
 #include "device_common.hpp"
 
@@ -115,60 +115,11 @@ struct ScaleOut {
     int group, ktn;  // tiled
 };
 
-// Wave tasks: (row r, chunk) for r < rows_out and chunk < chunks = ceil(nblk / 64), row-major,
-// 4 per workgroup (grid = ceil(rows_out * chunks / 4)); a task covers blocks 64 * chunk .. +63 of
-// its row. Rows rows .. rows_out-1 are zero rows that complete the last scale group of a tiled
-// output (no packed bytes). Block c of row r (c < nblk) writes the codes of values 32c .. 32c+31
-// (zero past cols; zero bytes for a block past the values), cut at row_bytes, and the scale
-// column c if c < so.ncols (127 for a block without values). V4: cols % 4 == 0 and x 16-byte
-// aligned (float4 loads); otherwise one float per lane per load.
-template <bool V4>
-__global__ void __launch_bounds__(PREP_THREADS)
-    prep_rows_kernel(const float* __restrict__ x, int cols, int nblk, uint8_t* __restrict__ packed,
-                     size_t row_bytes, ScaleOut so, int chunks, int rows, int rows_out) {
-    __shared__ float stage[PREP_THREADS / 64][PREP_BLKS_PER_WAVE * 33];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const size_t task = (size_t)blockIdx.x * (PREP_THREADS / 64) + wave;
-    const int r = (int)(task / chunks), chunk = (int)(task - (size_t)r * chunks);
-    const bool live = r < rows_out, data = r < rows;
-    const int blk0 = chunk * PREP_BLKS_PER_WAVE;
-    const int vblk = (cols + 31) / 32;  // blocks holding values
-    const float* xr = x + (size_t)r * cols;
-    float* st = stage[wave];
-    // coalesced loads of the wave's 2048 values, block-padded in LDS
-    if (data && blk0 < vblk) {
-        if constexpr (V4) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int p = 4 * (lane + 64 * j);  // value index within the wave's range
-                const int b = p >> 5, i = p & 31, e = blk0 * 32 + p;
-                v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (e < cols) v = *reinterpret_cast<const v4f*>(xr + e);
-                st[b * 33 + i] = v[0];
-                st[b * 33 + i + 1] = v[1];
-                st[b * 33 + i + 2] = v[2];
-                st[b * 33 + i + 3] = v[3];
-            }
-        } else {
-#pragma unroll 8
-            for (int j = 0; j < 32; j++) {
-                const int p = lane + 64 * j, e = blk0 * 32 + p;
-                st[(p >> 5) * 33 + (p & 31)] = e < cols ? xr[e] : 0.0f;
-            }
-        }
-    }
-    __syncthreads();
-    const int c = blk0 + lane;
-    if (!live || c >= nblk) return;
-    uint32_t w[6] = {0, 0, 0, 0, 0, 0};
-    int code = 127;
-    if (data && c < vblk) {
-        float v[32];
-#pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = st[lane * 33 + i];
-        code = quant32(v, w);
-    }
-    // packed bytes [24c, 24c + 24) of the row, cut at row_bytes (row_bytes % 4 == 0)
+// Packed bytes [24c, 24c + 24) of row r (cut at row_bytes, a multiple of 4) and scale column c
+// (if c < so.ncols) of block c.
+__device__ __forceinline__ void put_block(uint8_t* __restrict__ packed, size_t row_bytes,
+                                          const ScaleOut& so, int r, int c, bool data,
+                                          const uint32_t (&w)[6], int code) {
     const size_t o = (size_t)24 * c;
     if (data && o < row_bytes) {
         uint32_t* dst = reinterpret_cast<uint32_t*>(packed + (size_t)r * row_bytes + o);
@@ -182,6 +133,70 @@ __global__ void __launch_bounds__(PREP_THREADS)
             put_tiled_scale(so.p, r, c, so.group, so.ktn, code);
         else
             so.p[(size_t)r * so.ncols + c] = (uint8_t)code;
+    }
+}
+
+// One wave per workgroup (no barrier across waves); workgroup = task (row r, chunk), row-major,
+// r < rows_out, chunk < chunks = ceil(vblk / 64) with vblk = ceil(cols / 32) the blocks holding
+// values. A task quantises the value blocks 64 chunk .. +63 of its row (lane l: block
+// 64 chunk + l); the last chunk also writes the blocks vblk .. nblk-1 past the values (zero
+// codes, scale 127), so no workgroup is spent on a K-tail alone. Rows rows .. rows_out-1 are zero
+// rows that complete the last scale group of a tiled output (scales only). Block c of row r
+// (c < nblk) writes the codes of values 32c .. 32c+31 (zero past cols), cut at row_bytes, and the
+// scale column c if c < so.ncols. V4: cols % 4 == 0 and x 16-byte aligned (float4 loads);
+// otherwise one float per lane per load.
+template <bool V4>
+__global__ void __launch_bounds__(64)
+    prep_rows_kernel(const float* __restrict__ x, int cols, int nblk, uint8_t* __restrict__ packed,
+                     size_t row_bytes, ScaleOut so, int chunks, int rows) {
+    constexpr int BPW = PREP_BLKS_PER_WAVE;  // blocks per task, one per lane
+    __shared__ float stage[BPW * 33];
+    const int lane = threadIdx.x;
+    const int r = (int)(blockIdx.x / (unsigned)chunks);
+    const int chunk = (int)(blockIdx.x - (unsigned)r * chunks);
+    const bool data = r < rows;
+    const int blk0 = chunk * BPW;
+    const int vblk = (cols + 31) / 32;
+    const float* xr = x + (size_t)r * cols;
+    // coalesced loads of the task's values, block-padded in LDS
+    if (data) {
+        if constexpr (V4) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int p = 4 * (lane + 64 * j);  // value index within the task's range
+                const int b = p >> 5, i = p & 31, e = blk0 * 32 + p;
+                v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (e < cols) v = *reinterpret_cast<const v4f*>(xr + e);
+                stage[b * 33 + i] = v[0];
+                stage[b * 33 + i + 1] = v[1];
+                stage[b * 33 + i + 2] = v[2];
+                stage[b * 33 + i + 3] = v[3];
+            }
+        } else {
+#pragma unroll 8
+            for (int j = 0; j < 32; j++) {
+                const int p = lane + 64 * j, e = blk0 * 32 + p;
+                stage[(p >> 5) * 33 + (p & 31)] = e < cols ? xr[e] : 0.0f;
+            }
+        }
+    }
+    __syncthreads();
+    const int c = blk0 + lane;
+    if (c < nblk) {
+        uint32_t w[6] = {0, 0, 0, 0, 0, 0};
+        int code = 127;
+        if (data && c < vblk) {
+            float v[32];
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = stage[lane * 33 + i];
+            code = quant32(v, w);
+        }
+        put_block(packed, row_bytes, so, r, c, data, w, code);
+    }
+    if (chunk == chunks - 1) {
+        const uint32_t z[6] = {0, 0, 0, 0, 0, 0};
+        for (int cz = blk0 + BPW + lane; cz < nblk; cz += 64)
+            put_block(packed, row_bytes, so, r, cz, data, z, 127);
     }
 }
 
