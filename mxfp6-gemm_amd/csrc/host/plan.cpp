@@ -37,13 +37,15 @@ namespace plan {
 //              lines per 128 bytes instead of 1);
 //   t_wg     = T_WG + slabs * t_slab + T_OUT_KB * output KiB * per_cu;
 //   t        = T_LAUNCH + waves * t_wg, plus for a repack T_LAUNCH + its bytes (A read and written)
-//              at BYTES_PER_US, and for a split T_LAUNCH + the partials written and read back.
+//              at REPACK_BYTES_PER_US, and for a split T_LAUNCH + the partials written and read
+//              back at SPLIT_BYTES_PER_US.
 // The constants are a least-squares fit (log time) to every plan of the 56 measured shapes with
 // M % 128 == 0 (one MI355X; M from 128 to 8192, N from 256 to 102272, K from 1024 to 105728,
-// masked N included): the plan the model picks is within 1.1% of the measured best on average,
-// 14% at worst (fixed rules were up to 2x off on small-K grids), and it is the measured best on
-// the five benchmark workloads. On the 14 skinny-M and 6 ragged shapes measured, the same
-// constants pick within 16% and 7% of the best.
+// masked N included), the repack rate the repack kernel's measured one. Re-measured on the
+// current kernels (71 shapes), the plan the model picks is within 1.1% of the measured best on
+// average, 13% at worst (fixed rules were up to 2x off on small-K grids), and within 1% of the
+// best on the five benchmark workloads. On the 14 skinny-M and 6 ragged shapes, the same constants
+// pick within 16% and 6% of the best.
 namespace {
 struct Plan {
     TileChoice tc;
@@ -69,8 +71,8 @@ double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repa
     const double out_kb = tc.MT * tc.NT * (S > 1 ? 4.0 : 2.0) / 1024.0;
     const double t_wg = T_WG + slabs * t_slab + T_OUT_KB * out_kb * per_cu;
     double t = T_LAUNCH + (double)waves * t_wg;
-    if (repack) t += T_LAUNCH + 2.0 * ((M + 31) / 32 * 32) * (Kp / 4 * 3.0) / BYTES_PER_US;
-    if (S > 1) t += T_LAUNCH + (4.0 * S * M * N + 2.0 * M * N) / BYTES_PER_US;
+    if (repack) t += T_LAUNCH + 2.0 * ((M + 31) / 32 * 32) * (Kp / 4 * 3.0) / REPACK_BYTES_PER_US;
+    if (S > 1) t += T_LAUNCH + (4.0 * S * M * N + 2.0 * M * N) / SPLIT_BYTES_PER_US;
     return t;
 }
 

@@ -18,7 +18,8 @@ constexpr double T_SLAB_MIN = 0.25706;      // latency floor of one 64-wide K sl
 constexpr double T_MFMA = 0.011908;        // per MFMA per wave per slab, per workgroup on the busiest CU
 constexpr double T_COPY_KB = 0.011984;      // per KiB copied global->LDS per slab, per workgroup
 constexpr double T_OUT_KB = 0.017816;      // per KiB of output (FP16 tile or FP32 partial) per workgroup
-constexpr double BYTES_PER_US = 4.401662e6;   // repack and split-K partial traffic
+constexpr double REPACK_BYTES_PER_US = 5.5e6;        // A repack traffic (measured kernel rate)
+constexpr double SPLIT_BYTES_PER_US = 4.401662e6;   // split-K partials written and read back
 constexpr double A_ROWS_COST = 0.853373;    // extra copy cost per byte of a row-major A slab
 constexpr double PLAN_MIN_GAIN = 0.01;     // lead a more complex plan needs over a simpler one
 

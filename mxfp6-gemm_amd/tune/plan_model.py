@@ -18,11 +18,11 @@ K_TILE = 192
 MAX_SPLITS = 16
 TILES = [(256, 256, 4, 4), (256, 192, 4, 3), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2)]
 SKINNY = [(64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)]  # M % 128 != 0
-NAMES = ["T_LAUNCH", "T_WG", "T_SLAB_MIN", "T_MFMA", "T_COPY_KB", "T_OUT_KB", "BYTES_PER_US",
-         "A_ROWS_COST"]
+NAMES = ["T_LAUNCH", "T_WG", "T_SLAB_MIN", "T_MFMA", "T_COPY_KB", "T_OUT_KB", "REPACK_BYTES_PER_US",
+         "SPLIT_BYTES_PER_US", "A_ROWS_COST"]
 CONSTANTS = {"T_LAUNCH": 2.850807, "T_WG": 2.072229, "T_SLAB_MIN": 0.25706, "T_MFMA": 0.011908,
-             "T_COPY_KB": 0.011984, "T_OUT_KB": 0.017816, "BYTES_PER_US": 4.401662e6,
-             "A_ROWS_COST": 0.853373}
+             "T_COPY_KB": 0.011984, "T_OUT_KB": 0.017816, "REPACK_BYTES_PER_US": 5.5e6,
+             "SPLIT_BYTES_PER_US": 4.401662e6, "A_ROWS_COST": 0.853373}
 PLAN_MIN_GAIN = 0.01
 
 
@@ -41,9 +41,9 @@ def plan_time_us(c, tile, M, N, Kp, S, repack):
     t_wg = c["T_WG"] + slabs * t_slab + c["T_OUT_KB"] * out_kb * per_cu
     t = c["T_LAUNCH"] + waves * t_wg
     if repack:
-        t += c["T_LAUNCH"] + 2.0 * (-(-M // 32) * 32) * (Kp // 4 * 3.0) / c["BYTES_PER_US"]
+        t += c["T_LAUNCH"] + 2.0 * (-(-M // 32) * 32) * (Kp // 4 * 3.0) / c["REPACK_BYTES_PER_US"]
     if S > 1:
-        t += c["T_LAUNCH"] + (4.0 * S * M * N + 2.0 * M * N) / c["BYTES_PER_US"]
+        t += c["T_LAUNCH"] + (4.0 * S * M * N + 2.0 * M * N) / c["SPLIT_BYTES_PER_US"]
     return t
 
 
