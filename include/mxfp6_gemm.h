@@ -180,6 +180,14 @@ int mxfp6_quantize_async(const float* d_x, int rows, int cols, void* d_packed,
 int mxfp6_prepare_a_async(const float* d_A, int M, int K, int group, void* d_packed,
                           size_t a_row_bytes, uint8_t* d_tiled, void* stream);
 
+/* A operand straight into the preshuffled operand layout (the bytes mxfp6_preshuffle_rows_async
+ * would make of mxfp6_prepare_a_async's rows, i.e. preshuffle_B's layout, :182-207, applied to A)
+ * in d_ash (mxfp6_preshuffled_bytes(M, K) bytes, 16-byte aligned), scales as mxfp6_prepare_a_async.
+ * For mxfp6_gemm_explicit with a_layout = 2: a caller that quantises A on the device skips the
+ * repack of A. No counterpart in the reference (its A is row-major only). */
+int mxfp6_prepare_a_preshuffled_async(const float* d_A, int M, int K, int group, void* d_ash,
+                                      uint8_t* d_tiled, void* stream);
+
 /* B operand ready for mxfp6_gemm from row-major float d_B[K][N]: preprocess_B (:112-118), K
  * padded to kpad(K) with zero codes, preshuffle_B (:182-207) into d_bsh
  * (mxfp6_preshuffled_bytes(N, K) bytes, 16-byte aligned), and the scales tiled as for A with

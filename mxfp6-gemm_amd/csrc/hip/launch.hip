@@ -99,24 +99,37 @@ static int rows_in_groups(int dim, int group) {
 }
 
 extern "C" int mxfp6_hip_quantize_rows(const float* x, int rows, int cols, int nblk, void* packed,
-                                       size_t row_bytes, uint8_t* scales, int scale_mode,
-                                       int ncols, int group, int Kp, void* stream) {
-    // one wave per (row, 64 value blocks); the last chunk of a row also writes its K-tail blocks
-    const int vblk = (cols + 31) / 32;
-    const int rows_out = scale_mode ? rows_in_groups(rows, group) : rows;
-    const ScaleOut so{scales, scale_mode, ncols, group, Kp / 192};
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    uint8_t* pk = static_cast<uint8_t*>(packed);
+                                       size_t row_bytes, int preshuffled, uint8_t* scales,
+                                       int scale_mode, int ncols, int group, int Kp, void* stream) {
+    // one wave per (row, 64 value blocks); the last chunk of a row also writes its K-tail blocks;
     // one block per lane: more, smaller one-wave workgroups beat 2 or 4 blocks per lane (8192^2:
     // 76 us against 100 and 163 us; the LDS per workgroup bounds the waves per CU)
+    const int vblk = (cols + 31) / 32;
     const int chunks = (vblk + PREP_BLKS_PER_WAVE - 1) / PREP_BLKS_PER_WAVE;
+    const int rows32 = (rows + 31) / 32 * 32;
+    int rows_out = scale_mode ? rows_in_groups(rows, group) : rows;
+    if (preshuffled) rows_out = std::max(rows_out, rows32);
+    const PackedOut po{static_cast<uint8_t*>(packed), row_bytes, preshuffled ? Kp / 64 : 0, rows32};
+    const ScaleOut so{scales, scale_mode, ncols, group, Kp / 192};
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool v4 = cols % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    if (preshuffled && scale_mode == 1) {
+        // one whole output tile per wave (coalesced stores): 32-row blocks x 4 slabs per workgroup
+        const dim3 g((unsigned)((Kp / 64 + PSH_SLABS - 1) / PSH_SLABS), (unsigned)(rows_out / 32));
+        uint8_t* ash = static_cast<uint8_t*>(packed);
+        if (v4)
+            prep_rows_preshuffled_kernel<true><<<g, dim3(64 * PSH_SLABS), 0, st>>>(
+                x, rows, cols, Kp / 64, ash, rows32, so);
+        else
+            prep_rows_preshuffled_kernel<false><<<g, dim3(64 * PSH_SLABS), 0, st>>>(
+                x, rows, cols, Kp / 64, ash, rows32, so);
+        return hipGetLastError() == hipSuccess ? 0 : 2;
+    }
     const dim3 grid((unsigned)((size_t)rows_out * chunks));
-    if (cols % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0)
-        prep_rows_kernel<true><<<grid, dim3(64), 0, st>>>(x, cols, nblk, pk, row_bytes, so, chunks,
-                                                          rows);
+    if (v4)
+        prep_rows_kernel<true><<<grid, dim3(64), 0, st>>>(x, cols, nblk, po, so, chunks, rows);
     else
-        prep_rows_kernel<false><<<grid, dim3(64), 0, st>>>(x, cols, nblk, pk, row_bytes, so, chunks,
-                                                           rows);
+        prep_rows_kernel<false><<<grid, dim3(64), 0, st>>>(x, cols, nblk, po, so, chunks, rows);
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

@@ -30,6 +30,9 @@
 //                     one-wave workgroup takes 64 consecutive 32-blocks of one row: coalesced
 //                     float4 loads into LDS, then lane l quantises block l and writes its 24
 //                     bytes (consecutive lanes, consecutive bytes).
+//   prep_rows_preshuffled_kernel  row-major float A -> the preshuffled operand layout + tiled
+//                     scales: a workgroup stages 32 rows x 4 slabs in LDS, each wave then writes
+//                     one whole 1536-byte tile (lane t: row t % 32, 32-block half t / 32).
 //   prep_b_kernel     row-major float B [K][N] -> preshuffled B^T at Kp + tiled scales. Lane n of
 //                     a wave takes column n and one 32-block: 32 loads each coalesced across the
 //                     wave's 64 consecutive columns; its 24 bytes land at 16t / 1024 + 8t of the
@@ -115,18 +118,36 @@ struct ScaleOut {
     int group, ktn;  // tiled
 };
 
-// Packed bytes [24c, 24c + 24) of row r (cut at row_bytes, a multiple of 4) and scale column c
-// (if c < so.ncols) of block c.
-__device__ __forceinline__ void put_block(uint8_t* __restrict__ packed, size_t row_bytes,
-                                          const ScaleOut& so, int r, int c, bool data,
-                                          const uint32_t (&w)[6], int code) {
-    const size_t o = (size_t)24 * c;
-    if (data && o < row_bytes) {
-        uint32_t* dst = reinterpret_cast<uint32_t*>(packed + (size_t)r * row_bytes + o);
-        const int nd = (int)min((size_t)6, (row_bytes - o) / 4);
+// Packed output of prep_rows_kernel: row-major rows of row_bytes (k64n == 0), or the preshuffled
+// operand layout (k64n > 0 slabs per 32-row block; rows32 = rows rounded up to 32, the rows past the
+// data written as zero codes).
+struct PackedOut {
+    uint8_t* p;
+    size_t row_bytes;
+    int k64n, rows32;
+};
+
+// Packed codes of block c of row r and its scale column c (if c < so.ncols). Row-major: bytes
+// [24c, 24c + 24) of the row, cut at row_bytes (a multiple of 4), data rows only. Preshuffled:
+// the block's 24 bytes at 16t and 1024 + 8t of tile (r / 32, c / 2), t = r % 32 + 32 (c % 2).
+__device__ __forceinline__ void put_block(const PackedOut& po, const ScaleOut& so, int r, int c,
+                                          bool data, const uint32_t (&w)[6], int code) {
+    if (po.k64n > 0) {
+        if (r < po.rows32 && c < 2 * po.k64n) {
+            const int t = (r & 31) + ((c & 1) << 5);
+            uint8_t* tile = po.p + ((size_t)(r >> 5) * po.k64n + (c >> 1)) * OPBLK_BYTES;
+            *reinterpret_cast<v4i*>(tile + 16 * t) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+            *reinterpret_cast<v2i*>(tile + 1024 + 8 * t) = v2i{(int)w[4], (int)w[5]};
+        }
+    } else {
+        const size_t o = (size_t)24 * c;
+        if (data && o < po.row_bytes) {
+            uint32_t* dst = reinterpret_cast<uint32_t*>(po.p + (size_t)r * po.row_bytes + o);
+            const int nd = (int)min((size_t)6, (po.row_bytes - o) / 4);
 #pragma unroll
-        for (int d = 0; d < 6; d++)
-            if (d < nd) dst[d] = w[d];
+            for (int d = 0; d < 6; d++)
+                if (d < nd) dst[d] = w[d];
+        }
     }
     if (c < so.ncols) {
         if (so.tiled)
@@ -141,14 +162,15 @@ __device__ __forceinline__ void put_block(uint8_t* __restrict__ packed, size_t r
 // values. A task quantises the value blocks 64 chunk .. +63 of its row (lane l: block
 // 64 chunk + l); the last chunk also writes the blocks vblk .. nblk-1 past the values (zero
 // codes, scale 127), so no workgroup is spent on a K-tail alone. Rows rows .. rows_out-1 are zero
-// rows that complete the last scale group of a tiled output (scales only). Block c of row r
-// (c < nblk) writes the codes of values 32c .. 32c+31 (zero past cols), cut at row_bytes, and the
-// scale column c if c < so.ncols. V4: cols % 4 == 0 and x 16-byte aligned (float4 loads);
+// rows that complete the last 32-row block of a preshuffled output and the last scale group of a
+// tiled one (zero codes, scale 127). Block c of row r (c < nblk) writes the codes of values
+// 32c .. 32c+31 (zero past cols) as put_block places them, and the scale column c if
+// c < so.ncols. V4: cols % 4 == 0 and x 16-byte aligned (float4 loads);
 // otherwise one float per lane per load.
 template <bool V4>
 __global__ void __launch_bounds__(64)
-    prep_rows_kernel(const float* __restrict__ x, int cols, int nblk, uint8_t* __restrict__ packed,
-                     size_t row_bytes, ScaleOut so, int chunks, int rows) {
+    prep_rows_kernel(const float* __restrict__ x, int cols, int nblk, PackedOut po, ScaleOut so,
+                     int chunks, int rows) {
     constexpr int BPW = PREP_BLKS_PER_WAVE;  // blocks per task, one per lane
     __shared__ float stage[BPW * 33];
     const int lane = threadIdx.x;
@@ -191,13 +213,77 @@ __global__ void __launch_bounds__(64)
             for (int i = 0; i < 32; i++) v[i] = stage[lane * 33 + i];
             code = quant32(v, w);
         }
-        put_block(packed, row_bytes, so, r, c, data, w, code);
+        put_block(po, so, r, c, data, w, code);
     }
     if (chunk == chunks - 1) {
         const uint32_t z[6] = {0, 0, 0, 0, 0, 0};
         for (int cz = blk0 + BPW + lane; cz < nblk; cz += 64)
-            put_block(packed, row_bytes, so, r, cz, data, z, 127);
+            put_block(po, so, r, cz, data, z, 127);
     }
+}
+
+// Row-major float A -> the preshuffled operand layout, one output tile per wave. Workgroup
+// (32-row block mb, 4 slabs from s0 = 4 * blockIdx.x): its 32 rows x 256 values are loaded with
+// coalesced float4 loads (each row's 1 KiB contiguous) into LDS; wave w then quantises slab s0 + w:
+// lane t = 32h + i takes row 32mb + i, 32-block 2(s0 + w) + h, and its 24 bytes land at 16t and
+// 1024 + 8t of tile (mb, s0 + w), so each wave writes one whole 1536-byte tile with two
+// contiguous stores. Rows >= rows (up to the 32-row block) and values >= cols are zeros; the
+// scales go to the tiled layout (scale_mode 1) as in prep_rows_kernel, rows up to the group
+// multiple written by the workgroups of the extra blocks (grid.y = ceil(rows_out / 32)).
+// V4: cols % 4 == 0 and x 16-byte aligned.
+constexpr int PSH_SLABS = 4;
+template <bool V4>
+__global__ void __launch_bounds__(64 * PSH_SLABS)
+    prep_rows_preshuffled_kernel(const float* __restrict__ x, int rows, int cols, int k64n,
+                                 uint8_t* __restrict__ ash, int rows32, ScaleOut so) {
+    constexpr int BLK = 2 * PSH_SLABS;  // 32-value blocks per row in the workgroup's range
+    __shared__ float stage[32][BLK * 33];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int mb = blockIdx.y, s0 = blockIdx.x * PSH_SLABS;
+    const int c0 = 2 * s0;  // first block
+    // loads: wave w takes rows 8w .. 8w+7; per row 256 values = 64 float4, one per lane
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int i = wave * 8 + j, r = mb * 32 + i;
+        const int p = 4 * lane;  // value index in the row's range
+        const int e = c0 * 32 + p;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (r < rows) {
+            const float* xr = x + (size_t)r * cols;
+            if constexpr (V4) {
+                if (e < cols) {
+                    const v4f q = *reinterpret_cast<const v4f*>(xr + e);
+                    v[0] = q[0], v[1] = q[1], v[2] = q[2], v[3] = q[3];
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (e + k < cols) v[k] = xr[e + k];
+            }
+        }
+        const int b = p >> 5, o = p & 31;
+#pragma unroll
+        for (int k = 0; k < 4; k++) stage[i][b * 33 + o + k] = v[k];
+    }
+    __syncthreads();
+    const int s = s0 + wave;
+    if (s >= k64n) return;
+    const int i = lane & 31, h = lane >> 5, r = mb * 32 + i, c = 2 * s + h;
+    const int vblk = (cols + 31) / 32;
+    uint32_t w[6] = {0, 0, 0, 0, 0, 0};
+    int code = 127;
+    if (r < rows && c < vblk) {
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 32; k++) v[k] = stage[i][(2 * wave + h) * 33 + k];
+        code = quant32(v, w);
+    }
+    if (r < rows32) {
+        uint8_t* tile = ash + ((size_t)mb * k64n + s) * OPBLK_BYTES;
+        *reinterpret_cast<v4i*>(tile + 16 * lane) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        *reinterpret_cast<v2i*>(tile + 1024 + 8 * lane) = v2i{(int)w[4], (int)w[5]};
+    }
+    if (c < so.ncols) put_tiled_scale(so.p, r, c, so.group, so.ktn, code);
 }
 
 // grid: nchunks * kchunks workgroups, nchunks = ceil(NG / 64), kchunks = ceil(Kp/32 / 4):

@@ -54,14 +54,16 @@ int mxfp6_hip_has_tile(int MT, int NT, int mpw, int npw);
 
 /* Quantisation and layout kernels (csrc/hip/prep_kernel.hpp). All return 0 ok, 2 launch error.
  *
- * Row-major float x[rows][cols] (cols % 32 == 0, x 16-byte aligned): for each row r and block
- * c < nblk, the codes of values 32c .. 32c+31 (zero bytes for c >= cols/32) go to packed + r *
- * row_bytes + 24c, cut at row_bytes (row_bytes % 4 == 0); scale column c < ncols goes to
- * scales[r * ncols + c] (scale_mode 0) or to the tile_scale(group, 3) layout at Kp (scale_mode
- * 1, ncols = Kp / 32), code 127 for c >= cols / 32. */
+ * Row-major float x[rows][cols] (4-byte aligned; 16-byte aligned with cols % 4 == 0 reads float4):
+ * for each row r and block c < nblk, the codes of values 32c .. 32c+31 (zero past cols; zero bytes
+ * for a block past the values) go to packed + r * row_bytes + 24c, cut at row_bytes (row_bytes % 4
+ * == 0) -- or, with preshuffled != 0, to the preshuffled operand layout at Kp (nblk = Kp / 32,
+ * ceil(rows / 32) 32-row blocks, the rows past `rows` zero codes); scale column c < ncols goes to
+ * scales[r * ncols + c] (scale_mode 0) or to the tile_scale(group, 3) layout at Kp (scale_mode 1,
+ * ncols = Kp / 32), code 127 for a block without values. */
 int mxfp6_hip_quantize_rows(const float* x, int rows, int cols, int nblk, void* packed,
-                            size_t row_bytes, uint8_t* scales, int scale_mode, int ncols,
-                            int group, int Kp, void* stream);
+                            size_t row_bytes, int preshuffled, uint8_t* scales, int scale_mode,
+                            int ncols, int group, int Kp, void* stream);
 
 /* Row-major float B[K][N] -> preshuffled B^T at Kp (N/32 * Kp/64 * 1536 bytes) and its scales
  * in the tile_scale(group, 3) layout at Kp. N % (32 * group) == 0. */

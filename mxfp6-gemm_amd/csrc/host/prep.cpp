@@ -43,7 +43,7 @@ extern "C" int mxfp6_quantize_async(const float* d_x, int rows, int cols, void* 
     if (scale_cols < kblocks(cols)) return MXFP6_ERR_SHAPE;
     if (!aligned(d_x, 4) || !aligned(d_packed, 4)) return MXFP6_ERR_ARG;
     const int nblk = std::max(scale_cols, row_blocks(packed_row_bytes));
-    return status_of(mxfp6_hip_quantize_rows(d_x, rows, cols, nblk, d_packed, packed_row_bytes,
+    return status_of(mxfp6_hip_quantize_rows(d_x, rows, cols, nblk, d_packed, packed_row_bytes, 0,
                                              d_scales, 0, scale_cols, 1, K_TILE, stream));
 }
 
@@ -56,8 +56,19 @@ extern "C" int mxfp6_prepare_a_async(const float* d_A, int M, int K, int group, 
     if (!aligned(d_A, 4) || !aligned(d_packed, 4)) return MXFP6_ERR_ARG;
     const int Kp = kpad_of(K);
     const int nblk = std::max(Kp / 32, row_blocks(a_row_bytes));
-    return status_of(mxfp6_hip_quantize_rows(d_A, M, K, nblk, d_packed, a_row_bytes, d_tiled, 1,
+    return status_of(mxfp6_hip_quantize_rows(d_A, M, K, nblk, d_packed, a_row_bytes, 0, d_tiled, 1,
                                              Kp / 32, group, Kp, stream));
+}
+
+extern "C" int mxfp6_prepare_a_preshuffled_async(const float* d_A, int M, int K, int group,
+                                                 void* d_ash, uint8_t* d_tiled, void* stream) {
+    if (!d_A || !d_ash || !d_tiled) return MXFP6_ERR_NULL;
+    if (group < 1 || group > 4) return MXFP6_ERR_ARG;
+    if (M <= 0 || K <= 0) return MXFP6_ERR_SHAPE;
+    if (!aligned(d_A, 4) || !aligned(d_ash, 16)) return MXFP6_ERR_ARG;
+    const int Kp = kpad_of(K);
+    return status_of(mxfp6_hip_quantize_rows(d_A, M, K, Kp / 32, d_ash, 0, 1, d_tiled, 1, Kp / 32,
+                                             group, Kp, stream));
 }
 
 extern "C" int mxfp6_prepare_b_async(const float* d_B, int K, int N, int group, void* d_bsh,

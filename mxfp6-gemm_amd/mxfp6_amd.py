@@ -55,6 +55,8 @@ SIGNATURES = {
     "mxfp6_quantize_async": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_size_t, _vp, C.c_int, _vp]),
     "mxfp6_prepare_a_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp,
                                         _vp]),
+    "mxfp6_prepare_a_preshuffled_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp,
+                                                    _vp]),
     "mxfp6_prepare_b_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]),
     "mxfp6_tile_scales_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "mxfp6_preshuffled_bytes": (C.c_size_t, [C.c_int, C.c_int]),
@@ -196,6 +198,10 @@ def quantize_dev(dx, rows, cols, dpacked, packed_row_bytes, dscales, scale_cols,
 def prepare_a_dev(dA, M, K, group, dpacked, a_row_bytes, dtiled, stream=None):
     """float A[M][K] -> packed rows + tiled scales at kpad(K) on the device; returns the status."""
     return lib().mxfp6_prepare_a_async(dA, M, K, group, dpacked, a_row_bytes, dtiled, stream)
+
+
+def prepare_a_preshuffled_dev(dA, M, K, group, dash, dtiled, stream=None):
+    return lib().mxfp6_prepare_a_preshuffled_async(dA, M, K, group, dash, dtiled, stream)
 
 
 def prepare_b_dev(dB, K, N, group, dbsh, dtiled, stream=None):

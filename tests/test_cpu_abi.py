@@ -81,6 +81,10 @@ def test_prep_argument_checks_reject_before_launch(mx):
     assert mx.prepare_a_dev(p, 0, 64, 2, p, 48, p) == 2                 # M = 0
     assert mx.prepare_a_dev(p, 96, 40, 2, p, 44, p) == 2                # row shorter than codes
     assert mx.prepare_a_dev(p, 128, 64, 5, p, 48, p) == 5               # group
+    assert mx.prepare_a_preshuffled_dev(0, 64, 64, 2, p, p) == 1        # null input
+    assert mx.prepare_a_preshuffled_dev(p, 0, 64, 2, p, p) == 2         # M = 0
+    assert mx.prepare_a_preshuffled_dev(p, 64, 64, 0, p, p) == 5        # group
+    assert mx.prepare_a_preshuffled_dev(p, 64, 64, 2, p + 8, p) == 5    # A^sh not 16-byte aligned
     assert mx.prepare_b_dev(p, 64, 0, 2, p, p) == 2                     # N = 0
     assert mx.prepare_b_dev(p, -1, 64, 2, p, p) == 2                    # K < 0
     assert mx.prepare_b_dev(p, 64, 64, 2, p + 8, p) == 5                # Bsh not 16-byte aligned

@@ -198,3 +198,61 @@ def test_gemm_on_device_prepared_operands(mx, M, N, K, out_type):
     d_dev = run(da, db, dsa, dsb)
     d_host = run(to_dev(a_rows.reshape(-1)), to_dev(bsh), to_dev(sa_t), to_dev(sb_t))
     assert np.array_equal(d_dev, d_host)
+
+
+@pytest.mark.parametrize("M,K,group", [(32, 64, 1), (100, 1000, 2), (256, 2080, 4), (97, 8192, 3)])
+def test_prepare_a_preshuffled(mx, M, K, group):
+    """A quantised straight into the preshuffled layout equals the device preshuffle of
+    prepare_a's padded rows and the oracle's preshuffle of the quantised rows (zero rows up to
+    the next 32); the scales equal prepare_a's; and a GEMM reading it (a_layout 2) gives the bits
+    of the routed GEMM on the row-major A."""
+    say(f"prepare_a preshuffled M={M} K={K} group={group}")
+    Kp = _kpad(K)
+    rb = Kp // 4 * 3
+    x = specials_matrix(M, K, seed=M * 13 + K) if K % 32 == 0 else None
+    x = np.random.default_rng(M + K).standard_normal((M, K)).astype(np.float32) if x is None else x
+    dx = to_dev(x)
+    nts = mx.tiled_scale_bytes(M, K, group)
+    rows = torch.empty(M * rb, dtype=torch.uint8, device=DEV)
+    t_rows = torch.empty(nts, dtype=torch.uint8, device=DEV)
+    assert mx.prepare_a_dev(dx.data_ptr(), M, K, group, rows.data_ptr(), rb, t_rows.data_ptr()) == 0
+    nsh = mx.preshuffled_bytes(M, K)
+    via_rows = torch.empty(nsh, dtype=torch.uint8, device=DEV)
+    assert mx.preshuffle_rows(rows.data_ptr(), rb, M, Kp, via_rows.data_ptr()) == 0
+    ash = torch.full((nsh + 256,), 0xA5, dtype=torch.uint8, device=DEV)
+    t_sh = torch.full((nts,), 0xA5, dtype=torch.uint8, device=DEV)
+    assert mx.prepare_a_preshuffled_dev(dx.data_ptr(), M, K, group, ash.data_ptr(),
+                                        t_sh.data_ptr()) == 0
+    got = host(ash)
+    assert (got[nsh:] == 0xA5).all()
+    assert np.array_equal(got[:nsh], host(via_rows))
+    assert np.array_equal(host(t_sh), host(t_rows))
+    M32, K32 = -(-M // 32) * 32, -(-K // 32) * 32
+    xz = np.zeros((M32, K32), np.float32)
+    xz[:M, :K] = x
+    po, _ = oracle.quantize_ref(xz)
+    padded = np.zeros((M32, rb), np.uint8)
+    padded[:, :K32 // 4 * 3] = po.reshape(M32, -1)
+    assert np.array_equal(got[:nsh], oracle.preshuffle_b(padded, M32, Kp, rb))
+    # the GEMM on it: N = 256, B prepared on the device, the tile the router picks
+    N = 256
+    tile = mx.choose_tile(M, N, Kp)
+    if tile[2] != group:
+        return
+    B = np.random.default_rng(K).standard_normal((K, N)).astype(np.float32)
+    db = torch.empty(mx.preshuffled_bytes(N, K), dtype=torch.uint8, device=DEV)
+    dsb = torch.empty(mx.tiled_scale_bytes(N, K, tile[3]), dtype=torch.uint8, device=DEV)
+    assert mx.prepare_b_dev(to_dev(B).data_ptr(), K, N, tile[3], db.data_ptr(), dsb.data_ptr()) == 0
+    D1 = torch.empty(M * N * 4, dtype=torch.uint8, device=DEV)
+    D2 = torch.empty(M * N * 4, dtype=torch.uint8, device=DEV)
+    wsb = mx.workspace_size(M, N, Kp)
+    ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=DEV)
+    assert mx.gemm(0, M, N, Kp, rows.data_ptr(), db.data_ptr(), t_rows.data_ptr(), dsb.data_ptr(),
+                   D1.data_ptr(), rb, ws.data_ptr(), wsb) == 0
+    S = mx.splitk_segments(M, N, Kp)
+    wse = mx.plan_workspace_size(M, N, Kp, S, 0)
+    wsx = torch.empty(max(wse, 4), dtype=torch.uint8, device=DEV)
+    assert mx.gemm_explicit(0, M, N, Kp, tile, S, ash.data_ptr(), db.data_ptr(), t_sh.data_ptr(),
+                            dsb.data_ptr(), D2.data_ptr(), rb, wsx.data_ptr() if wse else 0, wse,
+                            a_layout=2) == 0
+    assert np.array_equal(host(D1), host(D2))
