@@ -44,17 +44,39 @@ __device__ __forceinline__ void wait_vmcnt0() {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// Bijective map of the linear workgroup id onto (tile_m, tile_n) such that each XCD receives a
-// contiguous run of the grouped order (groups of XG tile rows, tile_m fastest).
-__device__ __forceinline__ void xcd_tile(int gm, int gn, int XG, int pid, int& tm, int& tn) {
-    const int total = gm * gn;
+// Position of workgroup pid in an XCD-major order of `total` workgroups: workgroups are dispatched
+// to the XCDs round-robin (pid % NXCD), so XCD x receives the contiguous run of positions
+// [x * per (+ remainder), ...) in dispatch order. A bijection of [0, total).
+__device__ __forceinline__ int xcd_position(int total, int pid) {
     const int per = total / NXCD, rem = total % NXCD;
     const int x = pid % NXCD, j = pid / NXCD;
-    const int L = x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+    return x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+}
+
+// Tile of position L in the grouped order of a gm x gn tile grid: groups of XG tile rows, tile_m
+// fastest inside a group.
+__device__ __forceinline__ void grouped_tile(int gm, int gn, int XG, int L, int& tm, int& tn) {
     const int band = XG * gn;
     const int grp = L / band, rows = min(XG, gm - grp * XG), w = L - grp * band;
     tm = grp * XG + w % rows;
     tn = w / rows;
+}
+
+// Bijective map of the linear workgroup id onto (tile_m, tile_n) such that each XCD receives a
+// contiguous run of the grouped order.
+__device__ __forceinline__ void xcd_tile(int gm, int gn, int XG, int pid, int& tm, int& tn) {
+    grouped_tile(gm, gn, XG, xcd_position(gm * gn, pid), tm, tn);
+}
+
+// Split-K variant: the S K segments of a gm x gn grid are laid end to end (segment-major) and
+// each XCD receives a contiguous run of that order, so an XCD holds whole K segments (or a
+// contiguous part of one) instead of a slice of every segment. pid counts over all S * gm * gn
+// workgroups; z is the K segment.
+__device__ __forceinline__ void xcd_split_tile(int gm, int gn, int S, int XG, int pid, int& tm,
+                                               int& tn, int& z) {
+    const int T = gm * gn, L = xcd_position(T * S, pid);
+    z = L / T;
+    grouped_tile(gm, gn, XG, L - z * T, tm, tn);
 }
 
 }  // namespace mxfp6_dev
