@@ -21,7 +21,9 @@ namespace plan {
 //   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3   (12)
 //   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4   (8)
 //   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (4; two workgroups fit a CU's LDS)
-// and, for M not a multiple of 128 (M a multiple of 32), the skinny tiles (waves 1x4):
+// and the skinny tiles (waves 1x4), the only ones for M not a multiple of 128 (M a multiple of
+// 32), and on small grids faster than the big ones for any M (C1, 256x256x1024: 32x128 6.3 us
+// against 8.2 us on 128x128):
 //   64x256 (MPW 2, NPW 2), 32x256 (1, 2), 64x128 (2, 1), 32x128 (1, 1; two per CU)
 // Ragged shapes (M not a multiple of 32 or N not a multiple of 128) take any of the nine tiles,
 // the last tile row and column masked (wg counts the partial tiles).
@@ -39,13 +41,13 @@ namespace plan {
 //   t        = T_LAUNCH + waves * t_wg, plus for a repack T_LAUNCH + its bytes (A read and written)
 //              at REPACK_BYTES_PER_US, and for a split T_LAUNCH + the partials written and read
 //              back at SPLIT_BYTES_PER_US.
-// The constants are a least-squares fit (log time) to every plan of the 56 measured shapes with
-// M % 128 == 0 (one MI355X; M from 128 to 8192, N from 256 to 102272, K from 1024 to 105728,
-// masked N included), the repack rate the repack kernel's measured one. Re-measured on the
-// current kernels (71 shapes), the plan the model picks is within 1.1% of the measured best on
-// average, 13% at worst (fixed rules were up to 2x off on small-K grids), and within 1% of the
-// best on the five benchmark workloads. On the 14 skinny-M and 6 ragged shapes, the same constants
-// pick within 16% and 6% of the best.
+// The constants are a least-squares fit (log time) to every plan of the 66 measured shapes with
+// M % 128 == 0 (one MI355X; M from 128 to 8192, N from 128 to 102272, K from 1024 to 105728,
+// masked N and the skinny tiles included), plans within 1.3x of their shape's best weighing 5x
+// the others; the repack rate is the repack kernel's measured one. On the 63 of those shapes whose
+// pick was measured, the plan the model picks is within 2.1% of the measured best on average, 16%
+// at worst, and it is the best on the five benchmark workloads; on the 14 skinny-M and ragged
+// shapes within 3.4% on average, 10% at worst.
 namespace {
 struct Plan {
     TileChoice tc;
@@ -91,27 +93,25 @@ const int kNSkinny = (int)(sizeof(kSkinny) / sizeof(kSkinny[0]));
 
 // The least-time plan. Candidates are visited from the simplest (no split, no repack) and a
 // plan needs a PLAN_MIN_GAIN lead to displace an earlier one, so near-ties keep the plan with
-// fewer launches and less workspace. Regular shapes take the tiles whose MT divides M (the
-// skinny ones when M is not a multiple of 128), with the last tile column masked when NT does
-// not divide N (the reference's NMASK route, src/kernel.hpp:144-154, for any tile: N = 102272
-// runs 256x256 over ceil(N/256) columns instead of 128x128); ragged shapes any of the nine, big
-// tiles first. Shapes gemm() rejects get the trivial plan.
+// fewer launches and less workspace. Regular shapes take the tiles whose MT divides M, with the
+// last tile column masked when NT does not divide N (the reference's NMASK route,
+// src/kernel.hpp:144-154, for any tile: N = 102272 runs 256x256 over ceil(N/256) columns instead
+// of 128x128); ragged shapes any of the nine, big tiles first. Shapes gemm() rejects get the
+// trivial plan.
 Plan best_plan(int M, int N, int Kp) {
     Plan best = {{128, 128, 2, 2}, 1, false};
     if (!shape_ok(M, N, Kp)) return best;
     double best_t = -1.0;
     const int k_tiles = Kp / K_TILE;
     const bool reg = regular(M, N);
-    const bool skinny = M % 128 != 0;
-    const int n_cands = reg ? (skinny ? kNSkinny : kNCands) : kNCands + kNSkinny;
-    // regular shapes: the dividing tiles first, then (pass 1) the N-masked ones
+    // big tiles first, then the skinny ones; on regular shapes only the tiles whose MT divides M
+    // (so M % 128 != 0 leaves the skinny ones), the dividing tiles first, then (pass 1) the
+    // N-masked ones
     for (int pass = 0; pass < (reg ? 2 : 1); pass++)
         for (int rp = 0; rp < 2; rp++)
             for (int S = 1; S <= MAX_SPLITS && S <= k_tiles; S++)
-                for (int ci = 0; ci < n_cands; ci++) {
-                    const TileChoice& tc =
-                        reg ? (skinny ? kSkinny[ci] : kCands[ci])
-                            : (ci < kNCands ? kCands[ci] : kSkinny[ci - kNCands]);
+                for (int ci = 0; ci < kNCands + kNSkinny; ci++) {
+                    const TileChoice& tc = ci < kNCands ? kCands[ci] : kSkinny[ci - kNCands];
                     if (reg && (M % tc.MT != 0 || (N % tc.NT != 0) != (pass == 1))) continue;
                     const double t = plan_time_us(tc, M, N, Kp, S, rp != 0);
                     if (best_t < 0 || t < best_t * (1.0 - PLAN_MIN_GAIN)) {

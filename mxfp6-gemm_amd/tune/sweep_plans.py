@@ -47,9 +47,12 @@ def sweep(M, N, K):
     regular = M % 32 == 0 and N % 128 == 0
     for t in TILES:
         # the plans the router considers: on a regular shape (M % 32 == 0, N % 128 == 0) the
-        # tiles whose MT divides M, the skinny ones (fewer than 128 rows) exactly when
-        # M % 128 != 0, N masked when NT does not divide it; on a ragged shape every tile
-        if regular and (M % t[0] or (t[0] < 128) != (M % 128 != 0)):
+        # tiles whose MT divides M, N masked when NT does not divide it; on a ragged shape every
+        # tile. The skinny tiles (fewer than 128 rows) are measured on M % 128 == 0 shapes only
+        # up to 2048 workgroups (they lose on larger grids, and take long there).
+        if regular and M % t[0]:
+            continue
+        if t[0] < 128 and M % 128 == 0 and -(-M // t[0]) * -(-N // t[1]) > 2048:
             continue
         bsh, sa, sb = p.layouts(t)
         dB, dsa, dsb = (torch.from_numpy(x).cuda() for x in (bsh, sa, sb))

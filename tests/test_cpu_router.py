@@ -54,14 +54,15 @@ def test_oracle_split_plan_reference_cases(orc):
 
 
 def test_router_covers_every_multiple_of_128(mx):
-    """Every M, N multiple of 128: an implemented tile whose MT divides M; NT divides N or the
-    last tile column is masked (the reference's NMASK route, for any tile)."""
+    """Every M, N multiple of 128: an implemented tile (the skinny ones included) whose MT
+    divides M; NT divides N or the last tile column is masked (the reference's NMASK route, for
+    any tile)."""
     bad = masked = 0
     for M in range(128, 16385, 128):
         for N in range(128, 24577, 128):
             for K in (512, 16128, 105728):
                 t = mx.choose_tile(M, N, _kpad(K))
-                if M % t[0] or tuple(t) not in IMPLEMENTED:
+                if M % t[0] or tuple(t) not in IMPLEMENTED | SKINNY:
                     bad += 1
                 masked += N % t[1] != 0
     assert bad == 0 and masked > 0
@@ -102,7 +103,7 @@ def test_router_benchmark_shapes(mx):
     # The plan-time model's picks for the five benchmark workloads; each is the fastest of all
     # plans (tile x 1..16 segments x A layout) measured on MI355X for that shape.
     want = {
-        (256, 256, 1024): ((128, 128, 2, 2), 1),
+        (256, 256, 1024): ((32, 128, 1, 1), 1),
         (8192, 8192, 8192): ((256, 256, 4, 4), 1),
         (2048, 6144, 16128): ((256, 192, 4, 3), 1),
         (2048, 1024, 105728): ((256, 256, 4, 4), 8),
@@ -122,14 +123,17 @@ def test_router_benchmark_shapes(mx):
 def test_router_small_k_plans(mx):
     """Shapes whose measured best plan (MI355X, every tile x split x A layout) differs from the
     large-K habit of 256x256 tiles with a repacked A: short K favours more, smaller workgroups
-    and no extra launch for the repack; the router's model reproduces the measured winners."""
+    (down to the 32- and 64-row tiles) and no extra launch for the repack; the router's model
+    reproduces the measured winners."""
     want = {  # (M, N, K): (tile, S, repack) measured fastest
-        (2048, 2048, 2048): ((128, 128, 2, 2), 1, False),   # 14.5 us vs 29.2 for 256x256 + repack
-        (2048, 1024, 1024): ((128, 128, 2, 2), 1, False),   # 9.1 us vs 14.1 with a repack
-        (4096, 4096, 1024): ((256, 256, 4, 4), 1, False),   # 22.9 us vs 27.7 with a repack
-        (2048, 4096, 1024): ((128, 256, 2, 4), 1, False),   # 14.3 us vs 24.6 for 256x256
-        (512, 1024, 16384): ((128, 128, 2, 2), 8, False),   # 21.8 us: 64 workgroups x 8 segments
-        (8192, 8192, 2048): ((256, 256, 4, 4), 1, True),    # 114.4 us vs 120.4 unrepacked
+        (256, 256, 1024): ((32, 128, 1, 1), 1, False),     # 6.5 us vs 7.1 for the next plan
+        (1024, 1024, 1024): ((32, 128, 1, 1), 1, False),   # 6.8 us vs 7.3
+        (2048, 1024, 1024): ((64, 128, 2, 1), 1, False),   # 7.8 us vs 8.1
+        (2048, 256, 2048): ((32, 128, 1, 1), 1, False),    # 8.7 us vs 9.8 (no split)
+        (4096, 4096, 1024): ((256, 256, 4, 4), 1, False),  # 22.7 us vs 27.5 with a repack
+        (2048, 4096, 1024): ((128, 256, 2, 4), 1, False),  # 14.3 us vs 17.9
+        (4096, 2048, 2048): ((128, 256, 2, 4), 1, False),  # 20.8 us vs 26.5
+        (8192, 8192, 2048): ((256, 256, 4, 4), 1, True),   # 117.7 us vs 122.0 unrepacked
     }
     for (M, N, K), (tile, S, rp) in want.items():
         Kp = _kpad(K)
@@ -141,7 +145,7 @@ def test_router_small_k_plans(mx):
 def test_router_equals_the_tuning_model(mx):
     """The Python model in mxfp6-gemm_amd/tune (the one the constants are fitted with) and the
     library's router make the same choice on every shape of the recorded plan measurements and
-    on a grid of other shapes; and with the committed constants its picks are within 2% of the
+    on a grid of other shapes; and with the committed constants its picks are within 3% of the
     measured best on average."""
     import math
     import os
@@ -166,18 +170,18 @@ def test_router_equals_the_tuning_model(mx):
               if M % 32 == 0 and N % 128 == 0 and N % pm.best_plan(
                   pm.CONSTANTS, M, N, _kpad(K))[0][1] != 0]
     gm = math.exp(sum(math.log(g) for g in big) / len(big))
-    assert len(big) >= 48 and gm < 1.02, (len(big), gm)
+    assert len(big) >= 60 and gm < 1.03, (len(big), gm)
     # N-masked picks on regular shapes are among them (the reference's NMASK route)
     assert len(masked) >= 5
-    # the skinny tiles and the ragged shapes use the same constants (fitted on M % 128 == 0):
-    # their picks are within 17% and 10% of the measured best
-    assert len(skinny) >= 6 and max(skinny) < 1.17, skinny
+    # the skinny-M and the ragged shapes use the same constants (fitted on M % 128 == 0):
+    # their picks are within 12% and 10% of the measured best
+    assert len(skinny) >= 6 and max(skinny) < 1.12, skinny
     assert len(ragged) >= 6 and max(ragged) < 1.10, ragged
 
 
 def test_router_skinny_m(mx):
     """M a multiple of 32 but not of 128 routes to the 32- or 64-row tiles (one wave row, four
-    wave columns); the tile divides the shape, the split keeps >= 1 K-tile per segment, and the
+    wave columns); the tile's rows divide M, the split keeps >= 1 K-tile per segment, and the
     workspace is the plan's."""
     skinny = {(32, 128, 1, 1), (32, 256, 1, 2), (64, 128, 2, 1), (64, 256, 2, 2)}
     for M in (32, 64, 96, 160, 224, 480, 1056):
@@ -186,7 +190,8 @@ def test_router_skinny_m(mx):
                 Kp = _kpad(K)
                 t = tuple(mx.choose_tile(M, N, Kp))
                 S = mx.splitk_segments(M, N, Kp)
-                assert t in skinny and M % t[0] == 0 and N % t[1] == 0, (M, N, K, t)
+                # MT divides M; NT divides N or the last tile column is masked
+                assert t in skinny and M % t[0] == 0, (M, N, K, t)
                 assert 1 <= S <= min(16, Kp // 192)
                 rp = mx.repacks_a(M, N, Kp)
                 want = ((S * M * N * 4 if S > 1 else 0) + 255) // 256 * 256 + (M * Kp // 4 * 3 if rp else 0)
