@@ -278,20 +278,25 @@ def run_prep(steps, warmup):
         for c in calls.values():
             assert c() == 0
     torch.cuda.synchronize()
-    evs = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(steps)] for k in calls}
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for i in range(steps):
         for k, c in calls.items():
-            evs[k][i][0].record(stream)
             if c() != 0:
                 raise RuntimeError(f"{k} failed")
-            evs[k][i][1].record(stream)
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    k_ms = {k: sum(a.elapsed_time(b) for a, b in v) / steps for k, v in evs.items()}
+    # each kernel alone: `steps` back-to-back launches between two events on the launch stream
+    k_ms = {}
+    for k, c in calls.items():
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(steps):
+            c()
+        b.record(stream)
+        torch.cuda.synchronize()
+        k_ms[k] = a.elapsed_time(b) / steps
     per_op = M * K * 4 + M * Kp * 3 // 4 + M * Kp // 32  # A and B have the same shape
     gbs = 2 * per_op / (ms * 1e-3) / 1e9
     dom = max(k_ms, key=k_ms.get)

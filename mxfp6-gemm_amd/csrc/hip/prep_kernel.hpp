@@ -28,8 +28,9 @@
 //   prep_rows_kernel  row-major float [rows][cols] -> packed rows (+ zero tail up to row_bytes) and
 //                     scales, raw [rows][scale_cols] (tail columns 127) or tiled at Kp. A
 //                     one-wave workgroup takes 64 consecutive 32-blocks of one row: coalesced
-//                     float4 loads into LDS, then lane l quantises block l and writes its 24
-//                     bytes (consecutive lanes, consecutive bytes).
+//                     float4 loads into LDS, then lane l quantises block l; the chunk's 1536
+//                     packed bytes go back through LDS and out as 16-byte stores (6 strided
+//                     dword stores per lane before: 82 -> 65 us at 8192 x 8192).
 //   prep_rows_preshuffled_kernel  row-major float A -> the preshuffled operand layout + tiled
 //                     scales: a workgroup stages 32 rows x 4 slabs in LDS, each wave then writes
 //                     one whole 1536-byte tile (lane t: row t % 32, 32-block half t / 32).
@@ -172,7 +173,7 @@ __global__ void __launch_bounds__(64)
     prep_rows_kernel(const float* __restrict__ x, int cols, int nblk, PackedOut po, ScaleOut so,
                      int chunks, int rows) {
     constexpr int BPW = PREP_BLKS_PER_WAVE;  // blocks per task, one per lane
-    __shared__ float stage[BPW * 33];
+    __shared__ __attribute__((aligned(16))) float stage[BPW * 33];
     const int lane = threadIdx.x;
     const int r = (int)(blockIdx.x / (unsigned)chunks);
     const int chunk = (int)(blockIdx.x - (unsigned)r * chunks);
@@ -204,7 +205,35 @@ __global__ void __launch_bounds__(64)
     }
     __syncthreads();
     const int c = blk0 + lane;
-    if (c < nblk) {
+    // a whole chunk of value blocks into 16-byte aligned row-major rows: staged in LDS and stored
+    // as 16-byte contiguous pieces
+    const bool full = po.k64n == 0 && data && (po.row_bytes % 16) == 0 && blk0 + BPW <= vblk &&
+                      (size_t)24 * (blk0 + BPW) <= po.row_bytes;
+    if (full) {
+        uint32_t w[6];
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = stage[lane * 33 + i];
+        const int code = quant32(v, w);
+        __syncthreads();
+        uint32_t* ob = reinterpret_cast<uint32_t*>(stage);
+#pragma unroll
+        for (int d = 0; d < 6; d++) ob[lane * 6 + d] = w[d];
+        __syncthreads();
+        uint8_t* dst = po.p + (size_t)r * po.row_bytes + (size_t)24 * blk0;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int q = lane + 64 * k;
+            if (q < BPW * 24 / 16)
+                *reinterpret_cast<v4i*>(dst + 16 * q) = *reinterpret_cast<const v4i*>(ob + 4 * q);
+        }
+        if (c < so.ncols) {
+            if (so.tiled)
+                put_tiled_scale(so.p, r, c, so.group, so.ktn, code);
+            else
+                so.p[(size_t)r * so.ncols + c] = (uint8_t)code;
+        }
+    } else if (c < nblk) {
         uint32_t w[6] = {0, 0, 0, 0, 0, 0};
         int code = 127;
         if (data && c < vblk) {
