@@ -3,7 +3,9 @@
 // summation order as the reference's reduce_splitk, src/kernel.hpp:305-313).
 // HBM-bound: reads S*total*4 bytes and writes total*sizeof(OutT) bytes. With VEC = 4 each thread
 // handles 4 consecutive elements with 16-byte loads (total a multiple of 4); VEC = 1 (a ragged
-// M x N) one element per thread.
+// M x N) one element per thread. The loads of up to 8 segments are issued before their sums, so
+// a thread waits for one memory latency per 8 segments rather than one per segment (the adds
+// keep the segment order).
 #pragma once
 #include "device_common.hpp"
 
@@ -14,13 +16,30 @@ __global__ void __launch_bounds__(256)
     reduce_splitk_kernel(const float* __restrict__ ws, OutT* __restrict__ D, size_t total, int S) {
     const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * VEC;
     if (i >= total) return;
+    constexpr int BATCH = 8;
     if constexpr (VEC == 1) {
         float acc = 0.f;
-        for (int s = 0; s < S; s++) acc += ws[(size_t)s * total + i];
+        for (int s0 = 0; s0 < S; s0 += BATCH) {
+            float p[BATCH];
+#pragma unroll
+            for (int j = 0; j < BATCH; j++)
+                if (s0 + j < S) p[j] = ws[(size_t)(s0 + j) * total + i];
+#pragma unroll
+            for (int j = 0; j < BATCH; j++)
+                if (s0 + j < S) acc += p[j];
+        }
         D[i] = cvt_out<OutT>(acc);
     } else {
         v4f acc = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < S; s++) acc += *reinterpret_cast<const v4f*>(ws + (size_t)s * total + i);
+        for (int s0 = 0; s0 < S; s0 += BATCH) {
+            v4f p[BATCH];
+#pragma unroll
+            for (int j = 0; j < BATCH; j++)
+                if (s0 + j < S) p[j] = *reinterpret_cast<const v4f*>(ws + (size_t)(s0 + j) * total + i);
+#pragma unroll
+            for (int j = 0; j < BATCH; j++)
+                if (s0 + j < S) acc += p[j];
+        }
         if constexpr (sizeof(OutT) == 4) {
             *reinterpret_cast<v4f*>(D + i) = acc;
         } else {
