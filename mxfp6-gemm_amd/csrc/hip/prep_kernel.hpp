@@ -266,7 +266,10 @@ __global__ void __launch_bounds__(64 * PSH_SLABS)
     prep_rows_preshuffled_kernel(const float* __restrict__ x, int rows, int cols, int k64n,
                                  uint8_t* __restrict__ ash, int rows32, ScaleOut so) {
     constexpr int BLK = 2 * PSH_SLABS;  // 32-value blocks per row in the workgroup's range
-    __shared__ float stage[32][BLK * 33];
+    // rows BLK * 33 + 1 dwords apart: the quantising reads (lane = row i, block half h) then hit
+    // distinct banks for the 32 rows (a stride of BLK * 33 = 264 mapped rows i and i + 8 to one
+    // bank: 79 -> 68 us at 8192 x 8192)
+    __shared__ float stage[32][BLK * 33 + 1];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int mb = blockIdx.y, s0 = blockIdx.x * PSH_SLABS;
     const int c0 = 2 * s0;  // first block
