@@ -86,6 +86,21 @@ def test_pipelined_split_bitwise_equals_direct_split(g):
     assert np.array_equal(Dr.view(np.uint32), Dd.view(np.uint32))
 
 
+@pytest.mark.parametrize("tile", [(128, 256, 2, 4), (128, 384, 4, 3), (256, 256, 4, 4),
+                                  (256, 256, 2, 4), (256, 192, 4, 3)])
+@pytest.mark.parametrize("S,a_layout", [(3, 0), (8, 1)])
+def test_segment_per_xcd_split_bitwise_equals_direct_split(g, tile, S, a_layout):
+    """Split grids of at most 128 tiles of at least 128 x 256 hand each XCD whole K segments
+    (the workgroup -> (tile, segment) map differs from the grid's); every partial must still land
+    in its segment's slot, so the result equals the direct kernel's split bit for bit."""
+    M, N, K = 512, 768, 4224  # 22 K-tiles: uneven segments for S = 3 and 8
+    p = mx.make_problem(M, N, K, seed=83)
+    dp = g.DevProblem(p, tile)
+    Dr = g.run_explicit(dp, mx.OUT_F32, splits=S, a_layout=a_layout)
+    Dd = g.run_direct(dp, mx.OUT_F32, splits=S)
+    assert np.array_equal(Dr.view(np.uint32), Dd.view(np.uint32))
+
+
 # ---- M not a multiple of 128: the skinny tiles ------------------------------------------------
 
 SKINNY = [(32, 128, 1, 1), (32, 256, 1, 2), (64, 128, 2, 1), (64, 256, 2, 2)]
