@@ -121,10 +121,27 @@ Plan best_plan(int M, int N, int Kp) {
                 }
     return best;
 }
+
+// best_plan evaluates the model for every (tile, split, layout): a few microseconds of host time,
+// as long as a small GEMM runs on the GPU. gemm() and the routing queries look the plan up in a
+// per-thread cache of the last shapes instead (16 entries indexed by a hash of the shape; no
+// lock, and the plan of a shape never changes).
+Plan cached_plan(int M, int N, int Kp) {
+    struct Entry {
+        int M, N, Kp;
+        Plan plan;
+        bool valid;
+    };
+    thread_local Entry cache[16] = {};
+    const unsigned h = ((unsigned)M * 73856093u ^ (unsigned)N * 19349663u ^ (unsigned)Kp * 83492791u) >> 4;
+    Entry& e = cache[h % 16];
+    if (!e.valid || e.M != M || e.N != N || e.Kp != Kp) e = {M, N, Kp, best_plan(M, N, Kp), true};
+    return e.plan;
+}
 }  // namespace
 
 TileChoice route(int M, int N, int Kp) {
-    return best_plan(M, N, Kp).tc;
+    return cached_plan(M, N, Kp).tc;
 }
 
 size_t split_bytes(int M, int N, int S) {
@@ -142,11 +159,11 @@ size_t plan_bytes(int M, int N, int Kp, int S, bool repack) {
 }
 
 bool route_repacks(int M, int N, int Kp) {
-    return shape_ok(M, N, Kp) && best_plan(M, N, Kp).repack;
+    return shape_ok(M, N, Kp) && cached_plan(M, N, Kp).repack;
 }
 
 int splitk_segments(int M, int N, int Kp) {
-    return shape_ok(M, N, Kp) ? best_plan(M, N, Kp).S : 1;
+    return shape_ok(M, N, Kp) ? cached_plan(M, N, Kp).S : 1;
 }
 
 size_t workspace_bytes(int M, int N, int Kp) {
@@ -227,7 +244,7 @@ int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void*
                  size_t ws_bytes, void* stream) {
     const int st = check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
     if (st != MXFP6_OK) return st;
-    const Plan pl = best_plan(M, N, Kp);
+    const Plan pl = cached_plan(M, N, Kp);
     const TileChoice tc = pl.tc;
     int S = pl.S;
     bool rp = pl.repack;
