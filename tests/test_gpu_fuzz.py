@@ -1,0 +1,80 @@
+"""Seeded random shapes through the routed gemm(), against the FP64 oracle.
+
+Twenty-four shapes drawn once from a fixed seed: M and N log-uniform in [32, 4096] (a third of
+them rounded to multiples of 128, a third to multiples of 32 and 128, the rest ragged), K a
+multiple of 32 up to 8192; and eight shapes that reach the routes small random shapes rarely do.
+The output type cycles through FP32, FP16 and BF16. Each runs with the workspace the router asks
+for (so the plans it picks are exercised: big and skinny tiles, N-masked and ragged tiles,
+split-K on either XCD map, repacked A) and again with no
+workspace (the documented fallback to the unsplit, unrepacked plan), and is checked against the
+FP64 oracle at this build's bar (tests/checks.py) on every row of a small M, or on 48 spread rows.
+Outputs and workspaces carry guard regions that must survive the call.
+"""
+import numpy as np
+import pytest
+import torch
+
+import checks
+import mxfp6_amd as mx
+import oracle
+from gpu_util import DevProblem, TORCH_OUT, say
+
+pytestmark = pytest.mark.gpu
+
+GUARD = 4096
+
+
+# shapes that reach the routes random small shapes rarely do (the router's pick in the comment)
+ROUTES = [(8192, 4096, 4096),   # 256x256, A repacked
+          (2048, 6144, 4096),   # 256x192, A repacked
+          (3072, 3072, 3072),   # 128x384
+          (2048, 1024, 16384),  # 128x256, 4 K segments
+          (1024, 2432, 32768),  # 256x256 over a masked last column, 6 segments, whole segments per XCD
+          (2048, 2048, 2048),   # 128x128
+          (2047, 1000, 4096),   # ragged, 64x128
+          (4096, 1152, 32768)]  # 256x256, 3 segments, whole segments per XCD
+
+
+def _shapes(n=24, seed=20261201):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        M, N = (int(round(2 ** rng.uniform(5, 12))) for _ in range(2))
+        if i % 3 == 0:
+            M, N = max(128, M // 128 * 128), max(128, N // 128 * 128)
+        elif i % 3 == 1:
+            M, N = max(32, M // 32 * 32), max(128, N // 128 * 128)
+        K = int(rng.integers(1, 257)) * 32
+        out.append((M, N, K, i % 3))
+    return out + [(M, N, K, i % 3) for i, (M, N, K) in enumerate(ROUTES)]
+
+
+def _run(dp, out_type, with_ws):
+    p = dp.p
+    n = p.M * p.N * mx.OUT_BYTES[out_type]
+    ws_bytes = mx.workspace_size(p.M, p.N, p.Kp) if with_ws else 0
+    D = torch.full((n + GUARD,), 0x5A, dtype=torch.uint8, device="cuda")
+    ws = torch.full((max(ws_bytes, 4) + GUARD,), 0x3C, dtype=torch.uint8, device="cuda")
+    a, b, sa, sb = dp.ptrs()
+    say(f"  routed {p.M}x{p.N}x{p.K} (Kp {p.Kp}) tile {dp.tile} S "
+        f"{mx.splitk_segments(p.M, p.N, p.Kp)} repack {mx.repacks_a(p.M, p.N, p.Kp)} out "
+        f"{mx.OUT_NAMES[out_type]} ws {ws_bytes}")
+    rc = mx.gemm(out_type, p.M, p.N, p.Kp, a, b, sa, sb, D.data_ptr(), p.a_row_bytes,
+                 ws.data_ptr() if ws_bytes else 0, ws_bytes)
+    assert rc == 0, mx.STATUS.get(rc, rc)
+    torch.cuda.synchronize()
+    assert (D[n:].cpu().numpy() == 0x5A).all(), "write past the end of D"
+    assert (ws[max(ws_bytes, 4):].cpu().numpy() == 0x3C).all(), "write past the workspace"
+    return D[:n].view(TORCH_OUT[out_type]).float().reshape(p.M, p.N).cpu().numpy()
+
+
+@pytest.mark.parametrize("M,N,K,out_type", _shapes())
+def test_routed_random_shape(M, N, K, out_type):
+    p = mx.make_problem(M, N, K, seed=M * 131 + N * 17 + K)
+    dp = DevProblem(p, mx.choose_tile(M, N, p.Kp))
+    rows = None if M <= 48 else np.unique(np.r_[0:4, M - 4:M,
+                                                 np.linspace(0, M - 1, 40).astype(int)])
+    R, ab = oracle.problem_f64(p, rows=rows)
+    for with_ws in (True, False):
+        D = _run(dp, out_type, with_ws)
+        checks.check(D if rows is None else D[rows], R, ab, out_type)
