@@ -136,7 +136,7 @@ extern "C" int mxfp6_hip_quantize_rows(const float* x, int rows, int cols, int n
 extern "C" int mxfp6_hip_prepare_b(const float* B, int K, int N, int Kp, int group, void* bsh,
                                    uint8_t* tiled, void* stream) {
     const int NG = rows_in_groups(N, group);
-    const unsigned nchunks = (unsigned)((NG + 63) / 64), kchunks = (unsigned)((Kp / 32 + 3) / 4);
+    const unsigned nchunks = (unsigned)((NG + PREP_THREADS - 1) / PREP_THREADS), kchunks = (unsigned)(Kp / 32);
     prep_b_kernel<<<dim3(nchunks * kchunks), dim3(PREP_THREADS), 0,
                     static_cast<hipStream_t>(stream)>>>(B, K, N, NG, Kp, group,
                                                         static_cast<uint8_t*>(bsh), tiled,

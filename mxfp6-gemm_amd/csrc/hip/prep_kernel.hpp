@@ -318,18 +318,19 @@ __global__ void __launch_bounds__(64 * PSH_SLABS)
     if (c < so.ncols) put_tiled_scale(so.p, r, c, so.group, so.ktn, code);
 }
 
-// grid: nchunks * kchunks workgroups, nchunks = ceil(NG / 64), kchunks = ceil(Kp/32 / 4):
-// workgroup (nb, kc) = one wave per 64 columns and 4 consecutive 32-blocks of K (one per wave),
-// K-chunk major. Columns N .. NG-1 (NG = N rounded up to whole scale groups of 32 * group
-// columns) are zero columns: they complete the last 32-column tile of bsh and the last scale
-// group. Values past K in the last 32-block are zero.
+// grid: nchunks * kchunks workgroups, nchunks = ceil(NG / 256), kchunks = Kp / 32: workgroup
+// (nb, kc) = 32-block kc of 256 consecutive columns, 64 per wave, K-block major (the four waves
+// read 1 KiB of each row together: 60 -> 56 us at 8192 x 8192 against 64 columns x 4 blocks).
+// Columns N .. NG-1 (NG = N rounded up to whole scale groups of 32 * group columns) are zero
+// columns: they complete the last 32-column tile of bsh and the last scale group. Values past K
+// in the last 32-block are zero.
 __global__ void __launch_bounds__(PREP_THREADS)
     prep_b_kernel(const float* __restrict__ B, int K, int N, int NG, int Kp, int group,
                   uint8_t* __restrict__ bsh, uint8_t* __restrict__ tiled, int nchunks) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int kc = (int)(blockIdx.x / nchunks), nb = (int)(blockIdx.x - (unsigned)kc * nchunks);
-    const int n = nb * 64 + lane;
-    const int c = kc * (PREP_THREADS / 64) + wave;
+    const int n = nb * PREP_THREADS + wave * 64 + lane;
+    const int c = kc;
     if (c >= Kp / 32 || n >= NG) return;
     uint32_t w[6] = {0, 0, 0, 0, 0, 0};
     int code = 127;
