@@ -221,3 +221,35 @@ def test_router_ragged_shapes(mx):
                 want = (((S * M * N * 4 if S > 1 else 0) + 255) // 256 * 256
                         + (-(-M // 32) * 32 * Kp // 4 * 3 if rp else 0))
                 assert mx.workspace_size(M, N, Kp) == (want if (S > 1 or rp) else 0)
+
+
+def test_plan_cache_is_per_thread_and_transparent(mx):
+    """gemm() and the routing queries read a per-thread cache of recent plans: concurrent queries
+    from several threads (ctypes releases the GIL) over more shapes than the cache holds, in
+    different orders, give the same answers as a single thread."""
+    import random
+    import threading
+    shapes = [(M, N, K) for M in (32, 96, 256, 2048, 8191) for N in (128, 1000, 6144)
+              for K in (192, 4096, 105728)]
+    want = {s: (tuple(mx.choose_tile(s[0], s[1], _kpad(s[2]))),
+                mx.splitk_segments(s[0], s[1], _kpad(s[2])), mx.repacks_a(s[0], s[1], _kpad(s[2])),
+                mx.workspace_size(s[0], s[1], _kpad(s[2])))
+            for s in shapes}
+    bad = []
+
+    def worker(seed):
+        rng = random.Random(seed)
+        for _ in range(400):
+            M, N, K = rng.choice(shapes)
+            Kp = _kpad(K)
+            got = (tuple(mx.choose_tile(M, N, Kp)), mx.splitk_segments(M, N, Kp),
+                   mx.repacks_a(M, N, Kp), mx.workspace_size(M, N, Kp))
+            if got != want[(M, N, K)]:
+                bad.append(((M, N, K), got))
+
+    threads = [threading.Thread(target=worker, args=(s,)) for s in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not bad, bad[:3]
