@@ -49,11 +49,11 @@ __global__ void __launch_bounds__(REPACK_THREADS)
             continue;
         }
         if constexpr (VEC == 16)
-            *reinterpret_cast<v4i*>(d) = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(s));
+            *reinterpret_cast<v4i*>(d) = *reinterpret_cast<const v4i*>(s);
         else if constexpr (VEC == 8)
-            *reinterpret_cast<v2i*>(d) = __builtin_nontemporal_load(reinterpret_cast<const v2i*>(s));
+            *reinterpret_cast<v2i*>(d) = *reinterpret_cast<const v2i*>(s);
         else
-            *reinterpret_cast<int*>(d) = __builtin_nontemporal_load(reinterpret_cast<const int*>(s));
+            *reinterpret_cast<int*>(d) = *reinterpret_cast<const int*>(s);
     }
     __syncthreads();
 
@@ -73,8 +73,10 @@ __global__ void __launch_bounds__(REPACK_THREADS)
             lo = *reinterpret_cast<const v2i*>(s);
             hi = *reinterpret_cast<const v2i*>(s + REPACK_SEG);
         }
-        // streaming store: the copy is read once by the next kernel, keep it out of L2
-        __builtin_nontemporal_store(v4i{lo.x, lo.y, hi.x, hi.y}, reinterpret_cast<v4i*>(out + (size_t)c * 16));
+        // ordinary (temporal) loads and stores: the tile kernel reads the copy right after, and
+        // what stays cached of it helps (C3-sized A 1-3% faster end to end than with
+        // nontemporal accesses; unchanged at 8192^3 and at 2048 x 105728)
+        *reinterpret_cast<v4i*>(out + (size_t)c * 16) = v4i{lo.x, lo.y, hi.x, hi.y};
     }
 }
 
