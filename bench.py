@@ -3,14 +3,21 @@ MFMA peak.
 
 A step is one mxfp6_gemm_async call: the whole hot path the router picks for the shape (for the
 default workload: the repack of A into the preshuffled layout, then the 256x256 tile kernel),
-over operands already resident in HBM. Default workload: M = N = K = 8192, FP16 out, A and B
+over operands already resident in HBM, with the plan's whole workspace
+(mxfp6_gemm_preferred_workspace_size). Default workload: M = N = K = 8192, FP16 out, A and B
 drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX rule.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--all] [--no-cpu]
+                  [--no-ref]
   python bench.py --prep      (device operand preparation: float -> MXFP6 device layouts, GB/s)
 
-Prints one JSON line per workload (only the default one unless --all). Besides the contract
-fields it reports:
+Prints one JSON line per workload (only the default one unless --all). The headline `value` is
+the mean over exactly K timed steps after W warm-up steps (no extra warm-up: an idle MI355X sits
+in deep sleep near 160 MHz, so a short warm-up leaves part of the clock ramp inside the timed
+loop; `sclk_mhz` reports the clock the loop ran at). Besides the contract fields it reports:
+  sclk_mhz      the graphics clock sampled (amdsmi GPU metrics, mean over the XCDs) while the timed
+                loop ran, and frac_at_sclk = value / (4,194,304 flop/clk x sclk), the fraction of
+                the dense MXFP6 MFMA peak at the clock the chip actually ran;
   roofline      the dominant kernel (the tile kernel) against the dense MXFP6 MFMA peak: its
                 algorithmic flops per launch / its average launch duration, timed live with HIP
                 events on the launch stream in a second loop of K steps that issues the step's
@@ -18,13 +25,23 @@ fields it reports:
                 traffic = HBM bytes per launch from the committed rocprofv3 counter summary of
                 the same kernel and workload (FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel
                 calibration), null when no summary matches;
+  vs_baseline   value / the reference GPU library's TFLOPs on the same operands in this process
+                (oracle/_ref/libmxfp6ref.so, built from the reference's own sources; its own
+                router and workspace), timed by the reference's method (tests/test_gemm.cpp:33-55:
+                8 warm-ups, best mean of 4 x 20 back-to-back launches) after the headline loop;
+  per_config    the five workloads, this library and the reference library each timed by that
+                same method on identical operands: TFLOPs, fraction of 10.1 PF, ratio, and for the
+                split-K workload the algorithmic HBM GB/s;
   cpu_baseline  the reference CPU GEMM's arithmetic on this host (a bounded sample, scaled).
+The reference library and the oracle are baselines only: nothing here routes the measured GEMM
+through them.
 """
 import argparse
 import json
 import os
 import re
 import sys
+import threading
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -38,6 +55,8 @@ SEED = 0x4D584636
 # MI355X published dense MXFP6 / MXFP4 MFMA peak (TFLOP/s) and HBM bandwidth (GB/s)
 PEAK_TFLOPS = 10100.0
 PEAK_HBM_GBS = 8000.0
+# dense MXFP6 MFMA flops per clock: 256 CUs x 4 SIMDs x 131,072 flop per 32-cycle 32x32x64 MFMA
+FLOP_PER_CLK = 256 * 4 * 2 * 32 * 32 * 64 // 32
 
 # name -> (M, N, K, out_type, (dist_a, sigma_a), (dist_b, sigma_b), description)
 CONFIGS = {
@@ -53,6 +72,7 @@ CONFIGS = {
            (mx.DIST_STUDENT_T3, 1.0), "A,B ~ Student-t(3)"),
 }
 PROFILES = os.path.join(ROOT, "profiles")
+METRIC = "MXFP6 GEMM TFLOPs (FP16 out) and % of MXFP6 MFMA peak, 1xMI355X"
 
 
 def log(msg):
@@ -84,6 +104,68 @@ def profiled_traffic(workload, kernel):
         if w and k and b and w.group(1) == workload and k.group(1).strip() == kernel:
             return float(b.group(1))
     return None
+
+
+class ClockSampler:
+    """Samples the graphics clock of the GPU behind cuda:0 (amdsmi GPU metrics: the current
+    clock of each XCD, averaged) in a background thread between start() and stop(). stop()
+    returns the mean over the samples in MHz, or None when amdsmi is unavailable."""
+
+    def __init__(self):
+        self.handle, self.error = None, None
+        try:
+            import amdsmi
+            import torch
+            self.amdsmi = amdsmi
+            amdsmi.amdsmi_init()
+            handles = amdsmi.amdsmi_get_processor_handles()
+            prop = torch.cuda.get_device_properties(0)
+            want = (getattr(prop, "pci_domain_id", 0), getattr(prop, "pci_bus_id", -1),
+                    getattr(prop, "pci_device_id", 0))
+            for h in handles:
+                bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)  # "dddd:bb:dd.f"
+                dom, bus, rest = bdf.split(":")
+                if (int(dom, 16), int(bus, 16), int(rest.split(".")[0], 16)) == want:
+                    self.handle = h
+            if self.handle is None and len(handles) == 1:
+                self.handle = handles[0]
+            if self.handle is None:
+                self.error = f"no amdsmi device matches PCI {want}"
+        except Exception as e:  # no amdsmi, no permission, no device
+            self.error = f"{type(e).__name__}: {e}"
+        self.samples, self._stop, self._th = [], threading.Event(), None
+
+    def read(self):
+        m = self.amdsmi.amdsmi_get_gpu_metrics_info(self.handle)
+        vals = m.get("current_gfxclks")
+        vals = vals if isinstance(vals, (list, tuple)) else [m.get("current_gfxclk")]
+        vals = [v for v in vals if isinstance(v, int) and 0 < v < 0xFFFF]
+        return sum(vals) / len(vals) if vals else None
+
+    def _run(self):
+        while not self._stop.is_set():
+            try:
+                v = self.read()
+            except Exception as e:
+                self.error = f"{type(e).__name__}: {e}"
+                return
+            if v is not None:
+                self.samples.append(v)
+            time.sleep(0.0002)
+
+    def start(self):
+        self.samples.clear()
+        self._stop.clear()
+        if self.handle is not None:
+            self._th = threading.Thread(target=self._run, daemon=True)
+            self._th.start()
+
+    def stop(self):
+        self._stop.set()
+        if self._th is not None:
+            self._th.join()
+            self._th = None
+        return round(sum(self.samples) / len(self.samples), 1) if self.samples else None
 
 
 def cpu_baseline(p, target_cpu_s=12.0):
@@ -130,70 +212,172 @@ def copy_calibration(mib=256, reps=5):
     log(f"[bench] copy calibration: {reps} copies of {mib} MiB")
 
 
-def run_config(name, steps, warmup, with_cpu):
+def reference_library():
+    """The reference GPU library built from its own sources (oracle/_ref), or None."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    try:
+        import oracle
+        return oracle.ref()
+    except Exception as e:
+        log(f"[bench] reference library unavailable: {e}")
+        return None
+
+
+def best_of(fn, stream, reps=4, n=20, warm=8):
+    """The reference's timing method (tests/test_gemm.cpp:33-55): `warm` calls, then `reps`
+    repetitions of `n` back-to-back calls between two events; returns (best mean, median mean)
+    in milliseconds."""
     import torch
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    means = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(n):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        means.append(a.elapsed_time(b) / n)
+    return min(means), float(np.median(means))
 
-    M, N, K, out_type, (da, sa_), (db, sb_), desc = CONFIGS[name]
-    cfg_idx = int(name[1:])
-    t0 = time.perf_counter()
-    p = mx.make_problem(M, N, K, da, sa_, db, sb_, seed=SEED ^ cfg_idx)
-    tile = mx.choose_tile(M, N, p.Kp)
-    S = mx.splitk_segments(M, N, p.Kp)
-    repack = mx.repacks_a(M, N, p.Kp)
-    bsh, sa, sb = p.layouts(tile)
-    dev = torch.device("cuda:0")
-    dA = torch.from_numpy(p.a_packed).to(dev)
-    dB = torch.from_numpy(bsh).to(dev)
-    dsa = torch.from_numpy(sa).to(dev)
-    dsb = torch.from_numpy(sb).to(dev)
-    D = torch.empty(M * N * mx.OUT_BYTES[out_type], dtype=torch.uint8, device=dev)
-    ws_bytes = mx.workspace_size(M, N, p.Kp)
-    ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
-    log(f"[bench] {name}: {M}x{N}x{K} (Kp {p.Kp}) tile {tile} S {S} repack A {repack} "
-        f"ws {ws_bytes} B; inputs ready in {time.perf_counter() - t0:.1f} s")
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
-    args = (out_type, M, N, p.Kp, dA.data_ptr(), dB.data_ptr(), dsa.data_ptr(), dsb.data_ptr(),
-            D.data_ptr(), p.a_row_bytes, ws.data_ptr() if ws_bytes else 0, ws_bytes)
 
-    def step():
-        rc = mx.gemm(*args, stream=sp)
+class Workload:
+    """Device operands of one workload for this library's route and, when the reference library
+    is given, for the reference library's own route (its scale grouping and workspace)."""
+
+    def __init__(self, name, ref=None):
+        import torch
+        M, N, K, ot, (da, sa_), (db, sb_), desc = CONFIGS[name]
+        self.name, self.M, self.N, self.K, self.ot, self.desc = name, M, N, K, ot, desc
+        t0 = time.perf_counter()
+        p = mx.make_problem(M, N, K, da, sa_, db, sb_, seed=SEED ^ int(name[1:]))
+        self.p = p
+        dev = torch.device("cuda:0")
+        self.tile = mx.choose_tile(M, N, p.Kp)
+        self.S = mx.splitk_segments(M, N, p.Kp)
+        self.repack = mx.repacks_a(M, N, p.Kp)
+        bsh, sa, sb = p.layouts(self.tile)
+        self.dA = torch.from_numpy(p.a_packed).to(dev)
+        self.dB, self.dsa, self.dsb = (torch.from_numpy(x).to(dev) for x in (bsh, sa, sb))
+        self.D = torch.empty(M * N * mx.OUT_BYTES[ot], dtype=torch.uint8, device=dev)
+        self.ws_bytes = mx.preferred_workspace_size(M, N, p.Kp)
+        self.ws = torch.empty(max(self.ws_bytes, 4), dtype=torch.uint8, device=dev)
+        self.ref = ref
+        if ref is not None:
+            import ctypes as C
+            tr = (C.c_int * 4)()
+            ref.ref_choose_tile(M, N, p.Kp, tr)
+            self.ref_tile = tuple(tr)
+            if self.ref_tile == tuple(self.tile):
+                self.rB, self.rsa, self.rsb = self.dB, self.dsa, self.dsb
+            else:
+                rbsh, rsa, rsb = p.layouts(self.ref_tile)
+                self.rB, self.rsa, self.rsb = (torch.from_numpy(x).to(dev)
+                                               for x in (rbsh, rsa, rsb))
+            self.rws_bytes = ref.ref_gemm_workspace_size(M, N, p.Kp)
+            self.rws = torch.empty(max(self.rws_bytes, 4), dtype=torch.uint8, device=dev)
+            self.rD = torch.empty_like(self.D)
+        self.flops = 2.0 * M * N * K
+        log(f"[bench] {name}: {M}x{N}x{K} (Kp {p.Kp}) tile {self.tile} S {self.S} repack A "
+            f"{self.repack} ws {self.ws_bytes} B; inputs ready in {time.perf_counter() - t0:.1f} s")
+
+    def ours(self, stream):
+        rc = mx.gemm(self.ot, self.M, self.N, self.p.Kp, self.dA.data_ptr(), self.dB.data_ptr(),
+                     self.dsa.data_ptr(), self.dsb.data_ptr(), self.D.data_ptr(),
+                     self.p.a_row_bytes, self.ws.data_ptr() if self.ws_bytes else 0,
+                     self.ws_bytes, stream=stream.cuda_stream)
         if rc != 0:
             raise RuntimeError(f"mxfp6_gemm failed: {mx.STATUS.get(rc, rc)}")
 
-    flops = 2.0 * M * N * K
+    def theirs(self, stream):
+        # the reference API launches on the null stream; the timing events go on that stream too
+        self.ref.ref_gemm(self.ot, self.M, self.N, self.p.Kp, self.dA.data_ptr(),
+                          self.rB.data_ptr(), self.rsa.data_ptr(), self.rsb.data_ptr(),
+                          self.rD.data_ptr(), self.p.a_row_bytes, self.p.b_row_bytes,
+                          self.rws.data_ptr() if self.rws_bytes else None, self.rws_bytes)
+
+    def agree(self):
+        """Loose sanity check between the two libraries' outputs (full parity is the tests'
+        job): the largest difference relative to the largest magnitude."""
+        import torch
+        tt = {0: torch.float32, 1: torch.float16, 2: torch.bfloat16}[self.ot]
+        a = self.D.view(tt).float()
+        b = self.rD.view(tt).float()
+        return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+def compare(w, stream):
+    """This library and the reference library on the same operands, by the reference's timing
+    method, one after the other."""
+    import torch
+    null = torch.cuda.default_stream()
+    ms_o, med_o = best_of(lambda: w.ours(stream), stream)
+    out = {"workload": workload_name(w.M, w.N, w.K, w.ot), "tile": list(w.tile),
+           "splitk": w.S, "a_repacked": w.repack, "us": round(ms_o * 1e3, 2),
+           "tflops": round(w.flops / ms_o / 1e9, 1),
+           "frac": round(w.flops / ms_o / 1e9 / PEAK_TFLOPS, 4),
+           "median_us": round(med_o * 1e3, 2)}
+    if w.S > 1:
+        # algorithmic bytes, and with the split-K partials written and read back
+        ab = alg_bytes(w.M, w.N, w.K, w.ot)
+        out["hbm_gbs_alg"] = round(ab / ms_o / 1e6, 1)
+        out["hbm_gbs_alg_with_partials"] = round(
+            (ab + 2 * 4 * w.S * w.M * w.N) / ms_o / 1e6, 1)
+    if w.ref is not None:
+        ms_r, med_r = best_of(lambda: w.theirs(null), null)
+        tf_r = w.flops / ms_r / 1e9
+        out.update({"ref_tile": list(w.ref_tile), "ref_us": round(ms_r * 1e3, 2),
+                    "ref_tflops": round(tf_r, 1), "ref_median_us": round(med_r * 1e3, 2),
+                    "ratio": round(ms_r / ms_o, 3), "max_rel_diff_vs_ref": w.agree()})
+    log(f"[bench] {w.name}: ours {out['us']} us ({out['tflops']} TF)" +
+        (f" | reference {out['ref_us']} us ({out['ref_tflops']} TF) | ratio {out['ratio']}"
+         if w.ref is not None else ""))
+    return out
+
+
+def headline(name, steps, warmup, ref, clock):
+    """The contract measurement of one workload: `warmup` untimed steps, then exactly `steps`
+    steps between two synchronisations; then the dominant kernel timed alone."""
+    import torch
+    w = Workload(name, ref)
+    M, N, K, p = w.M, w.N, w.K, w.p
+    stream = torch.cuda.current_stream()
     for _ in range(warmup):
-        step()
+        w.ours(stream)
     torch.cuda.synchronize()
-    # timed region: exactly `steps` steps between two synchronisations
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    clock.start()
     w0 = time.perf_counter()
     ev0.record(stream)
     for _ in range(steps):
-        step()
+        w.ours(stream)
     ev1.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - w0) * 1e3
+    sclk = clock.stop()
     ms = ev0.elapsed_time(ev1) / steps
-    tflops = flops / (ms * 1e-3) / 1e12
+    tflops = w.flops / (ms * 1e-3) / 1e12
 
     # dominant kernel: the same launches issued one by one, HIP events around the tile kernel
     kernel_name = "slab_kernel"
-    if S == 1 and repack:
-        ash = torch.empty(M * p.Kp // 4 * 3, dtype=torch.uint8, device=dev)
+    if w.S == 1 and w.repack:
+        ash = torch.empty(mx.preshuffled_bytes(M, p.Kp), dtype=torch.uint8, device="cuda:0")
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(steps)]
+        sp = stream.cuda_stream
 
         def split_step(i):
             # what gemm() does for this plan, launch by launch: repack A, then the tile kernel
             # reading the repacked copy (A layout 2)
-            if mx.preshuffle_rows(dA.data_ptr(), p.a_row_bytes, M, p.Kp, ash.data_ptr(), sp):
+            if mx.preshuffle_rows(w.dA.data_ptr(), p.a_row_bytes, M, p.Kp, ash.data_ptr(), sp):
                 raise RuntimeError("repack failed")
             if i >= 0:
                 evs[i][0].record(stream)
-            rc = mx.gemm_explicit(out_type, M, N, p.Kp, tile, 1, ash.data_ptr(), dB.data_ptr(),
-                                  dsa.data_ptr(), dsb.data_ptr(), D.data_ptr(), p.a_row_bytes,
-                                  stream=sp, a_layout=mx.A_PRESHUFFLED)
+            rc = mx.gemm_explicit(w.ot, M, N, p.Kp, w.tile, 1, ash.data_ptr(), w.dB.data_ptr(),
+                                  w.dsa.data_ptr(), w.dsb.data_ptr(), w.D.data_ptr(),
+                                  p.a_row_bytes, stream=sp, a_layout=mx.A_PRESHUFFLED)
             if rc != 0:
                 raise RuntimeError(f"mxfp6_gemm_explicit failed: {mx.STATUS.get(rc, rc)}")
             if i >= 0:
@@ -202,23 +386,24 @@ def run_config(name, steps, warmup, with_cpu):
         for _ in range(max(2, warmup // 2)):
             split_step(-1)
         torch.cuda.synchronize()
+        clock.start()
         for i in range(steps):
             split_step(i)
         torch.cuda.synchronize()
+        k_sclk = clock.stop()
         k_ms = sum(a.elapsed_time(b) for a, b in evs) / steps
         kernel_scope = "tile kernel alone (repack of A timed outside)"
     else:
-        k_ms = ms
-        kernel_scope = "whole step (" + ("tile kernel + split-K reduce" if S > 1 else
+        k_ms, k_sclk = ms, sclk
+        kernel_scope = "whole step (" + ("tile kernel + split-K reduce" if w.S > 1 else
                                          "tile kernel") + ")"
-    k_tflops = flops / (k_ms * 1e-3) / 1e12
-
-    log(f"[bench] {name}: {ms * 1e3:.1f} us/step over {steps} steps ({tflops:.1f} TFLOP/s), "
-        f"tile kernel {k_ms * 1e3:.1f} us ({k_tflops:.1f} TFLOP/s), wall {wall_ms:.1f} ms")
-    workload = workload_name(M, N, K, out_type)
-    traffic = profiled_traffic(workload, kernel_name)
+    k_tflops = w.flops / (k_ms * 1e-3) / 1e12
+    log(f"[bench] {name}: {ms * 1e3:.1f} us/step over {steps} steps ({tflops:.1f} TFLOP/s, "
+        f"sclk {sclk} MHz), tile kernel {k_ms * 1e3:.1f} us ({k_tflops:.1f} TFLOP/s, sclk "
+        f"{k_sclk} MHz), wall {wall_ms:.1f} ms")
+    workload = workload_name(M, N, K, w.ot)
     out = {
-        "metric": "MXFP6 GEMM TFLOPs (FP16 out) and % of MXFP6 MFMA peak, 1xMI355X",
+        "metric": METRIC,
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -231,20 +416,57 @@ def run_config(name, steps, warmup, with_cpu):
         "dtype": "mxfp6_e2m3 (fp32 accumulate)",
         "data": "synthetic",
         "config": {"workload": workload, "M": M, "N": N, "K": K, "Kp": p.Kp,
-                   "out": mx.OUT_NAMES[out_type], "inputs": desc, "tile": list(tile),
-                   "splitk": S, "a_repacked": repack, "a_layout": "compact row-major",
-                   "parallelism": "single GPU"},
+                   "out": mx.OUT_NAMES[w.ot], "inputs": w.desc, "tile": list(w.tile),
+                   "splitk": w.S, "a_repacked": w.repack, "a_layout": "compact row-major",
+                   "workspace_bytes": w.ws_bytes, "parallelism": "single GPU"},
         "pct_of_peak": round(100.0 * tflops / PEAK_TFLOPS, 2),
-        "hbm_gbs_alg": round(alg_bytes(M, N, K, out_type) / (ms * 1e-3) / 1e9, 1),
+        "sclk_mhz": sclk,
+        "frac_at_sclk": round(tflops * 1e12 / (FLOP_PER_CLK * sclk * 1e6), 4) if sclk else None,
+        "hbm_gbs_alg": round(alg_bytes(M, N, K, w.ot) / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(k_tflops / PEAK_TFLOPS, 4),
-                     "traffic": traffic, "kernel": kernel_name, "scope": kernel_scope,
-                     "kernel_ms": round(k_ms, 6)},
+                     "traffic": profiled_traffic(workload, kernel_name), "kernel": kernel_name,
+                     "scope": kernel_scope, "kernel_ms": round(k_ms, 6), "sclk_mhz": k_sclk,
+                     "frac_at_sclk": (round(k_tflops * 1e12 / (FLOP_PER_CLK * k_sclk * 1e6), 4)
+                                      if k_sclk else None)},
     }
-    if with_cpu:
-        log(f"[bench] {name}: CPU baseline ...")
-        out["cpu_baseline"] = cpu_baseline(p)
-    return out
+    if clock.error:
+        out["sclk_note"] = clock.error
+    return w, out
+
+
+def run(names, steps, warmup, with_cpu, with_ref, per_config):
+    import torch
+    ref = reference_library() if with_ref else None
+    clock = ClockSampler()
+    lines = []
+    for n in names:
+        w, out = headline(n, steps, warmup, ref, clock)
+        if ref is not None:
+            c = compare(w, torch.cuda.current_stream())
+            out["vs_baseline"] = round(out["value"] / c["ref_tflops"], 3)
+            out["baseline"] = {
+                "kind": "reference GPU library (libmxfp6gemm built from its own sources), same "
+                        "process, same operands, its own router; timed by its own method "
+                        "(8 warm-ups, best mean of 4 x 20 launches)",
+                "value": c["ref_tflops"], "unit": "TFLOP/s", "tile": c["ref_tile"],
+                "ours_same_method_tflops": c["tflops"], "ratio_same_method": c["ratio"]}
+        if with_cpu and n == names[0]:
+            log(f"[bench] {n}: CPU baseline ...")
+            out["cpu_baseline"] = cpu_baseline(w.p)
+        lines.append((w, out))
+        del w
+        torch.cuda.empty_cache()
+    if per_config:
+        pc = {}
+        for n in sorted(CONFIGS):
+            w = Workload(n, ref)
+            pc[n] = compare(w, torch.cuda.current_stream())
+            del w
+            torch.cuda.empty_cache()
+        lines[0][1]["per_config"] = pc
+    for _, out in lines:
+        print(json.dumps(out), flush=True)
 
 
 def run_prep(steps, warmup):
@@ -322,14 +544,16 @@ def run_prep(steps, warmup):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # long enough for the power controller's clock transient at the start of a burst of GEMMs
-    # to settle (tens of milliseconds on MI355X)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    ap.add_argument("--all", action="store_true", help="every workload, one JSON line each")
+    ap.add_argument("--all", action="store_true",
+                    help="a headline line for every workload (vs_baseline each)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-clock", action="store_true", help=argparse.SUPPRESS)  # accepted, no-op
+    ap.add_argument("--no-ref", action="store_true",
+                    help="skip the reference library baseline (vs_baseline null)")
+    ap.add_argument("--no-per-config", action="store_true",
+                    help="skip the per-workload comparison block")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run the 256 MiB copy kernel that calibrates the HBM byte counters")
     ap.add_argument("--prep", action="store_true",
@@ -346,9 +570,8 @@ def main():
     if a.prep:
         print(json.dumps(run_prep(a.steps, a.warmup)), flush=True)
         return
-    names = sorted(CONFIGS) if a.all else [a.config]
-    for n in names:
-        print(json.dumps(run_config(n, a.steps, a.warmup, not a.no_cpu)), flush=True)
+    names = sorted(CONFIGS, key=lambda n: n != a.config) if a.all else [a.config]
+    run(names, a.steps, a.warmup, not a.no_cpu, not a.no_ref, not a.no_per_config and not a.all)
 
 
 if __name__ == "__main__":

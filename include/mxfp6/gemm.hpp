@@ -41,7 +41,9 @@ struct TileChoice {
 TileChoice choose_tile(int M, int N, int Kp);
 
 // Bytes of FP32 split-K workspace gemm() uses for (M, N, Kp); 0 when the shape is not split.
-// The buffer is owned by the caller (allocate once, reuse; one per concurrent stream).
+// The buffer is owned by the caller (allocate once, reuse; one per concurrent stream). A larger
+// workspace (mxfp6_gemm_preferred_workspace_size in mxfp6_gemm.h) also lets gemm() repack A into
+// the layout its kernel reads fastest; the output is the same bits.
 size_t gemm_workspace_size(int M, int N, int Kp);
 
 // Launches D = A·B on the null stream; asynchronous to the host.
@@ -53,7 +55,8 @@ size_t gemm_workspace_size(int M, int N, int Kp);
 //   B_row_bytes is accepted for interface compatibility; B is addressed via its preshuffle.
 //   ws / ws_bytes: split-K workspace sized by gemm_workspace_size(); (nullptr, 0) never
 //   splits. A shape that would split with a missing or short workspace runs unsplit and a
-//   warning goes to stderr.
+//   warning goes to stderr. Extra workspace bytes beyond the partials may hold a repacked copy
+//   of A (see gemm_workspace_size).
 void gemm(OutType ot, int M, int N, int Kp, const void* dA, const void* dBsh, const uint8_t* dsA,
           const uint8_t* dsB, void* dD, int A_row_bytes, int B_row_bytes, void* ws, size_t ws_bytes);
 

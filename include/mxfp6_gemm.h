@@ -41,11 +41,18 @@ int mxfp6_kpad(int K);
 /* choose_tile(M, N, Kp) -> tile[4] = {MT, NT, MPW, NPW}.   Replaces gemm.hpp:46 / gemm.cpp:12-59. */
 int mxfp6_choose_tile(int M, int N, int Kp, int tile[4]);
 
-/* gemm_workspace_size(M, N, Kp): workspace bytes gemm() uses for (M, N, Kp), 0 if none: the
- * split-K FP32 partials of a split shape, plus (at the next 256-byte boundary) M * packed(Kp)
- * bytes when the plan repacks A into the preshuffled operand layout first (mxfp6_gemm_repacks_a).
- * Replaces gemm.hpp:53 / gemm.cpp:61-63 (there: the split-K partials only). */
+/* gemm_workspace_size(M, N, Kp): bytes of FP32 split-K partials gemm() uses for (M, N, Kp)
+ * (splits * M * N * 4), 0 when the shape is not split.   Replaces gemm.hpp:53 / gemm.cpp:61-63
+ * (same meaning). */
 size_t mxfp6_gemm_workspace_size(int M, int N, int Kp);
+
+/* The routed plan's whole workspace: the split-K partials, then (at the next 256-byte boundary)
+ * ceil(M/32)*32 * packed(Kp) bytes when the plan repacks A into the preshuffled operand layout
+ * first (mxfp6_gemm_repacks_a); 0 when the plan needs neither. gemm() given at least this much
+ * runs the repack; given only mxfp6_gemm_workspace_size's bytes it reads A row-major: the same
+ * output bits, slower on the shapes that repack. No counterpart in the reference (its kernels
+ * read A row-major). */
+size_t mxfp6_gemm_preferred_workspace_size(int M, int N, int Kp);
 
 /* Number of K segments gemm() uses for (M, N, Kp) when given a sufficient workspace.
  * Replaces src/dispatch.hpp:30-53 (detail::splitk_S). */
@@ -61,8 +68,9 @@ int mxfp6_splitk_segments(int M, int N, int Kp);
  * them, mxfp6_prepare_* and mxfp6_prepare_b / mxfp6_prepare_scales produce them. The scales are
  * tiled with the MPW / NPW choose_tile returns for the shape. Plus a status: a shape that would
  * split with a NULL or short workspace runs unsplit (stderr warning, status MXFP6_OK), as the
- * reference does. A workspace too short for the repacked A (but long enough for the partials)
- * only skips the repack: same result, slower. */
+ * reference does. A workspace of at least mxfp6_gemm_preferred_workspace_size bytes also holds
+ * the repacked A; a shorter one (such as exactly mxfp6_gemm_workspace_size's) skips the repack:
+ * same result, slower. */
 int mxfp6_gemm(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
                const uint8_t* dsA, const uint8_t* dsB, void* dD, int A_row_bytes, int B_row_bytes,
                void* ws, size_t ws_bytes);
@@ -151,7 +159,11 @@ int mxfp6_preprocess_scale(const uint8_t* scales, int dim, int K, uint8_t* out);
  * preprocess.hpp:182-207 (the reference reads rows of exactly 3*K/4 bytes). */
 int mxfp6_preshuffle_b(const uint8_t* packed, int N, int K, int row_bytes, uint8_t* out);
 
-/* tile_scale: preprocess_scale output for (dim, K) -> grouped layout.   preprocess.hpp:216-233 */
+/* tile_scale: preprocess_scale output for (dim, K) -> grouped layout.   preprocess.hpp:216-233
+ * group must divide dim / 32 (the header's tile_scale drops a partial last group, which a masked
+ * tile would read): otherwise mxfp6_tile_scale_bytes returns 0 and mxfp6_tile_scale
+ * MXFP6_ERR_ARG. mxfp6_prepare_scales / mxfp6_tiled_scale_bytes give the zero-extended layout of
+ * any grouping. */
 size_t mxfp6_tile_scale_bytes(int dim, int K, int group, int subs);
 int mxfp6_tile_scale(const uint8_t* pscale, int dim, int K, int group, int subs, uint8_t* out);
 

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <tuple>
+
 namespace mxfp6_dev {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -55,6 +57,23 @@ template <typename T>
 __device__ __forceinline__ uint32_t half_bits(T h) {
     static_assert(sizeof(T) == 2, "16-bit type");
     return __builtin_bit_cast(uint16_t, h);
+}
+
+// Launches kernel k on stream st through hipLaunchKernel and returns that launch's own status, so
+// an entry point's status neither reports nor clears an error left by an earlier runtime call of
+// the caller's (as reading hipGetLastError after a <<<>>> launch would). The arguments are
+// converted to the kernel's parameter types first.
+template <typename... KArgs, typename... Args>
+inline hipError_t launch_kernel(void (*k)(KArgs...), dim3 grid, dim3 block, hipStream_t st,
+                                Args... args) {
+    static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
+    std::tuple<KArgs...> a(args...);
+    return std::apply(
+        [&](auto&... v) {
+            void* p[] = {static_cast<void*>(&v)...};
+            return hipLaunchKernel(reinterpret_cast<const void*>(k), grid, block, p, 0, st);
+        },
+        a);
 }
 
 // First K-tile and K-tile count of split segment z when k_tiles tiles are divided into S

@@ -2,6 +2,7 @@
 // a stream. This file, the tile kernel's instantiation units (slab_*.hip) and the kernels they
 // include are the only HIP code in the library.
 #include <algorithm>
+#include <atomic>
 
 #include "../hip_layer.h"
 #include "direct_kernel.hpp"
@@ -14,17 +15,22 @@ using namespace mxfp6_dev;
 
 namespace {
 
+// Every launcher returns 0, 1 (no kernel for the descriptor) or 2 (a launch failed).
+int status_of(hipError_t e) {
+    return e == hipSuccess ? 0 : 2;
+}
+
 template <typename OutT>
 int launch_reduce(const mxfp6_launch_desc* d, hipStream_t st) {
     const size_t total = (size_t)d->M * d->N;
     OutT* D = static_cast<OutT*>(d->D);
     if (total % 4 == 0)
-        reduce_splitk_kernel<OutT, 4><<<dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0, st>>>(
-            d->ws, D, total, d->splits);
-    else
-        reduce_splitk_kernel<OutT, 1><<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st>>>(
-            d->ws, D, total, d->splits);
-    return 0;
+        return status_of(launch_kernel(reduce_splitk_kernel<OutT, 4>,
+                                       dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), st,
+                                       d->ws, D, total, d->splits));
+    return status_of(launch_kernel(reduce_splitk_kernel<OutT, 1>,
+                                   dim3((unsigned)((total + 255) / 256)), dim3(256), st, d->ws, D,
+                                   total, d->splits));
 }
 
 template <typename OutT>
@@ -33,16 +39,15 @@ int launch_direct(const mxfp6_launch_desc* d, hipStream_t st) {
     const uint8_t* A = static_cast<const uint8_t*>(d->A);
     const uint8_t* B = static_cast<const uint8_t*>(d->Bsh);
     if (d->splits > 1) {
-        direct_kernel<float, true><<<grid, dim3(256), 0, st>>>(A, B, d->sA, d->sB, nullptr, d->ws,
-                                                              d->M, d->N, d->Kp, d->A_row_bytes,
-                                                              d->mpw, d->npw, d->splits);
+        if (launch_kernel(direct_kernel<float, true>, grid, dim3(256), st, A, B, d->sA, d->sB,
+                          nullptr, d->ws, d->M, d->N, d->Kp, d->A_row_bytes, d->mpw, d->npw,
+                          d->splits) != hipSuccess)
+            return 2;
         return launch_reduce<OutT>(d, st);
     }
-    direct_kernel<OutT, false><<<grid, dim3(256), 0, st>>>(A, B, d->sA, d->sB,
-                                                          static_cast<OutT*>(d->D), nullptr, d->M,
-                                                          d->N, d->Kp, d->A_row_bytes, d->mpw,
-                                                          d->npw, 1);
-    return 0;
+    return status_of(launch_kernel(direct_kernel<OutT, false>, grid, dim3(256), st, A, B, d->sA,
+                                   d->sB, static_cast<OutT*>(d->D), nullptr, d->M, d->N, d->Kp,
+                                   d->A_row_bytes, d->mpw, d->npw, 1));
 }
 
 template <typename OutT>
@@ -78,15 +83,31 @@ extern "C" int mxfp6_hip_launch(const mxfp6_launch_desc* d) {
         default:
             return 1;
     }
-    if (rc != 0) return rc;
-    return hipGetLastError() == hipSuccess ? 0 : 2;
+    return rc;
 }
 
 extern "C" int mxfp6_hip_repack(const void* src, int row_bytes, int rows, int Kp, void* dst,
                                 void* stream) {
-    repack_rows_launch(static_cast<const uint8_t*>(src), row_bytes, rows, Kp / 64,
-                       static_cast<uint8_t*>(dst), static_cast<hipStream_t>(stream));
-    return hipGetLastError() == hipSuccess ? 0 : 2;
+    return status_of(repack_rows_launch(static_cast<const uint8_t*>(src), row_bytes, rows, Kp / 64,
+                                        static_cast<uint8_t*>(dst),
+                                        static_cast<hipStream_t>(stream)));
+}
+
+extern "C" int mxfp6_hip_device_cus(void) {
+    // per device: 0 = not read yet, -1 = the query failed
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev >= 64) dev = 63;
+    int c = cus[dev].load(std::memory_order_relaxed);
+    if (c == 0) {
+        int v = 0;
+        c = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0
+                ? v
+                : -1;
+        cus[dev].store(c, std::memory_order_relaxed);
+    }
+    return c > 0 ? c : 0;
 }
 
 extern "C" int mxfp6_hip_has_tile(int MT, int NT, int mpw, int npw) {
@@ -117,31 +138,23 @@ extern "C" int mxfp6_hip_quantize_rows(const float* x, int rows, int cols, int n
         // one whole output tile per wave (coalesced stores): 32-row blocks x 4 slabs per workgroup
         const dim3 g((unsigned)((Kp / 64 + PSH_SLABS - 1) / PSH_SLABS), (unsigned)(rows_out / 32));
         uint8_t* ash = static_cast<uint8_t*>(packed);
-        if (v4)
-            prep_rows_preshuffled_kernel<true><<<g, dim3(64 * PSH_SLABS), 0, st>>>(
-                x, rows, cols, Kp / 64, ash, rows32, so);
-        else
-            prep_rows_preshuffled_kernel<false><<<g, dim3(64 * PSH_SLABS), 0, st>>>(
-                x, rows, cols, Kp / 64, ash, rows32, so);
-        return hipGetLastError() == hipSuccess ? 0 : 2;
+        return status_of(launch_kernel(v4 ? prep_rows_preshuffled_kernel<true>
+                                          : prep_rows_preshuffled_kernel<false>,
+                                       g, dim3(64 * PSH_SLABS), st, x, rows, cols, Kp / 64, ash,
+                                       rows32, so));
     }
     const dim3 grid((unsigned)((size_t)rows_out * chunks));
-    if (v4)
-        prep_rows_kernel<true><<<grid, dim3(64), 0, st>>>(x, cols, nblk, po, so, chunks, rows);
-    else
-        prep_rows_kernel<false><<<grid, dim3(64), 0, st>>>(x, cols, nblk, po, so, chunks, rows);
-    return hipGetLastError() == hipSuccess ? 0 : 2;
+    return status_of(launch_kernel(v4 ? prep_rows_kernel<true> : prep_rows_kernel<false>, grid,
+                                   dim3(64), st, x, cols, nblk, po, so, chunks, rows));
 }
 
 extern "C" int mxfp6_hip_prepare_b(const float* B, int K, int N, int Kp, int group, void* bsh,
                                    uint8_t* tiled, void* stream) {
     const int NG = rows_in_groups(N, group);
     const unsigned nchunks = (unsigned)((NG + PREP_THREADS - 1) / PREP_THREADS), kchunks = (unsigned)(Kp / 32);
-    prep_b_kernel<<<dim3(nchunks * kchunks), dim3(PREP_THREADS), 0,
-                    static_cast<hipStream_t>(stream)>>>(B, K, N, NG, Kp, group,
-                                                        static_cast<uint8_t*>(bsh), tiled,
-                                                        (int)nchunks);
-    return hipGetLastError() == hipSuccess ? 0 : 2;
+    return status_of(launch_kernel(prep_b_kernel, dim3(nchunks * kchunks), dim3(PREP_THREADS),
+                                   static_cast<hipStream_t>(stream), B, K, N, NG, Kp, group,
+                                   static_cast<uint8_t*>(bsh), tiled, (int)nchunks));
 }
 
 extern "C" int mxfp6_hip_tile_scales(const uint8_t* s, int dim, int vblk, int ld, int Kp,
@@ -149,7 +162,7 @@ extern "C" int mxfp6_hip_tile_scales(const uint8_t* s, int dim, int vblk, int ld
     const int dim_out = rows_in_groups(dim, group);
     const size_t total = (size_t)dim_out * (Kp / 32);
     const unsigned blocks = (unsigned)std::min<size_t>((total + PREP_THREADS - 1) / PREP_THREADS, 65536);
-    tile_scales_kernel<<<dim3(blocks), dim3(PREP_THREADS), 0, static_cast<hipStream_t>(stream)>>>(
-        s, dim, dim_out, vblk, ld, Kp, group, tiled);
-    return hipGetLastError() == hipSuccess ? 0 : 2;
+    return status_of(launch_kernel(tile_scales_kernel, dim3(blocks), dim3(PREP_THREADS),
+                                   static_cast<hipStream_t>(stream), s, dim, dim_out, vblk, ld, Kp,
+                                   group, tiled));
 }

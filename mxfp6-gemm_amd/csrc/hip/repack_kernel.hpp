@@ -81,16 +81,14 @@ __global__ void __launch_bounds__(REPACK_THREADS)
 }
 
 // Launch: the widest load the source rows' alignment allows.
-inline void repack_rows_launch(const uint8_t* src, int row_bytes, int rows, int k64n,
-                               uint8_t* dst, hipStream_t st) {
+inline hipError_t repack_rows_launch(const uint8_t* src, int row_bytes, int rows, int k64n,
+                                     uint8_t* dst, hipStream_t st) {
     const dim3 grid((unsigned)((k64n + REPACK_KK - 1) / REPACK_KK), (unsigned)((rows + 31) / 32));
     const uintptr_t align = reinterpret_cast<uintptr_t>(src) | (uintptr_t)row_bytes;
-    if (align % 16 == 0)
-        repack_rows_kernel<16><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, rows, k64n, dst);
-    else if (align % 8 == 0)
-        repack_rows_kernel<8><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, rows, k64n, dst);
-    else
-        repack_rows_kernel<4><<<grid, dim3(REPACK_THREADS), 0, st>>>(src, row_bytes, rows, k64n, dst);
+    auto* k = align % 16 == 0 ? repack_rows_kernel<16>
+              : align % 8 == 0 ? repack_rows_kernel<8>
+                               : repack_rows_kernel<4>;
+    return launch_kernel(k, grid, dim3(REPACK_THREADS), st, src, row_bytes, rows, k64n, dst);
 }
 
 }  // namespace mxfp6_dev

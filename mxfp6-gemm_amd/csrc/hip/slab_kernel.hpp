@@ -412,17 +412,19 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
 // One launch of the tile kernel; KT is the kernel's output type (float for the split-K partials).
 template <int MT, int NT, int WM, int WN, int XG, int NS, typename KT, bool SPLIT, bool ASH,
           bool MASK>
-void slab_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipStream_t st) {
+hipError_t slab_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipStream_t st) {
     const dim3 grid((unsigned)((d->M + MT - 1) / MT), (unsigned)((d->N + NT - 1) / NT),
                     (unsigned)d->splits);
-    slab_kernel<MT, NT, WM, WN, NS, XG, KT, SPLIT, ASH, MASK><<<grid, dim3(64 * WM * WN), 0, st>>>(
-        A, static_cast<const uint8_t*>(d->Bsh), d->sA, d->sB,
-        SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr, d->M, d->N, d->Kp,
-        d->A_row_bytes, SPLIT ? d->splits : 1);
+    return launch_kernel(slab_kernel<MT, NT, WM, WN, NS, XG, KT, SPLIT, ASH, MASK>, grid,
+                         dim3(64 * WM * WN), st, A, static_cast<const uint8_t*>(d->Bsh), d->sA,
+                         d->sB, SPLIT ? nullptr : static_cast<KT*>(d->D),
+                         SPLIT ? d->ws : nullptr, d->M, d->N, d->Kp, d->A_row_bytes,
+                         SPLIT ? d->splits : 1);
 }
 
 // Ring depth per tile: as many slabs as fit 160 KiB of LDS (128 x 128 and 32 x 128: half of it,
-// two workgroups per CU). MASK when the tile does not divide M x N.
+// two workgroups per CU). MASK when the tile does not divide M x N. Returns 0, or 2 when a launch
+// fails.
 template <int MT, int NT, int WM, int WN, int XG, int NS, typename KT, bool SPLIT>
 int slab_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     static_assert(SlabGeom<MT, NT, WM, WN, NS>::LDS <= 160 * 1024, "LDS budget");
@@ -430,21 +432,24 @@ int slab_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     const uint8_t* A = static_cast<const uint8_t*>(d->A);
     if (d->a_layout == MXFP6_A_REPACK) {
         // repack A into the preshuffled layout, then run the kernel on it
-        repack_rows_launch(A, d->A_row_bytes, d->M, d->Kp / 64, static_cast<uint8_t*>(d->Ash), st);
+        if (repack_rows_launch(A, d->A_row_bytes, d->M, d->Kp / 64, static_cast<uint8_t*>(d->Ash),
+                               st) != hipSuccess)
+            return 2;
         A = static_cast<const uint8_t*>(d->Ash);
     }
+    hipError_t e;
     if (d->a_layout == MXFP6_A_ROWS) {
         if (mask)
-            slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, false, true>(d, A, st);
+            e = slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, false, true>(d, A, st);
         else
-            slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, false, false>(d, A, st);
+            e = slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, false, false>(d, A, st);
     } else {
         if (mask)
-            slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, true, true>(d, A, st);
+            e = slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, true, true>(d, A, st);
         else
-            slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, true, false>(d, A, st);
+            e = slab_kernel_launch<MT, NT, WM, WN, XG, NS, KT, SPLIT, true, false>(d, A, st);
     }
-    return 0;
+    return e == hipSuccess ? 0 : 2;
 }
 
 // Tile dispatch (declared in slab_run.hpp; instantiated once per (KT, SPLIT) in its own

@@ -25,7 +25,7 @@ inline bool tile_supported(int MT, int NT, int mpw, int npw) {
 
 // Runs the descriptor's plan on the tile kernel (after the A repack when a_layout asks for it):
 // KT = the kernel's output type, SPLIT = FP32 partials of d->splits K segments into d->ws (KT =
-// float). Returns 0, or 1 when no instantiation matches the tile.
+// float). Returns 0, 1 when no instantiation matches the tile, 2 when a launch fails.
 template <typename KT, bool SPLIT>
 int slab_run(const mxfp6_launch_desc* d, hipStream_t st);
 

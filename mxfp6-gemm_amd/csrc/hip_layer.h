@@ -49,6 +49,10 @@ int mxfp6_hip_launch(const mxfp6_launch_desc* d);
  * into the preshuffled operand layout at dst (rows * packed(Kp) bytes). 0 ok, 2 launch error. */
 int mxfp6_hip_repack(const void* src, int row_bytes, int rows, int Kp, void* dst, void* stream);
 
+/* Compute units of the current HIP device (hipDeviceAttributeMultiprocessorCount, read once per
+ * device), or 0 when the runtime reports no device. */
+int mxfp6_hip_device_cus(void);
+
 /* Whether the tile kernel has an instantiation for MT x NT with scale grouping (mpw, npw). */
 int mxfp6_hip_has_tile(int MT, int NT, int mpw, int npw);
 

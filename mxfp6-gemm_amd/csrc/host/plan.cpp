@@ -32,6 +32,7 @@ namespace plan {
 //   wg       = ceil(M / MT) * ceil(N / NT) workgroups per K segment;
 //   waves    = ceil(wg * S / (CUS * occupancy)) rounds of workgroups;
 //   per_cu   = ceil(min(wg * S, CUS * occupancy) / CUS) workgroups on the busiest CU;
+//              (CUS: the current device's compute units, 256 on an MI355X)
 //   t_slab   = max(T_SLAB_MIN, per_cu * (T_MFMA * mfmas + T_COPY_KB * copied KiB)) per 64-wide K
 //              slab: a latency floor (the ring keeps four slabs in flight), else the CU's MFMA and
 //              global->LDS copy work, shared by the workgroups resident on it; a row-major A slab
@@ -58,7 +59,7 @@ const TileChoice kCands[] = {{256, 256, 4, 4}, {256, 192, 4, 3}, {128, 384, 4, 3
                              {128, 256, 2, 4}, {128, 128, 2, 2}};
 const TileChoice kSkinny[] = {{64, 256, 2, 2}, {32, 256, 1, 2}, {64, 128, 2, 1}, {32, 128, 1, 1}};
 
-double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repack) {
+double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repack, int CUS) {
     const long wg = (long)((M + tc.MT - 1) / tc.MT) * ((N + tc.NT - 1) / tc.NT) * S;
     const int occ = (tc.NT == 128 && (tc.MT == 128 || tc.MT == 32)) ? 2 : 1;  // per CU (LDS)
     const long cap = (long)CUS * occ;
@@ -98,7 +99,7 @@ const int kNSkinny = (int)(sizeof(kSkinny) / sizeof(kSkinny[0]));
 // src/kernel.hpp:144-154, for any tile: N = 102272 runs 256x256 over ceil(N/256) columns instead
 // of 128x128); ragged shapes any of the nine, big tiles first. Shapes gemm() rejects get the
 // trivial plan.
-Plan best_plan(int M, int N, int Kp) {
+Plan best_plan(int M, int N, int Kp, int cus) {
     Plan best = {{128, 128, 2, 2}, 1, false};
     if (!shape_ok(M, N, Kp)) return best;
     double best_t = -1.0;
@@ -113,7 +114,11 @@ Plan best_plan(int M, int N, int Kp) {
                 for (int ci = 0; ci < kNCands + kNSkinny; ci++) {
                     const TileChoice& tc = ci < kNCands ? kCands[ci] : kSkinny[ci - kNCands];
                     if (reg && (M % tc.MT != 0 || (N % tc.NT != 0) != (pass == 1))) continue;
-                    const double t = plan_time_us(tc, M, N, Kp, S, rp != 0);
+                    // a regular shape's scales may be tiled by the header's tile_scale, which
+                    // holds floor(dim / (32 * group)) whole groups: the grouping must divide the
+                    // shape (an N-masked 256x192 or 128x384, NPW 3, needs (N / 32) % 3 == 0)
+                    if (reg && ((M / 32) % tc.MPW != 0 || (N / 32) % tc.NPW != 0)) continue;
+                    const double t = plan_time_us(tc, M, N, Kp, S, rp != 0, cus);
                     if (best_t < 0 || t < best_t * (1.0 - PLAN_MIN_GAIN)) {
                         best = {tc, S, rp != 0};
                         best_t = t;
@@ -125,17 +130,21 @@ Plan best_plan(int M, int N, int Kp) {
 // best_plan evaluates the model for every (tile, split, layout): a few microseconds of host time,
 // as long as a small GEMM runs on the GPU. gemm() and the routing queries look the plan up in a
 // per-thread cache of the last shapes instead (16 entries indexed by a hash of the shape; no
-// lock, and the plan of a shape never changes).
+// lock, and the plan of a shape on a device never changes). The key includes the compute-unit
+// count of the current device, which the HIP layer reads once per device.
 Plan cached_plan(int M, int N, int Kp) {
     struct Entry {
-        int M, N, Kp;
+        int M, N, Kp, cus;
         Plan plan;
         bool valid;
     };
     thread_local Entry cache[16] = {};
+    const int reported = mxfp6_hip_device_cus();
+    const int cus = reported > 0 ? reported : DEFAULT_CUS;
     const unsigned h = ((unsigned)M * 73856093u ^ (unsigned)N * 19349663u ^ (unsigned)Kp * 83492791u) >> 4;
     Entry& e = cache[h % 16];
-    if (!e.valid || e.M != M || e.N != N || e.Kp != Kp) e = {M, N, Kp, best_plan(M, N, Kp), true};
+    if (!e.valid || e.M != M || e.N != N || e.Kp != Kp || e.cus != cus)
+        e = {M, N, Kp, cus, best_plan(M, N, Kp, cus), true};
     return e.plan;
 }
 }  // namespace
@@ -166,7 +175,17 @@ int splitk_segments(int M, int N, int Kp) {
     return shape_ok(M, N, Kp) ? cached_plan(M, N, Kp).S : 1;
 }
 
+// gemm_workspace_size: the split-K partials of the routed plan, 0 when it is not split (the
+// reference's meaning, src/dispatch.hpp:55-59). With exactly that workspace gemm() runs the plan
+// on row-major A.
 size_t workspace_bytes(int M, int N, int Kp) {
+    return split_bytes(M, N, splitk_segments(M, N, Kp));
+}
+
+// The workspace of the routed plan in full: the split-K partials, then (at the next 256-byte
+// boundary) the repacked A when the plan repacks. gemm() given at least this much runs the plan
+// with the repack; the output is the same bits either way.
+size_t preferred_workspace_bytes(int M, int N, int Kp) {
     const int S = splitk_segments(M, N, Kp);
     const bool rp = route_repacks(M, N, Kp);
     return (S > 1 || rp) ? plan_bytes(M, N, Kp, S, rp) : 0;
@@ -252,8 +271,9 @@ int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void*
     if (kernel != MXFP6_KERNEL_TILE) rp = false;
     if (kernel != MXFP6_KERNEL_TILE && (M % 64 != 0 || N % 64 != 0)) return MXFP6_ERR_TILE;
     if (ws == nullptr) ws_bytes = 0;
-    // A workspace too small for the repacked A drops the repack (a pure speed choice); one too
-    // small for the split-K partials as well runs unsplit, with the reference's warning.
+    // A workspace too small for the repacked A (gemm_workspace_size's, the partials only) drops
+    // the repack, a pure speed choice with the same output bits; one too small for the split-K
+    // partials as well runs unsplit, with the reference's warning.
     if (rp && ws_bytes < plan_bytes(M, N, Kp, S, true)) rp = false;
     if (S > 1 && ws_bytes < plan_bytes(M, N, Kp, S, false)) {
         std::fprintf(stderr,
@@ -335,6 +355,10 @@ extern "C" int mxfp6_choose_tile(int M, int N, int Kp, int tile[4]) {
 
 extern "C" size_t mxfp6_gemm_workspace_size(int M, int N, int Kp) {
     return plan::workspace_bytes(M, N, Kp);
+}
+
+extern "C" size_t mxfp6_gemm_preferred_workspace_size(int M, int N, int Kp) {
+    return plan::preferred_workspace_bytes(M, N, Kp);
 }
 
 extern "C" int mxfp6_splitk_segments(int M, int N, int Kp) {

@@ -8,8 +8,9 @@
 namespace mxfp6 {
 namespace plan {
 
-// MI355X: 256 compute units (8 XCDs x 32 CUs).
-constexpr int CUS = 256;
+// Compute units the router plans for when the HIP runtime reports no device (a host without a
+// GPU): MI355X's 256 (8 XCDs x 32 CUs). On a device the count is read from it (plan.cpp).
+constexpr int DEFAULT_CUS = 256;
 // Plan-time model of the router (plan.cpp): least-squares fit on MI355X, microseconds.
 constexpr int MAX_SPLITS = 16;             // K segments considered
 constexpr double T_LAUNCH = 2.61668;       // one kernel launch (and its ramp), back to back
@@ -26,6 +27,7 @@ constexpr double PLAN_MIN_GAIN = 0.01;     // lead a more complex plan needs ove
 TileChoice route(int M, int N, int Kp);
 int splitk_segments(int M, int N, int Kp);
 size_t workspace_bytes(int M, int N, int Kp);
+size_t preferred_workspace_bytes(int M, int N, int Kp);
 bool route_repacks(int M, int N, int Kp);
 size_t plan_bytes(int M, int N, int Kp, int S, bool repack);
 int check_common(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,

@@ -240,8 +240,16 @@ extern "C" int mxfp6_preshuffle_b(const uint8_t* packed, int N, int K, int row_b
     return mxfp6_prepare_b(packed, N, K, (size_t)row_bytes, out, 1);
 }
 
+// The header's tile_scale keeps floor(dim / (32 * group)) whole groups and drops the rest; the
+// C ABI accepts only groupings that divide dim / 32, so its buffer is exactly the layout the
+// kernels read (mxfp6_tiled_scale_bytes sizes the zero-extended layout of any grouping).
+static bool tile_scale_args_ok(int dim, int K, int group, int subs) {
+    return dim > 0 && dim % 32 == 0 && K > 0 && K % 64 == 0 && group >= 1 && subs >= 1 &&
+           (dim / 32) % group == 0;
+}
+
 extern "C" size_t mxfp6_tile_scale_bytes(int dim, int K, int group, int subs) {
-    if (dim <= 0 || dim % 32 != 0 || K <= 0 || K % 64 != 0 || group < 1 || subs < 1) return 0;
+    if (!tile_scale_args_ok(dim, K, group, subs)) return 0;
     const size_t gp = (size_t)((group + 3) / 4 * 4);
     return (size_t)(dim / 32 / group) * (size_t)(K / 64 / subs) * 64 * subs * gp;
 }
@@ -249,8 +257,7 @@ extern "C" size_t mxfp6_tile_scale_bytes(int dim, int K, int group, int subs) {
 extern "C" int mxfp6_tile_scale(const uint8_t* pscale, int dim, int K, int group, int subs,
                                 uint8_t* out) {
     if (!pscale || !out) return MXFP6_ERR_NULL;
-    if (dim <= 0 || dim % 32 != 0 || K <= 0 || K % 64 != 0 || group < 1 || subs < 1)
-        return MXFP6_ERR_ARG;
+    if (!tile_scale_args_ok(dim, K, group, subs)) return MXFP6_ERR_ARG;
     PreprocessedScale ps;
     ps.dim = dim;
     ps.K = K;

@@ -39,6 +39,7 @@ SIGNATURES = {
     "mxfp6_kpad": (C.c_int, [C.c_int]),
     "mxfp6_choose_tile": (C.c_int, [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int)]),
     "mxfp6_gemm_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
+    "mxfp6_gemm_preferred_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     "mxfp6_splitk_segments": (C.c_int, [C.c_int, C.c_int, C.c_int]),
     "mxfp6_gemm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
                              C.c_int, C.c_int, _vp, C.c_size_t]),
@@ -133,7 +134,13 @@ def choose_tile(M: int, N: int, Kp: int) -> tuple:
 
 
 def workspace_size(M: int, N: int, Kp: int) -> int:
+    """gemm_workspace_size: the split-K partials only (the reference's meaning)."""
     return lib().mxfp6_gemm_workspace_size(M, N, Kp)
+
+
+def preferred_workspace_size(M: int, N: int, Kp: int) -> int:
+    """The routed plan's whole workspace: split-K partials plus the repacked A when it repacks."""
+    return lib().mxfp6_gemm_preferred_workspace_size(M, N, Kp)
 
 
 def splitk_segments(M: int, N: int, Kp: int) -> int:

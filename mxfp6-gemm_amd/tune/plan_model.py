@@ -57,7 +57,7 @@ def best_plan(c, M, N, Kp):
     requiring a PLAN_MIN_GAIN lead to replace an earlier one (as plan.cpp does). Regular shapes
     (M % 32 == 0, N % 128 == 0) take the tiles whose MT divides M, the 32- and 64-row ones
     included (the last tile column masked when NT does not divide N, visited after every dividing
-    plan); ragged ones any tile, masked."""
+    plan) whose scale grouping divides the shape; ragged ones any tile, masked."""
     best, best_t = ((128, 128, 2, 2), 1, False), None
     kt = Kp // K_TILE
     regular = M % 32 == 0 and N % 128 == 0
@@ -67,6 +67,9 @@ def best_plan(c, M, N, Kp):
             for S in range(1, min(MAX_SPLITS, kt) + 1):
                 for tile in cands:
                     if regular and (M % tile[0] or bool(N % tile[1]) != masked):
+                        continue
+                    # the header's tile_scale holds whole scale groups only
+                    if regular and ((M // 32) % tile[2] or (N // 32) % tile[3]):
                         continue
                     t = plan_time_us(c, tile, M, N, Kp, S, rp)
                     if best_t is None or t < best_t * (1.0 - PLAN_MIN_GAIN):

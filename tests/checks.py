@@ -3,6 +3,7 @@ operands over the nominal K, accumulated in FP64).
 
   FP32 output: |D - R| <= 1e-5 * sum_k |a_k b_k|      (per element; relative to the magnitude of
                the terms, so cancellation in R does not make the bound vanish)
+               and max|D - R| / max|R| <= 1e-5        (normwise over the elements compared)
   FP16/BF16:   |D - rn(R32)| <= 1 ulp(rn(R32))          R32 = float32(R), rn = round to nearest
                even in the output format, ulp = spacing of that format at |rn(R32)|
 NaN in R (a 0xFF scale) requires NaN in D.
@@ -26,8 +27,15 @@ def check_f32(D, R, absdot, rtol=F32_RTOL):
     bad = err > bound
     assert not bad.any(), (f"{bad.sum()} elements exceed {rtol}*sum|ab|; worst excess "
                            f"{(err - bound).max():.3e}")
-    denom = max(np.abs(R[ok]).max(), 1e-300) if ok.any() else 1.0
-    return float(err.max() / denom) if err.size else 0.0
+    if not err.size:
+        return 0.0
+    rmax = float(np.abs(R[ok]).max())
+    if rmax == 0.0:
+        assert err.max() == 0.0, "nonzero output where the oracle is all zero"
+        return 0.0
+    rel = float(err.max() / rmax)
+    assert rel <= rtol, f"normwise max|D-R|/max|R| = {rel:.3e} exceeds {rtol}"
+    return rel
 
 
 def round_bf16(x32: np.ndarray) -> np.ndarray:

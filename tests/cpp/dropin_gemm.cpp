@@ -9,7 +9,10 @@
 // plus one unit in the last place of the output format at |R| (FP16: 2^-10 |R|, BF16: 2^-7 |R|)
 // plus the format's smallest subnormal step.
 //
-//   dropin_gemm M N K out_type(0 = F32, 1 = F16, 2 = BF16)   -> exit status 0 when D passes
+//   dropin_gemm M N K out_type(0 = F32, 1 = F16, 2 = BF16) [ws]   -> exit status 0 when D passes
+//   ws: "ref" (default) allocates gemm_workspace_size() bytes, as a reference caller does;
+//       "preferred" allocates mxfp6_gemm_preferred_workspace_size() bytes (include/mxfp6_gemm.h),
+//       which also holds the repacked A on the shapes whose plan repacks.
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -22,6 +25,8 @@
 
 #include "mxfp6/gemm.hpp"
 #include "mxfp6/preprocess.hpp"
+#include "mxfp6_gemm.h"
+#include <cstring>
 
 using namespace mxfp6;
 
@@ -60,10 +65,11 @@ static double out_value(const std::vector<uint8_t>& D, OutType ot, size_t i) {
 }
 
 int main(int argc, char** argv) {
-    if (argc != 5) {
-        std::fprintf(stderr, "usage: %s M N K out_type\n", argv[0]);
+    if (argc != 5 && argc != 6) {
+        std::fprintf(stderr, "usage: %s M N K out_type [ref|preferred]\n", argv[0]);
         return 2;
     }
+    const bool preferred_ws = argc == 6 && std::strcmp(argv[5], "preferred") == 0;
     const int M = std::atoi(argv[1]), N = std::atoi(argv[2]), K = std::atoi(argv[3]);
     const OutType ot = (OutType)std::atoi(argv[4]);
     const size_t ob = ot == OutType::F32 ? 4 : 2;
@@ -102,7 +108,8 @@ int main(int argc, char** argv) {
     HIP_OK(hipMemcpy(dsB, sB.data.data(), sB.data.size(), hipMemcpyHostToDevice));
     HIP_OK(hipMalloc(&dD, (size_t)M * N * ob));
     HIP_OK(hipMemset(dD, 0x5A, (size_t)M * N * ob));
-    const size_t ws_bytes = gemm_workspace_size(M, N, Kp);
+    const size_t ws_bytes = preferred_ws ? mxfp6_gemm_preferred_workspace_size(M, N, Kp)
+                                         : gemm_workspace_size(M, N, Kp);
     if (ws_bytes) HIP_OK(hipMalloc(&ws, ws_bytes));
 
     // 4. launch

@@ -39,9 +39,12 @@ def to_f32(buf: torch.Tensor, out_type, M, N) -> np.ndarray:
     return buf.view(TORCH_OUT[out_type]).float().reshape(M, N).cpu().numpy()
 
 
-def run_routed(dp: DevProblem, out_type, with_ws=True, stream=None):
+def run_routed(dp: DevProblem, out_type, with_ws=True, stream=None, ws_kind="preferred"):
+    """ws_kind: "preferred" (the plan's whole workspace, repack included) or "split" (exactly
+    gemm_workspace_size's bytes, the reference's meaning: A is then read row-major)."""
     p = dp.p
-    ws_bytes = mx.workspace_size(p.M, p.N, p.Kp) if with_ws else 0
+    size = mx.preferred_workspace_size if ws_kind == "preferred" else mx.workspace_size
+    ws_bytes = size(p.M, p.N, p.Kp) if with_ws else 0
     ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device="cuda") if ws_bytes else None
     D = dp.out(out_type)
     a, b, sa, sb = dp.ptrs()

@@ -98,3 +98,16 @@ def test_prep_argument_checks_reject_before_launch(mx):
     assert mx.tiled_scale_bytes(96, 992, 3) == 1 * (1152 // 192) * 64 * 3 * 4
     assert mx.tiled_scale_bytes(96, 992, 2) == 2 * (1152 // 192) * 64 * 3 * 4
     assert mx.tiled_scale_bytes(1, 33, 4) == 1 * 1 * 64 * 3 * 4
+
+
+def test_tile_scale_rejects_partial_groups(mx):
+    """The C ABI's tile_scale (the header's floor-over-groups layout) accepts only groupings that
+    divide dim/32: a partial last group would be dropped, and a masked tile reads it."""
+    import ctypes as C
+    import numpy as np
+    assert mx.lib().mxfp6_tile_scale_bytes(416, 192, 3, 3) == 0       # 13 blocks, group 3
+    assert mx.lib().mxfp6_tile_scale_bytes(384, 192, 3, 3) == 4 * 1 * 64 * 3 * 4
+    buf = np.zeros(1 << 16, dtype=np.uint8)
+    ptr = buf.ctypes.data_as(C.c_void_p)
+    assert mx.lib().mxfp6_tile_scale(ptr, 416, 192, 3, 3, ptr) == 5
+    assert mx.lib().mxfp6_tile_scale(ptr, 384, 192, 3, 3, ptr) == 0

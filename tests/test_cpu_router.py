@@ -56,16 +56,33 @@ def test_oracle_split_plan_reference_cases(orc):
 def test_router_covers_every_multiple_of_128(mx):
     """Every M, N multiple of 128: an implemented tile (the skinny ones included) whose MT
     divides M; NT divides N or the last tile column is masked (the reference's NMASK route, for
-    any tile)."""
-    bad = masked = 0
+    any tile); the scale groupings MPW and NPW divide M/32 and N/32, so the header's tile_scale
+    (floor(dim / (32 * group)) groups) produces every scale group the kernel reads, and its size
+    equals the device layout's (mxfp6_tiled_scale_bytes, ceil over groups)."""
+    bad, badgroup, masked = [], [], 0
     for M in range(128, 16385, 128):
         for N in range(128, 24577, 128):
             for K in (512, 16128, 105728):
-                t = mx.choose_tile(M, N, _kpad(K))
+                Kp = _kpad(K)
+                t = mx.choose_tile(M, N, Kp)
                 if M % t[0] or tuple(t) not in IMPLEMENTED | SKINNY:
-                    bad += 1
+                    bad.append((M, N, K, t))
+                if (M // 32) % t[2] or (N // 32) % t[3]:
+                    badgroup.append((M, N, K, t))
                 masked += N % t[1] != 0
-    assert bad == 0 and masked > 0
+    assert not bad and not badgroup and masked > 0, (bad[:5], badgroup[:5])
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 8320, 8192), (640, 13184, 1024), (128, 6016, 105728),
+                                   (8192, 8320, 8192), (2048, 1152, 16128)])
+def test_header_tile_scale_size_matches_kernel_layout(mx, M, N, K):
+    """On shapes where an N-masked tile with three 32-column blocks per wave would have been
+    chosen, the header-sized scale buffers (tile_scale_bytes, floor) equal the size of the layout
+    the kernel reads (tiled_scale_bytes, ceil) for the routed grouping."""
+    Kp = _kpad(K)
+    t = mx.choose_tile(M, N, Kp)
+    for dim, g in ((M, t[2]), (N, t[3])):
+        assert mx.lib().mxfp6_tile_scale_bytes(dim, Kp, g, 3) == mx.tiled_scale_bytes(dim, Kp, g), (t, dim, g)
 
 
 def test_workspace_matches_split(mx):
@@ -75,12 +92,14 @@ def test_workspace_matches_split(mx):
                 Kp = _kpad(K)
                 S = mx.splitk_segments(M, N, Kp)
                 rp = mx.repacks_a(M, N, Kp)
-                ws = mx.workspace_size(M, N, Kp)
+                ws = mx.preferred_workspace_size(M, N, Kp)
                 # split partials first, then the repacked A at the next 256-byte boundary
                 split = S * M * N * 4 if S > 1 else 0
                 want = (split + 255) // 256 * 256 + (-(-M // 32) * 32 * Kp // 4 * 3 if rp else 0)
-                assert ws == want, (M, N, K, S, rp, ws)
-                assert mx.plan_workspace_size(M, N, Kp, S, rp) == want
+                assert ws == (want if (S > 1 or rp) else 0), (M, N, K, S, rp, ws)
+                assert mx.plan_workspace_size(M, N, Kp, S, rp) == (want if (S > 1 or rp) else 0)
+                # gemm_workspace_size keeps the reference's meaning: the partials only
+                assert mx.workspace_size(M, N, Kp) == split, (M, N, K)
                 if S > 1:
                     assert Kp // 192 >= S and S <= 16  # every segment holds >= 1 K-tile
 
@@ -97,6 +116,7 @@ def test_router_degenerate_shapes_do_not_trap(mx):
                 assert M % t[0] == 0 and N % t[1] == 0
         else:
             assert mx.workspace_size(M, N, Kp) == 0
+            assert mx.preferred_workspace_size(M, N, Kp) == 0
 
 
 def test_router_benchmark_shapes(mx):
@@ -195,7 +215,8 @@ def test_router_skinny_m(mx):
                 assert 1 <= S <= min(16, Kp // 192)
                 rp = mx.repacks_a(M, N, Kp)
                 want = ((S * M * N * 4 if S > 1 else 0) + 255) // 256 * 256 + (M * Kp // 4 * 3 if rp else 0)
-                assert mx.workspace_size(M, N, Kp) == (want if (S > 1 or rp) else 0)
+                assert mx.preferred_workspace_size(M, N, Kp) == (want if (S > 1 or rp) else 0)
+                assert mx.workspace_size(M, N, Kp) == (S * M * N * 4 if S > 1 else 0)
 
 
 def test_router_ragged_shapes(mx):
@@ -220,7 +241,8 @@ def test_router_ragged_shapes(mx):
                 assert (tile, S2, rp2) == (t, S, bool(rp)), (M, N, K)
                 want = (((S * M * N * 4 if S > 1 else 0) + 255) // 256 * 256
                         + (-(-M // 32) * 32 * Kp // 4 * 3 if rp else 0))
-                assert mx.workspace_size(M, N, Kp) == (want if (S > 1 or rp) else 0)
+                assert mx.preferred_workspace_size(M, N, Kp) == (want if (S > 1 or rp) else 0)
+                assert mx.workspace_size(M, N, Kp) == (S * M * N * 4 if S > 1 else 0)
 
 
 def test_plan_cache_is_per_thread_and_transparent(mx):

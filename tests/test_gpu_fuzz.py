@@ -50,9 +50,12 @@ def _shapes(n=24, seed=20261201):
 
 
 def _run(dp, out_type, with_ws):
+    """with_ws: "preferred" (the plan's whole workspace), "split" (gemm_workspace_size's bytes,
+    the split-K partials only: A read row-major) or False (no workspace: never split)."""
     p = dp.p
     n = p.M * p.N * mx.OUT_BYTES[out_type]
-    ws_bytes = mx.workspace_size(p.M, p.N, p.Kp) if with_ws else 0
+    size = mx.preferred_workspace_size if with_ws == "preferred" else mx.workspace_size
+    ws_bytes = size(p.M, p.N, p.Kp) if with_ws else 0
     D = torch.full((n + GUARD,), 0x5A, dtype=torch.uint8, device="cuda")
     ws = torch.full((max(ws_bytes, 4) + GUARD,), 0x3C, dtype=torch.uint8, device="cuda")
     a, b, sa, sb = dp.ptrs()
@@ -75,6 +78,6 @@ def test_routed_random_shape(M, N, K, out_type):
     rows = None if M <= 48 else np.unique(np.r_[0:4, M - 4:M,
                                                  np.linspace(0, M - 1, 40).astype(int)])
     R, ab = oracle.problem_f64(p, rows=rows)
-    for with_ws in (True, False):
+    for with_ws in ("preferred", "split", False):
         D = _run(dp, out_type, with_ws)
         checks.check(D if rows is None else D[rows], R, ab, out_type)

@@ -324,7 +324,8 @@ def test_stream_entry_point(g, orc):
                                             (4096, 4096, 768, 1), (2048, 1024, 12288, 0)])
 def test_reference_library_same_inputs(g, orc, ref_lib, M, N, K, out_type):
     """Our D and the reference library's D on the same operands (each with the scale grouping
-    of its own router) both meet the oracle bar, and agree with each other."""
+    of its own router) both meet the oracle bar; when both split K the same way (same segment
+    count, hence the same MFMA sequence and reduction order) they are bit-identical."""
     import ctypes as C
     import torch
     p = mx.make_problem(M, N, K, seed=M * 3 + N * 7 + K)
@@ -346,7 +347,12 @@ def test_reference_library_same_inputs(g, orc, ref_lib, M, N, K, out_type):
     checks.check(ours[rows], R, ab, out_type)
     checks.check(theirs[rows], R, ab, out_type)
     same = float((ours.view(np.uint32) == theirs.view(np.uint32)).mean())
-    g.say(f"    bit-identical to the reference library: {100 * same:.2f}% of elements")
+    s_ours = mx.splitk_segments(M, N, p.Kp)
+    s_ref = wsb // (M * N * 4) if wsb else 1
+    g.say(f"    segments ours {s_ours} reference {s_ref}; bit-identical to the reference library: "
+          f"{100 * same:.2f}% of elements")
+    if s_ours == s_ref:
+        assert same == 1.0
 
 
 # ---- FP16/BF16 epilogue: exactly the rounded FP32 result ------------------------------------

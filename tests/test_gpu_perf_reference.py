@@ -4,9 +4,9 @@ from the reference's own sources) on the five benchmark workloads, same device o
 Each side runs its own router (choose_tile / workspace) on identical packed operands; outputs are
 spot-checked against the FP64 oracle so a fast wrong result cannot pass. Timing follows the
 reference's methodology (warm-up, then the best mean of repetitions of 20 back-to-back launches).
-The printed table is the comparison; the assertion is only a regression guard (>= 0.8x), the goal
-(>= 1.0x on every workload) is tracked in the benchmark report. Set MXFP6_PERF_LOG=<file> to append
-one JSON line per workload.
+On the five benchmark workloads the goal is >= 1.0x; the assertion allows 3% for run-to-run noise
+(>= 0.97x). The off-benchmark shapes include known short-K losses (0.91-0.98x measured), so they are
+guarded at >= 0.85x only. Set MXFP6_PERF_LOG=<file> to append one JSON line per workload.
 """
 import ctypes as C
 import json
@@ -83,7 +83,7 @@ def test_throughput_vs_reference_library(orc, ref_lib, name):
     t = mx.choose_tile(M, N, p.Kp)
     bsh, sa, sb = p.layouts(t)
     dB, dsa, dsb = (torch.from_numpy(x).cuda() for x in (bsh, sa, sb))
-    wsb = mx.workspace_size(M, N, p.Kp)
+    wsb = mx.preferred_workspace_size(M, N, p.Kp)
     ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device="cuda")
 
     def ours():
@@ -131,4 +131,5 @@ def test_throughput_vs_reference_library(orc, ref_lib, name):
                                 "ours_tflops": tf_o, "ref_us": ms_ref * 1e3, "ref_tflops": tf_r,
                                 "ratio": tf_o / tf_r, "ours_tile": list(t),
                                 "ref_tile": list(tr)}) + "\n")
-    assert tf_o >= 0.8 * tf_r
+    floor = 0.97 if name[0] == "c" else 0.85
+    assert tf_o >= floor * tf_r, f"{name}: {tf_o / tf_r:.3f}x the reference (floor {floor})"

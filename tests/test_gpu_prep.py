@@ -184,7 +184,7 @@ def test_gemm_on_device_prepared_operands(mx, M, N, K, out_type):
     dsb = torch.empty(sb_t.size, dtype=torch.uint8, device=DEV)
     assert mx.prepare_a_dev(dA.data_ptr(), M, K, tile[2], da.data_ptr(), rb, dsa.data_ptr()) == 0
     assert mx.prepare_b_dev(dB.data_ptr(), K, N, tile[3], db.data_ptr(), dsb.data_ptr()) == 0
-    ws_bytes = mx.workspace_size(M, N, Kp)
+    ws_bytes = mx.preferred_workspace_size(M, N, Kp)
     ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=DEV)
     ob = mx.OUT_BYTES[out_type]
 

@@ -49,7 +49,7 @@ def _gemm(dp, out_type, explicit=None, splits=1, a_layout=0, a_dev=None):
     p = dp.p
     n = p.M * p.N * mx.OUT_BYTES[out_type]
     if explicit is None:
-        ws_bytes = mx.workspace_size(p.M, p.N, p.Kp)
+        ws_bytes = mx.preferred_workspace_size(p.M, p.N, p.Kp)
     else:
         ws_bytes = mx.plan_workspace_size(p.M, p.N, p.Kp, splits, a_layout == 1)
     D = _buf(n, 0x5A)
@@ -261,7 +261,7 @@ def test_gemm_on_device_prepared_ragged(M, N, K, out_type):
     dsb = torch.empty(mx.tiled_scale_bytes(N, K, t[3]), dtype=torch.uint8, device="cuda")
     assert mx.prepare_a_dev(_dev(A).data_ptr(), M, K, t[2], da.data_ptr(), rb, dsa.data_ptr()) == 0
     assert mx.prepare_b_dev(_dev(B).data_ptr(), K, N, t[3], db.data_ptr(), dsb.data_ptr()) == 0
-    ws_bytes = mx.workspace_size(M, N, Kp)
+    ws_bytes = mx.preferred_workspace_size(M, N, Kp)
     ws = _buf(max(ws_bytes, 4), 0x3C)
     n = M * N * mx.OUT_BYTES[out_type]
     D = _buf(n, 0x5A)

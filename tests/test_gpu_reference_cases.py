@@ -30,7 +30,7 @@ def _run(dp, out_type, how, tile=None, ws_bytes=None):
     a, b, sa, sb = dp.ptrs()
     say(f"  {how} {p.M}x{p.N}x{p.K} (Kp {p.Kp}) tile {tile or dp.tile} A_row_bytes {p.a_row_bytes}")
     if how == "routed":
-        wsb = mx.workspace_size(p.M, p.N, p.Kp) if ws_bytes is None else ws_bytes
+        wsb = mx.preferred_workspace_size(p.M, p.N, p.Kp) if ws_bytes is None else ws_bytes
         ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device="cuda")
         rc = mx.gemm(out_type, p.M, p.N, p.Kp, a, b, sa, sb, D.data_ptr(), p.a_row_bytes,
                      ws.data_ptr() if wsb else 0, wsb)
