@@ -15,9 +15,11 @@ Prints one JSON line per workload (only the default one unless --all). The headl
 the mean over exactly K timed steps after W warm-up steps (no extra warm-up: an idle MI355X sits
 in deep sleep near 160 MHz, so a short warm-up leaves part of the clock ramp inside the timed
 loop; `sclk_mhz` reports the clock the loop ran at). Besides the contract fields it reports:
-  sclk_mhz      the graphics clock sampled (amdsmi GPU metrics, mean over the XCDs) while the timed
-                loop ran, and frac_at_sclk = value / (4,194,304 flop/clk x sclk), the fraction of
-                the dense MXFP6 MFMA peak at the clock the chip actually ran;
+  sclk_mhz      the mean graphics clock over the timed loop (each XCD's shader cycle counter
+                against the 100 MHz reference counter, read by the library's clock sample just
+                before and just after the loop, outside its events; mean over the XCDs), and
+                frac_at_sclk = value / (4,194,304 flop/clk x sclk), the fraction of the dense
+                MXFP6 MFMA peak at the clock the chip actually ran;
   roofline      the dominant kernel (the tile kernel) against the dense MXFP6 MFMA peak: its
                 algorithmic flops per launch / its average launch duration, timed live with HIP
                 events on the launch stream in a second loop of K steps that issues the step's
@@ -41,7 +43,6 @@ import json
 import os
 import re
 import sys
-import threading
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -106,66 +107,41 @@ def profiled_traffic(workload, kernel):
     return None
 
 
-class ClockSampler:
-    """Samples the graphics clock of the GPU behind cuda:0 (amdsmi GPU metrics: the current
-    clock of each XCD, averaged) in a background thread between start() and stop(). stop()
-    returns the mean over the samples in MHz, or None when amdsmi is unavailable."""
+class ClockProbe:
+    """The graphics clock over a region of GPU work, from two clock samples of the library
+    (mxfp6_clock_sample_async: each of 256 one-wave workgroups reads its CU's shader cycle
+    counter and the 100 MHz reference counter) launched on the same stream just before and just
+    after the region, outside its timing events. stop() returns the mean over the XCDs (MHz)."""
+
+    NWG = 256
 
     def __init__(self):
-        self.handle, self.error = None, None
-        try:
-            import amdsmi
-            import torch
-            self.amdsmi = amdsmi
-            amdsmi.amdsmi_init()
-            handles = amdsmi.amdsmi_get_processor_handles()
-            prop = torch.cuda.get_device_properties(0)
-            want = (getattr(prop, "pci_domain_id", 0), getattr(prop, "pci_bus_id", -1),
-                    getattr(prop, "pci_device_id", 0))
-            for h in handles:
-                bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)  # "dddd:bb:dd.f"
-                dom, bus, rest = bdf.split(":")
-                if (int(dom, 16), int(bus, 16), int(rest.split(".")[0], 16)) == want:
-                    self.handle = h
-            if self.handle is None and len(handles) == 1:
-                self.handle = handles[0]
-            if self.handle is None:
-                self.error = f"no amdsmi device matches PCI {want}"
-        except Exception as e:  # no amdsmi, no permission, no device
-            self.error = f"{type(e).__name__}: {e}"
-        self.samples, self._stop, self._th = [], threading.Event(), None
+        import torch
+        self.bufs = [torch.zeros(self.NWG * 4, dtype=torch.int64, device="cuda:0")
+                     for _ in range(2)]
+        self.per_xcd = None
 
-    def read(self):
-        m = self.amdsmi.amdsmi_get_gpu_metrics_info(self.handle)
-        vals = m.get("current_gfxclks")
-        vals = vals if isinstance(vals, (list, tuple)) else [m.get("current_gfxclk")]
-        vals = [v for v in vals if isinstance(v, int) and 0 < v < 0xFFFF]
-        return sum(vals) / len(vals) if vals else None
+    def _sample(self, i, stream):
+        if mx.clock_sample(self.bufs[i].data_ptr(), self.NWG, stream.cuda_stream) != 0:
+            raise RuntimeError("clock sample failed")
 
-    def _run(self):
-        while not self._stop.is_set():
-            try:
-                v = self.read()
-            except Exception as e:
-                self.error = f"{type(e).__name__}: {e}"
-                return
-            if v is not None:
-                self.samples.append(v)
-            time.sleep(0.0002)
+    def start(self, stream):
+        self._sample(0, stream)
 
-    def start(self):
-        self.samples.clear()
-        self._stop.clear()
-        if self.handle is not None:
-            self._th = threading.Thread(target=self._run, daemon=True)
-            self._th.start()
+    def stop(self, stream):
+        import torch
+        self._sample(1, stream)
+        torch.cuda.synchronize()
+        a, b = (t.cpu().numpy().reshape(self.NWG, 4) for t in self.bufs)
+        self.per_xcd = mx.clock_between(a, b)
+        if not self.per_xcd:
+            return None
+        return round(sum(self.per_xcd.values()) / len(self.per_xcd), 1)
 
-    def stop(self):
-        self._stop.set()
-        if self._th is not None:
-            self._th.join()
-            self._th = None
-        return round(sum(self.samples) / len(self.samples), 1) if self.samples else None
+
+def frac_at(tflops, mhz):
+    """Fraction of the dense MXFP6 MFMA peak at the given graphics clock."""
+    return round(tflops * 1e12 / (FLOP_PER_CLK * mhz * 1e6), 4) if mhz else None
 
 
 def cpu_baseline(p, target_cpu_s=12.0):
@@ -226,21 +202,25 @@ def reference_library():
 def best_of(fn, stream, reps=4, n=20, warm=8):
     """The reference's timing method (tests/test_gemm.cpp:33-55): `warm` calls, then `reps`
     repetitions of `n` back-to-back calls between two events; returns (best mean, median mean)
-    in milliseconds."""
+    in milliseconds and the graphics clock (MHz) over the best repetition (clock samples taken
+    right outside its events, so no host-side gap between repetitions dilutes it)."""
     import torch
     for _ in range(warm):
         fn()
     torch.cuda.synchronize()
-    means = []
+    means, clocks = [], []
+    clock = ClockProbe()
     for _ in range(reps):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        clock.start(stream)
         a.record(stream)
         for _ in range(n):
             fn()
         b.record(stream)
-        torch.cuda.synchronize()
+        clocks.append(clock.stop(stream))
         means.append(a.elapsed_time(b) / n)
-    return min(means), float(np.median(means))
+    best = int(np.argmin(means))
+    return means[best], float(np.median(means)), clocks[best]
 
 
 class Workload:
@@ -310,15 +290,16 @@ class Workload:
 
 def compare(w, stream):
     """This library and the reference library on the same operands, by the reference's timing
-    method, one after the other."""
+    method, one after the other, with the clock each ran at."""
     import torch
     null = torch.cuda.default_stream()
-    ms_o, med_o = best_of(lambda: w.ours(stream), stream)
+    ms_o, med_o, sclk_o = best_of(lambda: w.ours(stream), stream)
     out = {"workload": workload_name(w.M, w.N, w.K, w.ot), "tile": list(w.tile),
            "splitk": w.S, "a_repacked": w.repack, "us": round(ms_o * 1e3, 2),
            "tflops": round(w.flops / ms_o / 1e9, 1),
            "frac": round(w.flops / ms_o / 1e9 / PEAK_TFLOPS, 4),
-           "median_us": round(med_o * 1e3, 2)}
+           "median_us": round(med_o * 1e3, 2), "sclk_mhz": sclk_o,
+           "frac_at_sclk": frac_at(w.flops / ms_o / 1e9, sclk_o)}
     if w.S > 1:
         # algorithmic bytes, and with the split-K partials written and read back
         ab = alg_bytes(w.M, w.N, w.K, w.ot)
@@ -326,18 +307,20 @@ def compare(w, stream):
         out["hbm_gbs_alg_with_partials"] = round(
             (ab + 2 * 4 * w.S * w.M * w.N) / ms_o / 1e6, 1)
     if w.ref is not None:
-        ms_r, med_r = best_of(lambda: w.theirs(null), null)
+        ms_r, med_r, sclk_r = best_of(lambda: w.theirs(null), null)
         tf_r = w.flops / ms_r / 1e9
         out.update({"ref_tile": list(w.ref_tile), "ref_us": round(ms_r * 1e3, 2),
                     "ref_tflops": round(tf_r, 1), "ref_median_us": round(med_r * 1e3, 2),
+                    "ref_sclk_mhz": sclk_r,
                     "ratio": round(ms_r / ms_o, 3), "max_rel_diff_vs_ref": w.agree()})
-    log(f"[bench] {w.name}: ours {out['us']} us ({out['tflops']} TF)" +
-        (f" | reference {out['ref_us']} us ({out['ref_tflops']} TF) | ratio {out['ratio']}"
+    log(f"[bench] {w.name}: ours {out['us']} us ({out['tflops']} TF, {sclk_o} MHz)" +
+        (f" | reference {out['ref_us']} us ({out['ref_tflops']} TF, {out['ref_sclk_mhz']} MHz)"
+         f" | ratio {out['ratio']}"
          if w.ref is not None else ""))
     return out
 
 
-def headline(name, steps, warmup, ref, clock):
+def headline(name, steps, warmup, ref):
     """The contract measurement of one workload: `warmup` untimed steps, then exactly `steps`
     steps between two synchronisations; then the dominant kernel timed alone."""
     import torch
@@ -348,7 +331,8 @@ def headline(name, steps, warmup, ref, clock):
         w.ours(stream)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    clock.start()
+    clock = ClockProbe()
+    clock.start(stream)
     w0 = time.perf_counter()
     ev0.record(stream)
     for _ in range(steps):
@@ -356,7 +340,8 @@ def headline(name, steps, warmup, ref, clock):
     ev1.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - w0) * 1e3
-    sclk = clock.stop()
+    sclk = clock.stop(stream)
+    sclk_xcd = clock.per_xcd
     ms = ev0.elapsed_time(ev1) / steps
     tflops = w.flops / (ms * 1e-3) / 1e12
 
@@ -386,11 +371,11 @@ def headline(name, steps, warmup, ref, clock):
         for _ in range(max(2, warmup // 2)):
             split_step(-1)
         torch.cuda.synchronize()
-        clock.start()
+        clock.start(stream)
         for i in range(steps):
             split_step(i)
         torch.cuda.synchronize()
-        k_sclk = clock.stop()
+        k_sclk = clock.stop(stream)
         k_ms = sum(a.elapsed_time(b) for a, b in evs) / steps
         kernel_scope = "tile kernel alone (repack of A timed outside)"
     else:
@@ -421,27 +406,24 @@ def headline(name, steps, warmup, ref, clock):
                    "workspace_bytes": w.ws_bytes, "parallelism": "single GPU"},
         "pct_of_peak": round(100.0 * tflops / PEAK_TFLOPS, 2),
         "sclk_mhz": sclk,
-        "frac_at_sclk": round(tflops * 1e12 / (FLOP_PER_CLK * sclk * 1e6), 4) if sclk else None,
+        "sclk_mhz_per_xcd": [round(v, 1) for v in sclk_xcd.values()] if sclk_xcd else None,
+        "frac_at_sclk": frac_at(tflops, sclk),
         "hbm_gbs_alg": round(alg_bytes(M, N, K, w.ot) / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(k_tflops / PEAK_TFLOPS, 4),
                      "traffic": profiled_traffic(workload, kernel_name), "kernel": kernel_name,
                      "scope": kernel_scope, "kernel_ms": round(k_ms, 6), "sclk_mhz": k_sclk,
-                     "frac_at_sclk": (round(k_tflops * 1e12 / (FLOP_PER_CLK * k_sclk * 1e6), 4)
-                                      if k_sclk else None)},
+                     "frac_at_sclk": frac_at(k_tflops, k_sclk)},
     }
-    if clock.error:
-        out["sclk_note"] = clock.error
     return w, out
 
 
 def run(names, steps, warmup, with_cpu, with_ref, per_config):
     import torch
     ref = reference_library() if with_ref else None
-    clock = ClockSampler()
     lines = []
     for n in names:
-        w, out = headline(n, steps, warmup, ref, clock)
+        w, out = headline(n, steps, warmup, ref)
         if ref is not None:
             c = compare(w, torch.cuda.current_stream())
             out["vs_baseline"] = round(out["value"] / c["ref_tflops"], 3)

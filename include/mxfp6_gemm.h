@@ -124,6 +124,16 @@ int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, int npw, cons
                       const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
                       int A_row_bytes, int splits, void* ws, size_t ws_bytes, void* stream);
 
+/* Clock sample, a measurement aid: nwg one-wave workgroups (1..65536) each record, at
+ * d_out[4*i .. 4*i+3], the shader clock counter (s_memtime, which counts at the current graphics
+ * clock of the XCD the workgroup ran on), the 100 MHz reference counter (s_memrealtime), the XCD
+ * id and the hardware id (shader engine, shader array and CU in bits 8..15). Two samples around
+ * a region of GPU work give each XCD's mean graphics clock over it: the cycle difference over the
+ * reference difference times 100 MHz, pairing workgroups that ran on the same CU (each CU's
+ * cycle counter has its own fixed offset). Asynchronous on `stream`. No counterpart in the
+ * reference (its benchmarks read the clock from the SMI tools). */
+int mxfp6_clock_sample_async(uint64_t* d_out, int nwg, void* stream);
+
 /* ---- element formats (reference include/mxfp6/types.hpp) ---------------------------------- */
 
 float mxfp6_fp6_e2m3_to_float(uint8_t code);    /* types.hpp:13-24 */

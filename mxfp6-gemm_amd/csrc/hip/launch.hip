@@ -93,6 +93,30 @@ extern "C" int mxfp6_hip_repack(const void* src, int row_bytes, int rows, int Kp
                                         static_cast<hipStream_t>(stream)));
 }
 
+// Clock sample: lane 0 of each one-wave workgroup stores the shader clock counter (s_memtime,
+// counting at the XCD's current graphics clock), the 100 MHz reference counter (s_memrealtime),
+// the XCD id and the hardware id (shader engine, shader array and CU in bits 8..15) of where it
+// ran. The counters are read once per workgroup; the stores are ordinary vector stores.
+__global__ void clock_sample_kernel(uint64_t* out) {
+    const uint64_t cyc = __builtin_amdgcn_s_memtime();
+    const uint64_t ref = __builtin_amdgcn_s_memrealtime();
+    uint32_t xcc, hw;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    if (threadIdx.x == 0) {
+        uint64_t* o = out + (size_t)blockIdx.x * 4;
+        o[0] = cyc;
+        o[1] = ref;
+        o[2] = xcc;
+        o[3] = hw;
+    }
+}
+
+extern "C" int mxfp6_hip_clock_sample(uint64_t* out, int nwg, void* stream) {
+    return status_of(launch_kernel(clock_sample_kernel, dim3((unsigned)nwg), dim3(64),
+                                   static_cast<hipStream_t>(stream), out));
+}
+
 extern "C" int mxfp6_hip_device_cus(void) {
     // per device: 0 = not read yet, -1 = the query failed
     static std::atomic<int> cus[64];

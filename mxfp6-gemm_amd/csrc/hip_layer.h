@@ -49,6 +49,9 @@ int mxfp6_hip_launch(const mxfp6_launch_desc* d);
  * into the preshuffled operand layout at dst (rows * packed(Kp) bytes). 0 ok, 2 launch error. */
 int mxfp6_hip_repack(const void* src, int row_bytes, int rows, int Kp, void* dst, void* stream);
 
+/* Clock sample (see mxfp6_clock_sample_async in include/mxfp6_gemm.h). 0 ok, 2 launch error. */
+int mxfp6_hip_clock_sample(uint64_t* out, int nwg, void* stream);
+
 /* Compute units of the current HIP device (hipDeviceAttributeMultiprocessorCount, read once per
  * device), or 0 when the runtime reports no device. */
 int mxfp6_hip_device_cus(void);

@@ -445,6 +445,12 @@ extern "C" size_t mxfp6_plan_workspace_size(int M, int N, int Kp, int splits, in
     return plan::plan_bytes(M, N, Kp, splits, a_repack != 0);
 }
 
+extern "C" int mxfp6_clock_sample_async(uint64_t* d_out, int nwg, void* stream) {
+    if (!d_out) return MXFP6_ERR_NULL;
+    if (nwg < 1 || nwg > 65536) return MXFP6_ERR_ARG;
+    return mxfp6_hip_clock_sample(d_out, nwg, stream) == 0 ? MXFP6_OK : MXFP6_ERR_HIP;
+}
+
 extern "C" int mxfp6_preshuffle_rows_async(const void* src, int row_bytes, int rows, int Kp,
                                            void* dst, void* stream) {
     if (!src || !dst) return MXFP6_ERR_NULL;

@@ -40,6 +40,7 @@ SIGNATURES = {
     "mxfp6_choose_tile": (C.c_int, [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int)]),
     "mxfp6_gemm_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     "mxfp6_gemm_preferred_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
+    "mxfp6_clock_sample_async": (C.c_int, [_vp, C.c_int, _vp]),
     "mxfp6_splitk_segments": (C.c_int, [C.c_int, C.c_int, C.c_int]),
     "mxfp6_gemm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
                              C.c_int, C.c_int, _vp, C.c_size_t]),
@@ -189,6 +190,32 @@ def repacks_a(M, N, Kp):
 
 def plan_workspace_size(M, N, Kp, splits, a_repack):
     return lib().mxfp6_plan_workspace_size(M, N, Kp, splits, int(a_repack))
+
+
+def clock_sample(d_out, nwg, stream=None):
+    """mxfp6_clock_sample_async: nwg x 4 uint64 records (cycles, 100 MHz reference, XCD, HW id)."""
+    return lib().mxfp6_clock_sample_async(d_out, nwg, stream)
+
+
+def clock_between(a, b):
+    """Mean graphics clock (MHz) per XCD between two clock samples a and b (uint64 arrays of
+    shape [nwg, 4] from clock_sample): for each CU seen in both samples, its cycle difference over
+    its reference difference times 100 MHz, averaged over the XCD's CUs. Returns {xcd: MHz}."""
+    import numpy as np
+
+    def per_cu(s):
+        d = {}
+        for cyc, ref, xcc, hw in np.asarray(s, dtype=np.uint64).tolist():
+            d[(int(xcc), (int(hw) >> 8) & 0xFF)] = (int(cyc), int(ref))
+        return d
+
+    da, db = per_cu(a), per_cu(b)
+    acc = {}
+    for key in da.keys() & db.keys():
+        (c0, r0), (c1, r1) = da[key], db[key]
+        if r1 > r0:
+            acc.setdefault(key[0], []).append((c1 - c0) / (r1 - r0) * 100.0)
+    return {x: sum(v) / len(v) for x, v in sorted(acc.items())}
 
 
 def preshuffle_rows(src, row_bytes, rows, Kp, dst, stream=None):
