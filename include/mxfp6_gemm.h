@@ -30,7 +30,9 @@ typedef enum mxfp6_status {
     MXFP6_ERR_OUT_TYPE = 3,  /* out_type not in {0, 1, 2} */
     MXFP6_ERR_TILE = 4,      /* tile not implemented, or it does not divide the shape */
     MXFP6_ERR_ARG = 5,       /* other invalid argument */
-    MXFP6_ERR_HIP = 6        /* the HIP runtime reported an error at launch */
+    MXFP6_ERR_HIP = 6,       /* the HIP runtime reported an error at launch */
+    MXFP6_ERR_SCRATCH = 7    /* mxfp6_gemm_noalloc_async: the plan's split-K partials exceed
+                                MXFP6_NOALLOC_SCRATCH_BYTES */
 } mxfp6_status;
 
 /* ---- GEMM (reference include/mxfp6/gemm.hpp, src/gemm.cpp) -------------------------------- */
@@ -79,6 +81,24 @@ int mxfp6_gemm(int out_type, int M, int N, int Kp, const void* dA, const void* d
 int mxfp6_gemm_async(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
                      const uint8_t* dsA, const uint8_t* dsB, void* dD, int A_row_bytes,
                      int B_row_bytes, void* ws, size_t ws_bytes, void* stream);
+
+/* Size of the device scratch of mxfp6_gemm_noalloc_async: 128 MiB per GPU. */
+#define MXFP6_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+
+/* mxfp6_gemm_async without a workspace argument, and without any device allocation or free (no
+ * hipMalloc, hipFree or allocating library call): the split-K partials, and the repacked A when it
+ * fits beside them, go to a device array of MXFP6_NOALLOC_SCRATCH_BYTES that the library holds
+ * per GPU from the first such call on that GPU until the process ends. Same plan and the same
+ * output bits as mxfp6_gemm_async with mxfp6_gemm_preferred_workspace_size bytes, except that a
+ * repacked A that does not fit is read row-major instead (same bits). A shape whose split-K
+ * partials (mxfp6_gemm_workspace_size) exceed the scratch is rejected with MXFP6_ERR_SCRATCH,
+ * before any device work. Every call on a GPU shares that GPU's scratch: calls that overlap on one
+ * GPU (concurrent streams or host threads) race; serialise them. No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). */
+int mxfp6_gemm_noalloc_async(int out_type, int M, int N, int Kp, const void* dA,
+                             const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
+                             int A_row_bytes, int B_row_bytes, void* stream);
 
 /* gemm_force_tile: run the tile {MT, NT, MPW, NPW} given by the caller instead of the router's
  * choice, unsplit. Test-only in the reference (src/gemm.cpp:85-107, not in its header); the

@@ -49,6 +49,11 @@ int mxfp6_hip_launch(const mxfp6_launch_desc* d);
  * into the preshuffled operand layout at dst (rows * packed(Kp) bytes). 0 ok, 2 launch error. */
 int mxfp6_hip_repack(const void* src, int row_bytes, int rows, int Kp, void* dst, void* stream);
 
+/* The no-allocation scratch of the current device (csrc/hip/scratch.hip): its device address,
+ * read with hipGetSymbolAddress on the first call per device, and its size in *bytes; NULL when
+ * the runtime cannot provide it. */
+void* mxfp6_hip_scratch(size_t* bytes);
+
 /* Clock sample (see mxfp6_clock_sample_async in include/mxfp6_gemm.h). 0 ok, 2 launch error. */
 int mxfp6_hip_clock_sample(uint64_t* out, int nwg, void* stream);
 

@@ -215,6 +215,7 @@ const char* status_text(int st) {
         case MXFP6_ERR_TILE: return "tile not implemented or does not divide the shape";
         case MXFP6_ERR_ARG: return "invalid argument";
         case MXFP6_ERR_HIP: return "HIP launch error";
+        case MXFP6_ERR_SCRATCH: return "split-K partials exceed the no-allocation scratch";
         default: return "unknown status";
     }
 }
@@ -380,6 +381,22 @@ extern "C" int mxfp6_gemm_async(int out_type, int M, int N, int Kp, const void* 
     (void)B_row_bytes;
     return plan::gemm_checked(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws,
                               ws_bytes, stream);
+}
+
+extern "C" int mxfp6_gemm_noalloc_async(int out_type, int M, int N, int Kp, const void* dA,
+                                        const void* dBsh, const uint8_t* dsA, const uint8_t* dsB,
+                                        void* dD, int A_row_bytes, int B_row_bytes, void* stream) {
+    (void)B_row_bytes;
+    const int st = plan::check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
+    if (st != MXFP6_OK) return st;
+    // the plan's split-K partials must fit; the repacked A is used only when it fits beside them
+    // (gemm_checked drops it otherwise)
+    if (plan::workspace_bytes(M, N, Kp) > MXFP6_NOALLOC_SCRATCH_BYTES) return MXFP6_ERR_SCRATCH;
+    size_t cap = 0;
+    void* scratch = mxfp6_hip_scratch(&cap);
+    if (scratch == nullptr) return MXFP6_ERR_HIP;
+    return plan::gemm_checked(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, scratch,
+                              cap, stream);
 }
 
 extern "C" int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4],

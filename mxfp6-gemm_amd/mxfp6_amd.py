@@ -30,7 +30,8 @@ DIST_NORMAL, DIST_UNIFORM, DIST_STUDENT_T3 = 0, 1, 2
 K_TILE = 192
 
 STATUS = {0: "OK", 1: "ERR_NULL", 2: "ERR_SHAPE", 3: "ERR_OUT_TYPE", 4: "ERR_TILE",
-          5: "ERR_ARG", 6: "ERR_HIP"}
+          5: "ERR_ARG", 6: "ERR_HIP", 7: "ERR_SCRATCH"}
+NOALLOC_SCRATCH_BYTES = 128 << 20  # MXFP6_NOALLOC_SCRATCH_BYTES
 
 # Every C symbol declared in include/mxfp6_gemm.h: (restype, argtypes).
 _u8p = C.POINTER(C.c_uint8)
@@ -46,6 +47,8 @@ SIGNATURES = {
                              C.c_int, C.c_int, _vp, C.c_size_t]),
     "mxfp6_gemm_async": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                    C.c_int, C.c_int, _vp, C.c_size_t, _vp]),
+    "mxfp6_gemm_noalloc_async": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp,
+                                           _vp, C.c_int, C.c_int, _vp]),
     "mxfp6_gemm_force_tile": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
                                         _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp]),
     "mxfp6_gemm_explicit": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
@@ -159,6 +162,14 @@ def gemm(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws=0, ws_bytes
     """mxfp6_gemm_async; returns the status (0 on success)."""
     return lib().mxfp6_gemm_async(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes,
                                   B_row_bytes, ws or None, ws_bytes, stream)
+
+
+def gemm_noalloc(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, stream=None,
+                 B_row_bytes=0) -> int:
+    """mxfp6_gemm_noalloc_async: no workspace argument, no device allocation (the library's
+    per-GPU scratch); returns the status."""
+    return lib().mxfp6_gemm_noalloc_async(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes,
+                                          B_row_bytes, stream)
 
 
 def gemm_null_stream(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws=0, ws_bytes=0,

@@ -111,3 +111,16 @@ def test_tile_scale_rejects_partial_groups(mx):
     ptr = buf.ctypes.data_as(C.c_void_p)
     assert mx.lib().mxfp6_tile_scale(ptr, 416, 192, 3, 3, ptr) == 5
     assert mx.lib().mxfp6_tile_scale(ptr, 384, 192, 3, 3, ptr) == 0
+
+
+def test_noalloc_rejects_before_device_work(mx):
+    """mxfp6_gemm_noalloc_async checks its arguments, then that the plan's split-K partials fit
+    its scratch, before touching the device: a shape whose partials exceed the 128 MiB scratch is
+    rejected with MXFP6_ERR_SCRATCH."""
+    p = 0x1000  # never dereferenced
+    Kp = mx.kpad(105728)
+    rb = Kp // 4 * 3
+    assert mx.gemm_noalloc(0, 8192, 13312, Kp, 0, p, p, p, p, rb) == 1     # null A
+    assert mx.gemm_noalloc(5, 8192, 13312, Kp, p, p, p, p, p, rb) == 3     # bad out type
+    assert mx.workspace_size(8192, 13312, Kp) > mx.NOALLOC_SCRATCH_BYTES
+    assert mx.gemm_noalloc(1, 8192, 13312, Kp, p, p, p, p, p, rb) == 7     # partials too large
