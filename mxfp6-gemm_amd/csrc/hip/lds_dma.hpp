@@ -32,12 +32,41 @@ __device__ __forceinline__ void dma16_flat(uint32_t lds, const void* gaddr) {
                  : "memory");
 }
 
+// 4 bytes per lane global -> LDS: lane l's dword goes to LDS m0 + 4*l.
+__device__ __forceinline__ void dma4_flat(uint32_t lds, const void* gaddr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+                 :
+                 : "s"(lds), "v"(gaddr)
+                 : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the LDS fence of __syncthreads (which waits for every outstanding LDS
+// read of the wave). The memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 typedef __attribute__((address_space(3))) const char* lds_cptr;
 
 // Returns x unchanged, hidden from the optimizer (forces a VGPR, defeats offset folding).
 __device__ __forceinline__ uint32_t opaque_v(uint32_t x) {
     asm volatile("" : "+v"(x));
     return x;
+}
+
+typedef __attribute__((address_space(1))) const uint8_t* gbl_cptr;
+
+// Returns p as a global-memory pointer with its provenance hidden from the optimizer: loads through
+// it are no longer known to read memory nothing writes, so they keep their order relative to asm
+// statements with a memory clobber (and are not merged across them).
+__device__ __forceinline__ gbl_cptr opaque_gptr(const uint8_t* p) {
+    gbl_cptr g = (gbl_cptr)p;
+    asm volatile("" : "+s"(g));
+    return g;
 }
 
 __device__ __forceinline__ void wait_vmcnt0() {

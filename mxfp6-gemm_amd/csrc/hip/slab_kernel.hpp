@@ -45,29 +45,13 @@
 
 #include "../hip_layer.h"
 #include "device_common.hpp"
+#include "epilogue.hpp"
 #include "lds_dma.hpp"
 #include "repack_kernel.hpp"
 #include "slab_run.hpp"
+#include "wide_kernel.hpp"
 
 namespace mxfp6_dev {
-
-// 4 bytes per lane global -> LDS: lane l's dword goes to LDS m0 + 4*l.
-__device__ __forceinline__ void dma4_flat(uint32_t lds, const void* gaddr) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
-                 :
-                 : "s"(lds), "v"(gaddr)
-                 : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Workgroup barrier without the LDS fence of __syncthreads (which waits for every outstanding LDS
-// read of the wave). The memory clobber keeps the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <int MT, int NT, int WM, int WN, int NS>
 struct SlabGeom {
@@ -351,60 +335,9 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
 
     // epilogue
     wait_vmcnt0();
-    const int m_w = wg_m * MT + wm * MPW * 32 + 4 * (lane >> 5);
-    const int n_w = wg_n * NT + wn * NPW * 32 + (lane & 31);
-    if constexpr (!SPLIT && sizeof(OutT) == 2) {
-        if (!MASK || (N & 1) == 0) {
-            // 16-bit output in 4-byte stores: lanes 2k and 2k+1 (columns c, c+1) trade halves so
-            // that the even lane holds rows +0 and +2 of both columns and the odd lane rows +1
-            // and +3 (one quad_perm DPP move and three byte permutes per 4 values), halving the
-            // store instructions. The conversions are the per-element ones of cvt_out.
-            const bool odd = (lane & 1) != 0;
-            const uint32_t sel_send = odd ? 0x05040100u : 0x07060302u;
-            const uint32_t sel_a = odd ? 0x03020504u : 0x05040100u;
-            const uint32_t sel_b = odd ? 0x03020706u : 0x07060100u;
-            const int m_p = m_w + (lane & 1), n_p = n_w & ~1;
-#pragma unroll
-            for (int mi = 0; mi < MPW; mi++)
-#pragma unroll
-                for (int ni = 0; ni < NPW; ni++)
-#pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const v16f& a = acc[mi][ni];
-                        const uint32_t p01 = half_bits(cvt_out<OutT>(a[4 * g])) |
-                                             (half_bits(cvt_out<OutT>(a[4 * g + 1])) << 16);
-                        const uint32_t p23 = half_bits(cvt_out<OutT>(a[4 * g + 2])) |
-                                             (half_bits(cvt_out<OutT>(a[4 * g + 3])) << 16);
-                        const uint32_t send = __builtin_amdgcn_perm(p23, p01, sel_send);
-                        const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp(
-                            (int)send, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
-                        const uint32_t oa = __builtin_amdgcn_perm(recv, p01, sel_a);
-                        const uint32_t ob = __builtin_amdgcn_perm(recv, p23, sel_b);
-                        const int m = m_p + mi * 32 + 8 * g, n = n_p + ni * 32;
-                        if (MASK && n >= N) continue;  // n even and N even: n + 1 < N as well
-                        uint32_t* d0 = reinterpret_cast<uint32_t*>(D + (size_t)m * N + n);
-                        if (!MASK || m < M) *d0 = oa;
-                        if (!MASK || m + 2 < M) *reinterpret_cast<uint32_t*>(D + (size_t)(m + 2) * N + n) = ob;
-                    }
-            return;
-        }
-    }
-#pragma unroll
-    for (int mi = 0; mi < MPW; mi++)
-#pragma unroll
-        for (int ni = 0; ni < NPW; ni++)
-#pragma unroll
-            for (int g = 0; g < 4; g++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int m = m_w + mi * 32 + 8 * g + r, n = n_w + ni * 32;
-                    if (MASK && (m >= M || n >= N)) continue;
-                    const size_t idx = (size_t)m * N + n;
-                    if (SPLIT)
-                        ws[(size_t)wg_z * M * N + idx] = acc[mi][ni][4 * g + r];
-                    else
-                        D[idx] = cvt_out<OutT>(acc[mi][ni][4 * g + r]);
-                }
+    store_tile<MPW, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N,
+                                             wg_m * MT + wm * MPW * 32 + 4 * (lane >> 5),
+                                             wg_n * NT + wn * NPW * 32 + (lane & 31), lane, wg_z);
 }
 
 // ---- launch ----------------------------------------------------------------------------------
@@ -452,11 +385,39 @@ int slab_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     return e == hipSuccess ? 0 : 2;
 }
 
+// The wide tile (128 x 512, B straight to registers): the A repack first when asked, MASK when
+// the tile does not divide M x N. Three LDS chunk buffers, XCD groups of 8 tile rows (4 buffers
+// and groups of 4 or 16 rows measured within run-to-run noise on 8192^3, 2048x1024x105728 and
+// 2048x6144x16128).
+constexpr int WIDE_NB = 3, WIDE_XG = 8;
+template <int NB, int XG, typename KT, bool SPLIT>
+int wide_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
+    using G = WideGeom<NB>;
+    static_assert(G::LDS <= 160 * 1024, "LDS budget");
+    const bool mask = d->M % G::MT != 0 || d->N % G::NT != 0;
+    const uint8_t* A = static_cast<const uint8_t*>(d->A);
+    if (d->a_layout == MXFP6_A_REPACK) {
+        if (repack_rows_launch(A, d->A_row_bytes, d->M, d->Kp / 64, static_cast<uint8_t*>(d->Ash),
+                               st) != hipSuccess)
+            return 2;
+        A = static_cast<const uint8_t*>(d->Ash);
+    }
+    hipError_t e;
+    if (d->a_layout == MXFP6_A_ROWS)
+        e = mask ? wide_kernel_launch<NB, XG, KT, SPLIT, false, true>(d, A, st)
+                 : wide_kernel_launch<NB, XG, KT, SPLIT, false, false>(d, A, st);
+    else
+        e = mask ? wide_kernel_launch<NB, XG, KT, SPLIT, true, true>(d, A, st)
+                 : wide_kernel_launch<NB, XG, KT, SPLIT, true, false>(d, A, st);
+    return e == hipSuccess ? 0 : 2;
+}
+
 // Tile dispatch (declared in slab_run.hpp; instantiated once per (KT, SPLIT) in its own
 // translation unit: slab_split.hip, slab_f32.hip, slab_f16.hip, slab_bf16.hip).
 template <typename KT, bool SPLIT>
 int slab_run(const mxfp6_launch_desc* d, hipStream_t st) {
     if (!tile_supported(d->MT, d->NT, d->mpw, d->npw)) return 1;
+    if (d->MT == 128 && d->NT == 512) return wide_launch_t<WIDE_NB, WIDE_XG, KT, SPLIT>(d, st);
     // skinny tiles: one wave row, four wave columns, a deeper ring
     if (d->MT == 32 && d->NT == 128) return slab_launch_t<32, 128, 1, 4, 4, 8, KT, SPLIT>(d, st);
     if (d->MT == 32 && d->NT == 256) return slab_launch_t<32, 256, 1, 4, 4, 8, KT, SPLIT>(d, st);

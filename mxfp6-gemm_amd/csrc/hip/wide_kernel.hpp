@@ -1,0 +1,282 @@
+// Wide tile kernel of libmxfp6gemm for gfx950: a 128 x 512 tile of D, four waves side by side.
+//
+// Wave w owns all 128 rows and columns [128 w, 128 w + 128) of the tile: MPW = NPW = 4 blocks of
+// 32, sixteen 32x32 FP32 accumulators in AGPRs, fed by v_mfma_scale_f32_32x32x64_f8f6f4 (FP6
+// E2M3 x FP6 E2M3 with per-lane E8M0 scales). No B block is needed by two waves, so
+//   B  streams straight from the preshuffled layout into the wave's MFMA operand registers: per
+//      64-wide K slab and block, one 16-byte load (lane t: bytes 16t) and one 8-byte load (bytes
+//      1024 + 8t) of the block's 1536-byte tile, each a contiguous piece of memory. The operands
+//      sit in a ring of three register slots; slot s holds slab 3c + s of K-tile c, and the loads
+//      of slab q + 3 are issued during slab q, a block's two loads right after the last MFMA that
+//      reads the block. The scales (tiled layout: a lane's three slab dwords of a K-tile are
+//      contiguous) come one K-tile ahead, one 12-byte load per operand at the start of K-tile c for
+//      K-tile c + 1, into registers moved to the current set when K-tile c ends.
+//   A  (the 128 rows, needed by every wave) is staged in LDS one K-tile at a time: a chunk holds,
+//      per row, the K-tile's 144 contiguous bytes of the row-major operand (or, for A repacked
+//      into the preshuffled layout, the K-tile's three 1536-byte tiles of each 32-row block),
+//      18 KiB, copied with direct-to-LDS 16-byte loads (global_load_lds_dwordx4). A row's 144
+//      bytes take 2-3 cache lines where a 64-wide slab copy of 48 bytes takes 1-2 per slab, so
+//      row-major A costs about half the L2 requests of a per-slab copy. Chunks go through a ring
+//      of NB LDS buffers: chunk c + NB - 1 is copied during K-tile c (5 copy instructions per wave:
+//      18 KiB is 18 wave copies, two dummies keep the count uniform), and a wave reads each slab's
+//      four A operand blocks during the previous slab into one of three register sets.
+// One workgroup barrier per K-tile, at the start of its last slab: before it, each wave waits for
+// its own copies of the next chunk (vmcnt, exact: the issue order is static) and for its LDS reads
+// (lgkmcnt(0)); after it the next chunk is complete for every wave and the chunk read before the
+// current one is free for the copies of K-tile c + NB - 1. The B loads and scale loads are
+// ordinary loads whose waits the compiler places before the MFMAs that use them.
+// Prefetches past the workgroup's last K-tile are clamped to that K-tile (valid addresses, data
+// never used), so the K loop has no branch. MASK (ragged M or N) clamps the copy and load sources
+// of the last tile row and column and masks the stores, as in the slab kernel.
+#pragma once
+
+#include "../hip_layer.h"
+#include "device_common.hpp"
+#include "epilogue.hpp"
+#include "lds_dma.hpp"
+
+namespace mxfp6_dev {
+
+// Vector-memory instructions a wave of the wide kernel issues per slab s of a K-tile, in order:
+// after MFMA 0 of slab 0: the two scale loads of the next K-tile; after MFMA 1: a copy; after
+// MFMA 3: 2 B loads; after MFMA 5: a copy (s < 2); after MFMAs 7, 11 and 15: 2 B loads each.
+constexpr int wide_copies_in_slab(int s) { return s < 2 ? 2 : 1; }
+constexpr int wide_ops_in_slab(int s) { return (s == 0 ? 2 : 0) + 8 + wide_copies_in_slab(s); }
+constexpr int wide_ops_in_ktile() { return wide_ops_in_slab(0) + wide_ops_in_slab(1) + wide_ops_in_slab(2); }
+
+template <int NB_>
+struct WideGeom {
+    static constexpr int MT = 128, NT = 512, MPW = 4, NPW = 4, NWAVES = 4, THREADS = 256;
+    static constexpr int NB = NB_;                               // LDS chunk buffers
+    static constexpr int CHUNK = MT * SUBS * SLAB_BYTES;         // 18432: one K-tile of A
+    static constexpr int COPIES = CHUNK / 1024;                  // 18 wave copies of 1 KiB
+    static constexpr int A_ISS = (COPIES + NWAVES - 1) / NWAVES; // 5 per wave per chunk
+    static constexpr int LDS = NB * CHUNK + 1024;                // + dummy sink
+    // Before the barrier at the start of slab 2 of K-tile c, the wave's copies of chunk c + 1
+    // (issued during K-tile c + 2 - NB, the last one after MFMA 1 of its slab 2) must have
+    // landed; issued after that copy: the 8 B loads of the rest of that slab, NB - 3 whole
+    // K-tiles, and slabs 0 and 1 of K-tile c.
+    static constexpr int CHUNK_WAIT =
+        8 + (NB - 3) * wide_ops_in_ktile() + wide_ops_in_slab(0) + wide_ops_in_slab(1);
+    // In the prologue: after chunk 0's copies, those of chunks 1 .. NB - 2, the 2 scale loads of
+    // K-tile 0 and the 24 B loads of its three slabs.
+    static constexpr int PRO_WAIT = (NB - 2) * A_ISS + 2 + SUBS * 2 * NPW;
+    static_assert(NB >= 3, "a chunk is read for a K-tile after its copies were issued");
+    static_assert(A_ISS == wide_copies_in_slab(0) + wide_copies_in_slab(1) + wide_copies_in_slab(2),
+                  "copies");
+    static_assert(CHUNK_WAIT <= 63 && PRO_WAIT <= 63, "vmcnt range");
+};
+
+template <int NB_, int XG, typename OutT, bool SPLIT, bool ASH, bool MASK>
+__global__ void __launch_bounds__(256, 1)
+    wide_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
+                const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
+                OutT* __restrict__ D, float* __restrict__ ws, int M, int N, int Kp,
+                int A_row_bytes, int S) {
+    using G = WideGeom<NB_>;
+    constexpr int MT = G::MT, NT = G::NT, MPW = G::MPW, NPW = G::NPW, NB = G::NB;
+    constexpr int CHUNK = G::CHUNK;
+    __shared__ __attribute__((aligned(1024))) char lds[G::LDS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int wg_m = blockIdx.x, wg_n = blockIdx.y, wg_z = SPLIT ? (int)blockIdx.z : 0;
+    if constexpr (XG > 0) {
+        const int gm = (int)gridDim.x, gn = (int)gridDim.y;
+        if (SPLIT && gm * gn <= 128)
+            xcd_split_tile(gm, gn, S, XG,
+                           (int)((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x),
+                           wg_m, wg_n, wg_z);
+        else if (!SPLIT || (gm * gn) % NXCD == 0)
+            xcd_tile(gm, gn, XG, (int)(blockIdx.y * gridDim.x + blockIdx.x), wg_m, wg_n);
+    }
+    const int k64n = Kp / 64, k_tiles = Kp / 192;
+    int kt0 = 0, nkt = k_tiles;
+    if (SPLIT) split_segment(k_tiles, S, wg_z, kt0, nkt);
+    const int kt_last = kt0 + nkt - 1;
+
+    // ---- A chunk copies: copy i of this wave fills bytes [1024 j, 1024 j + 1024) of a chunk,
+    // j = 4 i + wave; lane l's 16 bytes land at 1024 j + 16 l
+    const int a_row_last = M - 1 - wg_m * MT;                     // MASK: last valid row
+    const int a_blk_last = (M + 31) / 32 - 1 - wg_m * (MT / 32);  // MASK: last valid block
+    const uint8_t* a_tile = ASH ? A + (size_t)wg_m * (MT / 32) * k64n * OPBLK_BYTES
+                                : A + (size_t)wg_m * MT * A_row_bytes;
+    uint32_t a_voff[G::A_ISS];
+#pragma unroll
+    for (int i = 0; i < G::A_ISS; i++) {
+        const int j = i * G::NWAVES + wave;
+        const int x = (j < G::COPIES ? j : 0) * 1024 + 16 * lane;  // dummies copy chunk byte 16 l
+        if (ASH) {
+            int blk = x / (SUBS * OPBLK_BYTES);
+            const int rest = x - blk * (SUBS * OPBLK_BYTES);
+            if (MASK) blk = min(blk, a_blk_last);
+            a_voff[i] = (uint32_t)(blk * k64n * OPBLK_BYTES + rest);
+        } else {
+            int row = x / (SUBS * SLAB_BYTES);
+            const int col = x - row * (SUBS * SLAB_BYTES);
+            if (MASK) row = min(row, a_row_last);
+            a_voff[i] = (uint32_t)(row * A_row_bytes + col);
+        }
+    }
+    const uint32_t lds0 = lds_u32(lds);
+    const uint32_t lds_dummy = __builtin_amdgcn_readfirstlane(lds0 + NB * CHUNK);
+    // copy i of chunk kt (absolute K-tile, clamped to the segment) into LDS buffer buf
+    auto a_copy = [&](int i, int kt, int buf) {
+        const int j = i * G::NWAVES + wave;
+        const uint32_t dst = j < G::COPIES ? lds0 + buf * CHUNK + j * 1024 : lds_dummy;
+        const uint8_t* src = a_tile + (size_t)kt * (ASH ? SUBS * OPBLK_BYTES : SUBS * SLAB_BYTES);
+        dma16(__builtin_amdgcn_readfirstlane(dst), src, a_voff[i]);
+    };
+
+    // ---- B operand and scale loads of this wave
+    const int b_blk_last = (N + 31) / 32 - 1;
+    const int sa_grp_last = ((M + 31) / 32 + MPW - 1) / MPW - 1;
+    const int sb_grp_last = ((N + 31) / 32 + NPW - 1) / NPW - 1;
+    gbl_cptr b_col[NPW];
+#pragma unroll
+    for (int ni = 0; ni < NPW; ni++) {
+        int blk = wg_n * (NT / 32) + wave * NPW + ni;
+        if (MASK) blk = min(blk, b_blk_last);
+        b_col[ni] = opaque_gptr(Bsh + (size_t)blk * k64n * OPBLK_BYTES);
+    }
+    int ga = wg_m, gb = wg_n * G::NWAVES + wave;
+    if (MASK) ga = min(ga, sa_grp_last), gb = min(gb, sb_grp_last);
+    // lane's scale dwords of K-tile 0 (the dword of slab s at + 4 s)
+    const gbl_cptr sa_lane = opaque_gptr(sA + (size_t)ga * k_tiles * 64 * 12) + lane * 12;
+    const gbl_cptr sb_lane = opaque_gptr(sB + (size_t)gb * k_tiles * 64 * 12) + lane * 12;
+
+    // slab s of K-tile kt, block ni, into v
+    auto load_b = [&](v8i& v, int ni, int kt, int s) {
+        const gbl_cptr p = b_col[ni] + (size_t)(kt * SUBS + s) * OPBLK_BYTES;
+        const v4i y0 = *reinterpret_cast<__attribute__((address_space(1))) const v4i*>(p + 16 * lane);
+        const v2i y1 = *reinterpret_cast<__attribute__((address_space(1))) const v2i*>(p + 1024 + 8 * lane);
+        const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
+        v = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
+    };
+    // the lane's three slab scale dwords of K-tile kt, for A and for B
+    auto load_scales = [&](v3i& a, v3i& b, int kt) {
+        a = *reinterpret_cast<__attribute__((address_space(1))) const v3i_a4*>(sa_lane + (size_t)kt * 768);
+        b = *reinterpret_cast<__attribute__((address_space(1))) const v3i_a4*>(sb_lane + (size_t)kt * 768);
+    };
+
+    // ---- A operand reads (LDS): slab s of the chunk in buffer buf, block mi
+    const lds_cptr lds3 = (lds_cptr)lds;
+    const uint32_t a_rd = ASH ? (uint32_t)(lane * 16)
+                              : (uint32_t)((lane & 31) * SUBS * SLAB_BYTES + (lane >> 5) * 24);
+    auto read_a = [&](v8i& dst, int buf, int s, int mi) {
+        if (ASH) {
+            const uint32_t o = opaque_v(buf * CHUNK + (mi * SUBS + s) * OPBLK_BYTES + a_rd);
+            const v4i y0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(lds3 + o);
+            const v2i y1 = *reinterpret_cast<const __attribute__((address_space(3))) v2i*>(
+                lds3 + o + 1024 - 8 * lane);
+            const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
+            dst = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
+        } else {
+            const uint32_t o = opaque_v(buf * CHUNK + mi * 32 * SUBS * SLAB_BYTES + s * SLAB_BYTES + a_rd);
+            const v6i_a8 x = *reinterpret_cast<const __attribute__((address_space(3))) v6i_a8*>(lds3 + o);
+            dst = __builtin_shufflevector(x, x, 0, 1, 2, 3, 4, 5, -1, -1);
+        }
+    };
+
+    v16f acc[MPW][NPW];
+#pragma unroll
+    for (int i = 0; i < MPW; i++)
+#pragma unroll
+        for (int j = 0; j < NPW; j++) acc[i][j] = v16f{};
+
+    v8i RB[SUBS][NPW];     // B operands, slot s = slab s of a K-tile
+    v8i RA[SUBS][MPW];     // A operands
+    v3i sc_a, sc_b;        // scale dwords of the current K-tile
+    v3i sn_a, sn_b;        // and of the next one
+
+    // prologue: chunks 0 .. NB-2 in flight, then the scales of K-tile 0 and the B operands of its
+    // three slabs, in the order the loop issues them (the compiler, which places the B waits,
+    // then sees the same count of loads in flight on entry to the loop as around it; the empty
+    // asm statements keep it from merging or reordering the loads)
+#pragma unroll
+    for (int c = 0; c < NB - 1; c++)
+#pragma unroll
+        for (int i = 0; i < G::A_ISS; i++) a_copy(i, min(kt0 + c, kt_last), c);
+    load_scales(sc_a, sc_b, kt0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < SUBS; s++)
+#pragma unroll
+        for (int ni = 0; ni < NPW; ni++) {
+            load_b(RB[s][ni], ni, kt0, s);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    wait_vmcnt<G::PRO_WAIT>();  // chunk 0 landed
+    ring_barrier();
+#pragma unroll
+    for (int mi = 0; mi < MPW; mi++) read_a(RA[0][mi], 0, 0, mi);
+
+    int buf = 0;  // LDS buffer of K-tile c's chunk
+    for (int c = 0; c < nkt; c++) {
+        const int nbuf = buf + 1 == NB ? 0 : buf + 1;            // chunk c + 1
+        const int cbuf = buf == 0 ? NB - 1 : buf - 1;            // chunk c + NB - 1 (c - 1's)
+        const int kt_copy = min(kt0 + c + NB - 1, kt_last);
+        const int kt_next = min(kt0 + c + 1, kt_last);
+#pragma unroll
+        for (int s = 0; s < SUBS; s++) {
+            if (s == SUBS - 1) {
+                // chunk c + 1 complete for every wave before its first slab is read below; every
+                // wave's reads of chunk c - 1 are complete, so its buffer may take chunk c + NB - 1
+                wait_vmcnt<G::CHUNK_WAIT>();
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                ring_barrier();
+            }
+            // slab s + 1 of this K-tile, or slab 0 of the next, goes to RA[(s + 1) % 3]
+            const int rbuf = s + 1 < SUBS ? buf : nbuf;
+            const int rs = s + 1 < SUBS ? s + 1 : 0;
+            int ci = s == 0 ? 0 : s == 1 ? 2 : 4;  // first copy index of this slab
+            const int sa = s == 0 ? sc_a.x : s == 1 ? sc_a.y : sc_a.z;
+            const int sb = s == 0 ? sc_b.x : s == 1 ? sc_b.y : sc_b.z;
+#pragma unroll
+            for (int k = 0; k < MPW * NPW; k++) {
+                const int ni = k / MPW, mi = k % MPW;
+                switch (ni * 4 + mi) {
+#define WX_CASE(J, I)                                                                           \
+    case J * 4 + I:                                                                             \
+        acc[I][J] = mfma_fp6<I, J>(acc[I][J], RA[s][I], RB[s][J], sa, sb);                      \
+        break;
+                    WX_CASE(0, 0) WX_CASE(0, 1) WX_CASE(0, 2) WX_CASE(0, 3)
+                    WX_CASE(1, 0) WX_CASE(1, 1) WX_CASE(1, 2) WX_CASE(1, 3)
+                    WX_CASE(2, 0) WX_CASE(2, 1) WX_CASE(2, 2) WX_CASE(2, 3)
+                    WX_CASE(3, 0) WX_CASE(3, 1) WX_CASE(3, 2) WX_CASE(3, 3)
+#undef WX_CASE
+                }
+                if (s == 0 && k == 0) load_scales(sn_a, sn_b, kt_next);
+                if ((k == 1 || k == 5) && ci < (s == 0 ? 2 : s == 1 ? 4 : 5)) a_copy(ci++, kt_copy, cbuf);
+                if (k % MPW == MPW - 1) load_b(RB[s][ni], ni, kt_next, s);
+                if (k >= 8 && k < 8 + MPW) read_a(RA[(s + 1) % SUBS][k - 8], rbuf, rs, k - 8);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        sc_a = sn_a;
+        sc_b = sn_b;
+        buf = nbuf;
+    }
+
+    // epilogue (the clamped prefetches of the last K-tiles are drained first)
+    wait_vmcnt0();
+    store_tile<MPW, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N, wg_m * MT + 4 * (lane >> 5),
+                                             wg_n * NT + wave * NPW * 32 + (lane & 31), lane,
+                                             wg_z);
+}
+
+// One launch of the wide kernel (grid ceil(M/128) x ceil(N/512) x splits, 256 threads).
+template <int NB, int XG, typename KT, bool SPLIT, bool ASH, bool MASK>
+hipError_t wide_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipStream_t st) {
+    using G = WideGeom<NB>;
+    const dim3 grid((unsigned)((d->M + G::MT - 1) / G::MT), (unsigned)((d->N + G::NT - 1) / G::NT),
+                    (unsigned)d->splits);
+    return launch_kernel(wide_kernel<NB, XG, KT, SPLIT, ASH, MASK>, grid, dim3(G::THREADS), st,
+                         A, static_cast<const uint8_t*>(d->Bsh), d->sA, d->sB,
+                         SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr, d->M,
+                         d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1);
+}
+
+}  // namespace mxfp6_dev

@@ -1,0 +1,70 @@
+"""The wide tile (128 x 512, four waves side by side, B streamed straight into registers, A staged
+in LDS one K-tile per row): bit for bit equal to the direct kernel (same MFMAs, same K order) with
+row-major and repacked A, unsplit and split on both XCD maps; equal to the 256x256 slab kernel on
+ragged (masked) shapes, which groups scales the same way; all output types against the FP64
+oracle."""
+import numpy as np
+import pytest
+
+import checks
+import mxfp6_amd as mx
+import gpu_util as g
+
+pytestmark = pytest.mark.gpu
+
+WIDE = (128, 512, 4, 4)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 1024, 2112), (128, 512, 192), (256, 2048, 4224)])
+@pytest.mark.parametrize("a_layout", [0, 1])
+def test_wide_bitwise_equals_direct(M, N, K, a_layout):
+    p = mx.make_problem(M, N, K, seed=M + N + K + a_layout)
+    dp = g.DevProblem(p, WIDE)
+    Dw = g.run_explicit(dp, mx.OUT_F32, a_layout=a_layout)
+    Dd = g.run_direct(dp, mx.OUT_F32)
+    assert np.array_equal(Dw.view(np.uint32), Dd.view(np.uint32))
+
+
+@pytest.mark.parametrize("S", [2, 3, 8])
+@pytest.mark.parametrize("M,N", [(512, 1024), (2048, 1024)])
+def test_wide_split_bitwise_equals_direct_split(M, N, S):
+    """Split grids: at most 128 tiles hand each XCD whole K segments, more use the grid order;
+    every partial lands in its segment's slot either way."""
+    K = 4224  # 22 K-tiles: uneven segments
+    p = mx.make_problem(M, N, K, seed=S * 7 + M)
+    dp = g.DevProblem(p, WIDE)
+    for a_layout in (0, 1):
+        Dw = g.run_explicit(dp, mx.OUT_F32, splits=S, a_layout=a_layout)
+        Dd = g.run_direct(dp, mx.OUT_F32, splits=S)
+        assert np.array_equal(Dw.view(np.uint32), Dd.view(np.uint32)), a_layout
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 700, 960), (97, 1000, 2112), (129, 513, 384),
+                                   (1, 33, 192)])
+def test_wide_masked_equals_slab_masked(M, N, K):
+    """Ragged shapes run the wide tile masked; its FP32 output equals the masked 256x256 slab
+    kernel's (same scale grouping, same K order) bit for bit, and both meet the oracle bar."""
+    p = mx.make_problem(M, N, K, seed=M * 7 + N)
+    dw = g.DevProblem(p, WIDE)
+    ds = g.DevProblem(p, (256, 256, 4, 4))
+    for a_layout, S in ((0, 1), (1, 1), (0, 3)):
+        if S > p.Kp // 192:
+            continue
+        Dw = g.run_explicit(dw, mx.OUT_F32, splits=S, a_layout=a_layout)
+        Ds = g.run_explicit(ds, mx.OUT_F32, splits=S, a_layout=a_layout)
+        assert np.array_equal(Dw.view(np.uint32), Ds.view(np.uint32)), (a_layout, S)
+    import oracle
+    R, ab = oracle.problem_f64(p)
+    checks.check(Dw, R, ab, mx.OUT_F32)
+
+
+@pytest.mark.parametrize("out_type", [0, 1, 2])
+def test_wide_output_types_against_oracle(out_type):
+    import oracle
+    M, N, K = 256, 1024, 960  # K-tail: kpad(960) = 1152
+    p = mx.make_problem(M, N, K, dist_a=mx.DIST_STUDENT_T3, dist_b=mx.DIST_STUDENT_T3, seed=13)
+    dp = g.DevProblem(p, WIDE)
+    R, ab = oracle.problem_f64(p)
+    for a_layout in (0, 1):
+        D = g.run_explicit(dp, out_type, a_layout=a_layout)
+        checks.check(D, R, ab, out_type)
