@@ -15,9 +15,11 @@ namespace plan {
 
 // ---- router ------------------------------------------------------------------------------
 //
-// Candidate tiles (each an instantiation of the pipelined kernel, 4 waves per workgroup):
+// Candidate tiles (4 waves per workgroup):
 //   256x256, waves 2x2, each wave 128x128 -> MPW 4, NPW 4   (16 MFMAs per wave per 64-wide slab)
 //   256x192, waves 2x2, each wave 128x96  -> MPW 4, NPW 3   (12)
+//   128x512, waves 1x4, each wave 128x128 -> MPW 4, NPW 4   (16; the wide kernel: B straight into
+//            registers, A staged in LDS one K-tile at a time)
 //   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3   (12)
 //   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4   (8)
 //   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (4; two workgroups fit a CU's LDS)
@@ -25,30 +27,38 @@ namespace plan {
 // 32), and on small grids faster than the big ones for any M (C1, 256x256x1024: 32x128 6.3 us
 // against 8.2 us on 128x128):
 //   64x256 (MPW 2, NPW 2), 32x256 (1, 2), 64x128 (2, 1), 32x128 (1, 1; two per CU)
-// Ragged shapes (M not a multiple of 32 or N not a multiple of 128) take any of the nine tiles,
+// Ragged shapes (M not a multiple of 32 or N not a multiple of 128) take any of the ten tiles,
 // the last tile row and column masked (wg counts the partial tiles).
-// A plan is (tile, K segments S, A repacked or not); the router takes the plan with the least
-// predicted time. The time model (microseconds, MI355X) follows the kernel's structure:
+// A plan is (tile, K segments S from SPLIT_CHOICES, A repacked or not); the router takes the plan
+// with the least predicted time. The time model (microseconds, MI355X) follows the kernel's
+// structure:
 //   wg       = ceil(M / MT) * ceil(N / NT) workgroups per K segment;
 //   waves    = ceil(wg * S / (CUS * occupancy)) rounds of workgroups;
-//   per_cu   = ceil(min(wg * S, CUS * occupancy) / CUS) workgroups on the busiest CU;
+//   active   = min(wg * S, CUS * occupancy) workgroups in flight;
+//   per_cu   = ceil(active / CUS) workgroups on the busiest CU;
 //              (CUS: the current device's compute units, 256 on an MI355X)
-//   t_slab   = max(T_SLAB_MIN, per_cu * (T_MFMA * mfmas + T_COPY_KB * copied KiB)) per 64-wide K
-//              slab: a latency floor (the ring keeps four slabs in flight), else the CU's MFMA and
-//              global->LDS copy work, shared by the workgroups resident on it; a row-major A slab
-//              costs A_ROWS_COST more per byte than a preshuffled one (a copy touches ~3 cache
-//              lines per 128 bytes instead of 1);
+//   kb       = KiB a workgroup moves per 64-wide K slab: A (MT * 48 bytes, times 1 + A_ROWS_COST
+//              when read row-major: a copy touches ~3 cache lines per 128 bytes instead of 1) and
+//              B (NT / 32 * 1536 bytes);
+//   t_slab   = max(T_SLAB_MIN, per_cu * (T_MFMA * mfmas + T_COPY_KB * kb),
+//                  active * T_L2_KB * kb) per slab: a latency floor (the ring keeps several slabs
+//              in flight), the CU's MFMA and global->LDS copy work shared by the workgroups
+//              resident on it, and the chip's L2 -> CU delivery shared by every workgroup in
+//              flight; the 128x512 tile loads B into registers (T_BREG_KB per KiB) and copies A
+//              at its own row-major cost (A_ROWS_COST_WIDE: a K-tile row is 144 contiguous bytes);
 //   t_wg     = T_WG + slabs * t_slab + T_OUT_KB * output KiB * per_cu;
 //   t        = T_LAUNCH + waves * t_wg, plus for a repack T_LAUNCH + its bytes (A read and written)
 //              at REPACK_BYTES_PER_US, and for a split T_LAUNCH + the partials written and read
 //              back at SPLIT_BYTES_PER_US.
-// The constants are a least-squares fit (log time) to every plan of the 66 measured shapes with
-// M % 128 == 0 (one MI355X; M from 128 to 8192, N from 128 to 102272, K from 1024 to 105728,
-// masked N and the skinny tiles included), plans within 1.3x of their shape's best weighing 5x
-// the others; the repack rate is the repack kernel's measured one. On the 63 of those shapes whose
-// pick was measured, the plan the model picks is within 2.1% of the measured best on average, 16%
-// at worst, and it is the best on the five benchmark workloads; on the 14 skinny-M and ragged
-// shapes within 3.4% on average, 10% at worst.
+// The constants are fitted to every plan of the 82 measured shapes (one MI355X; M from 32 to
+// 8192, N from 77 to 102272, K from 1024 to 105728, ragged and skinny shapes included), choosing
+// the plan, not predicting every time: the fit minimises the summed log of (measured time of the
+// model's pick / measured best) over the shapes with M % 128 == 0, the five benchmark workloads
+// weighing 5x, plus 0.1x the log-time least squares of the plans within 1.3x of their shape's
+// best (0.2x weight for the others); the repack rate is the repack kernel's measured one. The
+// pick is then within 1.8% of the measured best on average over the 66 shapes with M % 128 == 0,
+// 26% at worst (2048x2048x8192), and the best on the five benchmark workloads; on the 16 skinny-M
+// and ragged shapes within 1.0% on average, 6% at worst.
 namespace {
 struct Plan {
     TileChoice tc;
@@ -56,7 +66,7 @@ struct Plan {
     bool repack;
 };
 const TileChoice kCands[] = {{256, 256, 4, 4}, {256, 192, 4, 3}, {128, 384, 4, 3},
-                             {128, 256, 2, 4}, {128, 128, 2, 2}};
+                             {128, 256, 2, 4}, {128, 128, 2, 2}, {128, 512, 4, 4}};
 const TileChoice kSkinny[] = {{64, 256, 2, 2}, {32, 256, 1, 2}, {64, 128, 2, 1}, {32, 128, 1, 1}};
 
 double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repack, int CUS) {
@@ -64,13 +74,16 @@ double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repa
     const int occ = (tc.NT == 128 && (tc.MT == 128 || tc.MT == 32)) ? 2 : 1;  // per CU (LDS)
     const long cap = (long)CUS * occ;
     const long waves = (wg + cap - 1) / cap;
-    const long per_cu = std::max(1L, (std::min(wg, cap) + CUS - 1) / CUS);  // on the busiest CU
+    const long active = std::min(wg, cap);
+    const long per_cu = std::max(1L, (active + CUS - 1) / CUS);  // on the busiest CU
     const int mfmas = tc.MPW * tc.NPW;  // per wave per slab
     const double slabs = (double)(Kp / 64) / S;
-    const double copy_kb =
-        (tc.MT * 48.0 * (repack ? 1.0 : 1.0 + A_ROWS_COST) + tc.NT / 32 * 1536.0) / 1024.0;
-    const double t_slab =
-        std::max(T_SLAB_MIN, (double)per_cu * (T_MFMA * mfmas + T_COPY_KB * copy_kb));
+    const bool wide = tc.MT == 128 && tc.NT == 512;
+    const double a_cost = repack ? 1.0 : 1.0 + (wide ? A_ROWS_COST_WIDE : A_ROWS_COST);
+    const double a_kb = tc.MT * 48.0 * a_cost / 1024.0, b_kb = tc.NT / 32 * 1536.0 / 1024.0;
+    const double work = T_COPY_KB * a_kb + (wide ? T_BREG_KB : T_COPY_KB) * b_kb;
+    const double t_slab = std::max({T_SLAB_MIN, (double)per_cu * (T_MFMA * mfmas + work),
+                                    (double)active * T_L2_KB * (a_kb + b_kb)});
     const double out_kb = tc.MT * tc.NT * (S > 1 ? 4.0 : 2.0) / 1024.0;
     const double t_wg = T_WG + slabs * t_slab + T_OUT_KB * out_kb * per_cu;
     double t = T_LAUNCH + (double)waves * t_wg;
@@ -97,7 +110,7 @@ const int kNSkinny = (int)(sizeof(kSkinny) / sizeof(kSkinny[0]));
 // fewer launches and less workspace. Regular shapes take the tiles whose MT divides M, with the
 // last tile column masked when NT does not divide N (the reference's NMASK route,
 // src/kernel.hpp:144-154, for any tile: N = 102272 runs 256x256 over ceil(N/256) columns instead
-// of 128x128); ragged shapes any of the nine, big tiles first. Shapes gemm() rejects get the
+// of 128x128); ragged shapes any of the ten, big tiles first. Shapes gemm() rejects get the
 // trivial plan.
 Plan best_plan(int M, int N, int Kp, int cus) {
     Plan best = {{128, 128, 2, 2}, 1, false};
@@ -110,8 +123,8 @@ Plan best_plan(int M, int N, int Kp, int cus) {
     // N-masked ones
     for (int pass = 0; pass < (reg ? 2 : 1); pass++)
         for (int rp = 0; rp < 2; rp++)
-            for (int S = 1; S <= MAX_SPLITS && S <= k_tiles; S++)
-                for (int ci = 0; ci < kNCands + kNSkinny; ci++) {
+            for (const int S : SPLIT_CHOICES)
+                for (int ci = 0; ci < kNCands + kNSkinny && S <= k_tiles; ci++) {
                     const TileChoice& tc = ci < kNCands ? kCands[ci] : kSkinny[ci - kNCands];
                     if (reg && (M % tc.MT != 0 || (N % tc.NT != 0) != (pass == 1))) continue;
                     // a regular shape's scales may be tiled by the header's tile_scale, which

@@ -1,9 +1,10 @@
 """The router's plan-time model (csrc/host/plan.cpp plan_time_us / best_plan) in Python, and its
-least-squares fit to measured plans (sweep_plans.py output).
+fit to measured plans (sweep_plans.py output), which scores the plans the model picks.
 
   python mxfp6-gemm_amd/tune/plan_model.py [plans.jsonl ...]   # refit, print the constants and
                                                               # how close the picks come to the
                                                               # measured best plan per shape
+  python mxfp6-gemm_amd/tune/plan_model.py --no-fit            # the same for CONSTANTS
 The constants in CONSTANTS are the ones compiled into plan.hpp; tests check that this model and
 the library's router pick the same plans.
 """
@@ -15,66 +16,104 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CUS = 256
 K_TILE = 192
-MAX_SPLITS = 16
-TILES = [(256, 256, 4, 4), (256, 192, 4, 3), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2)]
+SPLIT_CHOICES = (1, 2, 3, 4, 6, 8, 12, 16)
+TILES = [(256, 256, 4, 4), (256, 192, 4, 3), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2),
+         (128, 512, 4, 4)]
+WIDE = (128, 512)  # the tile whose B goes straight to registers (wide_kernel.hpp)
 SKINNY = [(64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)]
-NAMES = ["T_LAUNCH", "T_WG", "T_SLAB_MIN", "T_MFMA", "T_COPY_KB", "T_OUT_KB", "REPACK_BYTES_PER_US",
-         "SPLIT_BYTES_PER_US", "A_ROWS_COST"]
-CONSTANTS = {"T_LAUNCH": 2.61668, "T_WG": 1.17567, "T_SLAB_MIN": 0.187174, "T_MFMA": 0.00709531,
-             "T_COPY_KB": 0.0153215, "T_OUT_KB": 0.0256923, "REPACK_BYTES_PER_US": 5.5e6,
-             "SPLIT_BYTES_PER_US": 4.4079e6, "A_ROWS_COST": 0.581966}
+NAMES = ["T_LAUNCH", "T_WG", "T_SLAB_MIN", "T_MFMA", "T_COPY_KB", "T_BREG_KB", "T_L2_KB",
+         "T_OUT_KB", "REPACK_BYTES_PER_US", "SPLIT_BYTES_PER_US", "A_ROWS_COST", "A_ROWS_COST_WIDE"]
+CONSTANTS = {"T_LAUNCH": 2.80193, "T_WG": 1.22045, "T_SLAB_MIN": 0.148425, "T_MFMA": 0.0130223,
+             "T_COPY_KB": 0.0130326, "T_BREG_KB": 0.00701515, "T_L2_KB": 7.00392e-05,
+             "T_OUT_KB": 0.014044, "REPACK_BYTES_PER_US": 5.5e6, "SPLIT_BYTES_PER_US": 3.99902e+06,
+             "A_ROWS_COST": 0.746816, "A_ROWS_COST_WIDE": 0.425206}
 # the repack rate is the repack kernel's measured one, not fitted
 FIXED = {"REPACK_BYTES_PER_US": 5.5e6}
-# plans within NEAR x the best of their shape weigh 1 in the fit, the others FAR_WEIGHT: the fit
-# should rank the contenders, not predict every hopeless plan
-NEAR, FAR_WEIGHT = 1.3, 0.2
+# the fit: summed log(measured time of the pick / measured best) per shape (the benchmark
+# workloads BENCH_WEIGHT x), plus REG_WEIGHT x the log-time least squares of every measured plan,
+# those within NEAR x the best of their shape weighing 1, the others FAR_WEIGHT; a pick that was
+# not measured counts UNMEASURED
+NEAR, FAR_WEIGHT, REG_WEIGHT, BENCH_WEIGHT, UNMEASURED = 1.3, 0.2, 0.1, 5.0, 1.3
+BENCH = {(256, 256, 1024), (8192, 8192, 8192), (2048, 6144, 16128), (2048, 1024, 105728),
+         (2048, 5120, 105728)}
 PLAN_MIN_GAIN = 0.01
 
 
-def plan_time_us(c, tile, M, N, Kp, S, repack):
+def _features(tile, M, N, Kp, S, repack):
     MT, NT = tile[0], tile[1]
     wg = -(-M // MT) * -(-N // NT) * S
     occ = 2 if (MT, NT) in ((128, 128), (32, 128)) else 1
     cap = CUS * occ
-    waves = (wg + cap - 1) // cap
-    per_cu = max(1, -(-min(wg, cap) // CUS))  # workgroups on the busiest CU
-    mfmas = tile[2] * tile[3]
-    slabs = (Kp // 64) / S
-    copy_kb = (MT * 48.0 * (1.0 if repack else 1.0 + c["A_ROWS_COST"]) + NT // 32 * 1536.0) / 1024.0
-    t_slab = max(c["T_SLAB_MIN"], per_cu * (c["T_MFMA"] * mfmas + c["T_COPY_KB"] * copy_kb))
-    out_kb = MT * NT * (4.0 if S > 1 else 2.0) / 1024.0
-    t_wg = c["T_WG"] + slabs * t_slab + c["T_OUT_KB"] * out_kb * per_cu
-    t = c["T_LAUNCH"] + waves * t_wg
-    if repack:
-        t += c["T_LAUNCH"] + 2.0 * (-(-M // 32) * 32) * (Kp // 4 * 3.0) / c["REPACK_BYTES_PER_US"]
-    if S > 1:
-        t += c["T_LAUNCH"] + (4.0 * S * M * N + 2.0 * M * N) / c["SPLIT_BYTES_PER_US"]
+    active = min(wg, cap)
+    return dict(waves=(wg + cap - 1) // cap, active=active, per_cu=max(1, -(-active // CUS)),
+                mfmas=tile[2] * tile[3], slabs=(Kp // 64) / S, wide=(MT, NT) == WIDE,
+                repack=bool(repack), akb=MT * 48.0 / 1024.0, bkb=NT // 32 * 1536.0 / 1024.0,
+                out_kb=MT * NT * (4.0 if S > 1 else 2.0) / 1024.0, split=S > 1,
+                rep_bytes=2.0 * (-(-M // 32) * 32) * (Kp // 4 * 3.0),
+                split_bytes=4.0 * S * M * N + 2.0 * M * N)
+
+
+def _time(c, f, xp=None):
+    """plan.cpp plan_time_us over one plan's features (scalars) or arrays of them (xp = numpy)."""
+    where = (lambda q, a, b: a if q else b) if xp is None else xp.where
+    mx = max if xp is None else xp.maximum
+    a_cost = where(f["repack"], 1.0, 1.0 + where(f["wide"], c["A_ROWS_COST_WIDE"], c["A_ROWS_COST"]))
+    a_kb = f["akb"] * a_cost
+    work = c["T_COPY_KB"] * a_kb + where(f["wide"], c["T_BREG_KB"], c["T_COPY_KB"]) * f["bkb"]
+    t_slab = mx(mx(c["T_SLAB_MIN"], f["per_cu"] * (c["T_MFMA"] * f["mfmas"] + work)),
+                f["active"] * c["T_L2_KB"] * (a_kb + f["bkb"]))
+    t_wg = c["T_WG"] + f["slabs"] * t_slab + c["T_OUT_KB"] * f["out_kb"] * f["per_cu"]
+    t = c["T_LAUNCH"] + f["waves"] * t_wg
+    t = t + where(f["repack"], c["T_LAUNCH"] + f["rep_bytes"] / c["REPACK_BYTES_PER_US"], 0.0)
+    t = t + where(f["split"], c["T_LAUNCH"] + f["split_bytes"] / c["SPLIT_BYTES_PER_US"], 0.0)
     return t
 
 
-def best_plan(c, M, N, Kp):
-    """(tile, S, repack) with the least predicted time, visiting plans from the simplest and
-    requiring a PLAN_MIN_GAIN lead to replace an earlier one (as plan.cpp does). Regular shapes
-    (M % 32 == 0, N % 128 == 0) take the tiles whose MT divides M, the 32- and 64-row ones
-    included (the last tile column masked when NT does not divide N, visited after every dividing
-    plan) whose scale grouping divides the shape; ragged ones any tile, masked."""
-    best, best_t = ((128, 128, 2, 2), 1, False), None
+def plan_time_us(c, tile, M, N, Kp, S, repack):
+    return _time(c, _features(tile, M, N, Kp, S, repack))
+
+
+def candidates(M, N, Kp):
+    """The plans best_plan visits, in its order. Regular shapes (M % 32 == 0, N % 128 == 0) take
+    the tiles whose MT divides M, the 32- and 64-row ones included (the last tile column masked
+    when NT does not divide N, visited after every dividing plan) whose scale grouping divides
+    the shape; ragged ones any tile, masked."""
     kt = Kp // K_TILE
     regular = M % 32 == 0 and N % 128 == 0
     cands = (SKINNY if M % 128 else TILES + SKINNY) if regular else TILES + SKINNY
+    out = []
     for masked in ((False, True) if regular else (None,)):
         for rp in (False, True):
-            for S in range(1, min(MAX_SPLITS, kt) + 1):
+            for S in SPLIT_CHOICES:
+                if S > kt:
+                    continue
                 for tile in cands:
                     if regular and (M % tile[0] or bool(N % tile[1]) != masked):
                         continue
                     # the header's tile_scale holds whole scale groups only
                     if regular and ((M // 32) % tile[2] or (N // 32) % tile[3]):
                         continue
-                    t = plan_time_us(c, tile, M, N, Kp, S, rp)
-                    if best_t is None or t < best_t * (1.0 - PLAN_MIN_GAIN):
-                        best, best_t = (tile, S, rp), t
-    return best
+                    out.append((tile, S, rp))
+    return out
+
+
+def _pick(times):
+    """Index of the router's pick: visiting in order, a plan replaces the current one only with a
+    PLAN_MIN_GAIN lead."""
+    bi = 0
+    while True:
+        later = [i for i in range(bi + 1, len(times)) if times[i] < times[bi] * (1.0 - PLAN_MIN_GAIN)]
+        if not later:
+            return bi
+        bi = later[0]
+
+
+def best_plan(c, M, N, Kp):
+    """(tile, S, repack) with the least predicted time, as plan.cpp best_plan."""
+    cands = candidates(M, N, Kp)
+    if not cands:
+        return ((128, 128, 2, 2), 1, False)
+    return cands[_pick([plan_time_us(c, t, M, N, Kp, S, rp) for t, S, rp in cands])]
 
 
 def load(paths):
@@ -85,62 +124,112 @@ def load(paths):
     return recs
 
 
-def fit(recs, start):
+def fit(recs, start, restarts=12, seed=0):
+    """Pick-aware fit (see the weights above) by Nelder-Mead from a least-squares start, with
+    perturbed restarts; returns (constants, objective)."""
     import numpy as np
     from scipy.optimize import minimize
 
     names = [n for n in NAMES if n not in FIXED]
+    feats, segs = [], []
+    for r in recs:
+        M, N, K = r["shape"]
+        Kp = (K + K_TILE - 1) // K_TILE * K_TILE
+        meas = {(tuple(p[1]), p[2], p[3]): p[0] for p in r["plans"]}
+        best = r["plans"][0][0]
+        st = len(feats)
+        for tile, S, rp in candidates(M, N, Kp):
+            f = _features(tile, M, N, Kp, S, rp)
+            f["meas"] = meas.get((tuple(tile), S, int(rp)), float("nan"))
+            feats.append(f)
+        segs.append((st, len(feats), best, BENCH_WEIGHT if tuple(r["shape"]) in BENCH else 1.0))
+    F = {k: np.array([f[k] for f in feats], dtype=float) for k in feats[0]}
+    for k in ("wide", "repack", "split"):
+        F[k] = F[k] > 0
+    has = ~np.isnan(F["meas"])
+    logm = np.log(np.where(has, F["meas"], 1.0))
+    regw = np.zeros(len(feats))
+    for st, en, best, w in segs:
+        regw[st:en] = np.where(F["meas"][st:en] < NEAR * best, 1.0, FAR_WEIGHT) * w
+    regw = regw * has
 
-    def loss(x):
+    def consts(x):
         c = dict(zip(names, np.abs(x)))
         c.update(FIXED)
-        s = 0.0
-        for r in recs:
-            M, N, K = r["shape"]
-            Kp = (K + K_TILE - 1) // K_TILE * K_TILE
-            best = r["plans"][0][0]
-            for us, tile, S, rp in r["plans"]:
-                w = 1.0 if us < NEAR * best else FAR_WEIGHT
-                s += w * (math.log(plan_time_us(c, tile, M, N, Kp, S, rp)) - math.log(us)) ** 2
-        return s
+        return c
 
-    x0 = np.array([start[n] for n in names])
-    res = minimize(loss, x0, method="Nelder-Mead",
-                   options={"maxiter": 40000, "xatol": 1e-7, "fatol": 1e-9})
-    c = dict(zip(names, [float(v) for v in np.abs(res.x)]))
-    c.update(FIXED)
-    return c, float(res.fun)
+    def reg_loss(x):
+        d = np.log(np.maximum(_time(consts(x), F, np), 1e-9)) - logm
+        return float(np.sum(regw * d * d))
+
+    def total(x):
+        t = _time(consts(x), F, np)
+        s = 0.0
+        for st, en, best, w in segs:
+            tt = t[st:en]
+            bi = 0
+            while True:
+                later = np.nonzero(tt[bi + 1:] < tt[bi] * (1.0 - PLAN_MIN_GAIN))[0]
+                if len(later) == 0:
+                    break
+                bi += 1 + int(later[0])
+            m = F["meas"][st + bi]
+            s += w * math.log(m / best if m == m else UNMEASURED)
+        d = np.log(np.maximum(t, 1e-9)) - logm
+        return s + REG_WEIGHT * float(np.sum(regw * d * d))
+
+    x = np.array([start[n] for n in names])
+    x = minimize(reg_loss, x, method="Nelder-Mead",
+                 options={"maxiter": 20000, "xatol": 1e-8, "fatol": 1e-10}).x
+    best_x, best_f = x, total(x)
+    rng = np.random.default_rng(seed)
+    for k in range(restarts):
+        x0 = best_x * (1 + 0.1 * rng.standard_normal(len(best_x))) if k else best_x
+        r = minimize(total, x0, method="Nelder-Mead",
+                     options={"maxiter": 6000, "xatol": 1e-9, "fatol": 1e-12})
+        if r.fun < best_f:
+            best_x, best_f = r.x, r.fun
+    return consts(best_x), float(best_f)
 
 
 def evaluate(c, recs):
-    """Measured time of the model's pick / measured best, per shape whose pick was measured."""
+    """Measured time of the model's pick / measured best, per shape (nan: the pick was not
+    measured)."""
     out = []
     for r in recs:
         M, N, K = r["shape"]
         Kp = (K + K_TILE - 1) // K_TILE * K_TILE
         tile, S, rp = best_plan(c, M, N, Kp)
         meas = [p[0] for p in r["plans"] if tuple(p[1]) == tile and p[2] == S and p[3] == int(rp)]
-        if meas:
-            out.append((tuple(r["shape"]), meas[0] / r["plans"][0][0]))
+        out.append((tuple(r["shape"]), meas[0] / r["plans"][0][0] if meas else float("nan")))
     return out
 
 
 def main():
     paths = sys.argv[1:] or [os.path.join(HERE, "plans_mi355x.jsonl")]
-    recs = load(paths)
+    recs = load([p for p in paths if p != "--no-fit"] or [os.path.join(HERE, "plans_mi355x.jsonl")])
     # the constants are fitted on the shapes with M % 128 == 0 (every tile measured on them)
     fit_recs = [r for r in recs if r["shape"][0] % 128 == 0]
-    c, l = fit(fit_recs, CONSTANTS)
-    print("fitted constants (log-time loss %.3f over %d shapes):" % (l, len(fit_recs)))
-    for n in NAMES:
-        print(f"  {n:14s} {c[n]:.6g}")
+    if "--no-fit" in sys.argv:
+        c = CONSTANTS
+    else:
+        fit_recs = [r for r in recs if r["shape"][0] % 128 == 0]
+        c, l = fit(fit_recs, CONSTANTS)
+        print("fitted constants (objective %.3f over %d shapes):" % (l, len(fit_recs)))
+        for n in NAMES:
+            print(f"  {n:20s} {c[n]:.6g}")
     for label, sel in (("M % 128 == 0", lambda s: s[0] % 128 == 0),
-                       ("skinny M", lambda s: s[0] % 128 != 0)):
+                       ("skinny M or ragged", lambda s: s[0] % 128 != 0)):
         ev = [(s, g) for s, g in evaluate(c, recs) if sel(s)]
-        if ev:
-            gm = math.exp(sum(math.log(g) for _, g in ev) / len(ev))
-            print(f"{label}: picks measured for {len(ev)} shapes: geomean {gm:.3f}x of the best, "
-                  f"worst {max(g for _, g in ev):.3f}x")
+        meas = [g for _, g in ev if g == g]
+        if meas:
+            gm = math.exp(sum(math.log(g) for g in meas) / len(meas))
+            print(f"{label}: {len(ev)} shapes, picks measured for {len(meas)}: geomean "
+                  f"{gm:.3f}x of the best, worst {max(meas):.3f}x")
+    for s, g in evaluate(c, recs):
+        if s in BENCH:
+            print(f"  benchmark {s}: pick {best_plan(c, s[0], s[1], (s[2] + K_TILE - 1) // K_TILE * K_TILE)}"
+                  f" at {g:.3f}x of the best")
 
 
 if __name__ == "__main__":

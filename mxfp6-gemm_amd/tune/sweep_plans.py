@@ -7,6 +7,10 @@ warm-ups. One JSON line per shape: {"shape": [M, N, K], "plans": [[us, tile, S, 
 sorted by time.
 
   python mxfp6-gemm_amd/tune/sweep_plans.py 2048x2048x2048,8192x8192x8192 out.jsonl
+  python mxfp6-gemm_amd/tune/sweep_plans.py SHAPES out.jsonl --tiles 128x512x4x4
+      (only the plans of the listed tiles)
+  python mxfp6-gemm_amd/tune/sweep_plans.py --merge base.jsonl new.jsonl merged.jsonl
+      (each shape of base with the plans of the tiles measured in new replaced by new's)
 """
 import json
 import os
@@ -39,14 +43,14 @@ def best_us(fn, reps=3, n=20, warm=5):
     return best * 1e3
 
 
-def sweep(M, N, K):
+def sweep(M, N, K, tiles=TILES):
     p = mx.make_problem(M, N, K, seed=7)
     kt = p.Kp // mx.K_TILE
     dA = torch.from_numpy(p.a_packed).cuda()
     D = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
     res = []
     regular = M % 32 == 0 and N % 128 == 0
-    for t in TILES:
+    for t in tiles:
         # the plans the router considers: on a regular shape (M % 32 == 0, N % 128 == 0) the
         # tiles whose MT divides M, N masked when NT does not divide it; on a ragged shape every
         # tile. The skinny tiles (fewer than 128 rows) are measured on M % 128 == 0 shapes only
@@ -76,11 +80,34 @@ def sweep(M, N, K):
     return {"shape": [M, N, K], "plans": [list(r) for r in res]}
 
 
+def merge(base_path, new_path, out_path):
+    new = {}
+    for line in open(new_path):
+        rec = json.loads(line)
+        new[tuple(rec["shape"])] = rec["plans"]
+    with open(out_path, "w") as out:
+        for line in open(base_path):
+            rec = json.loads(line)
+            plans = new.get(tuple(rec["shape"]))
+            if plans is not None:
+                tiles = {tuple(pl[1]) for pl in plans}
+                rec["plans"] = sorted([pl for pl in rec["plans"] if tuple(pl[1]) not in tiles] +
+                                      plans)
+            out.write(json.dumps(rec) + "\n")
+
+
 def main():
+    if sys.argv[1] == "--merge":
+        merge(*sys.argv[2:5])
+        return
     shapes = [tuple(int(v) for v in s.split("x")) for s in sys.argv[1].split(",")]
+    tiles = TILES
+    if "--tiles" in sys.argv:
+        tiles = [tuple(int(v) for v in t.split("x"))
+                 for t in sys.argv[sys.argv.index("--tiles") + 1].split(",")]
     with open(sys.argv[2], "a") as out:
         for M, N, K in shapes:
-            rec = sweep(M, N, K)
+            rec = sweep(M, N, K, tiles)
             best = rec["plans"][0]
             print(f"{M}x{N}x{K}: best {best[0]:.1f} us tile {tuple(best[1])} S {best[2]} "
                   f"a_layout {best[3]} ({len(rec['plans'])} plans)", flush=True)

@@ -17,7 +17,7 @@ with open(os.path.join(GOLD, "ref_routing.json")) as f:
     REF = json.load(f)
 
 IMPLEMENTED = {(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3), (256, 256, 4, 4),
-               (256, 192, 4, 3)}
+               (256, 192, 4, 3), (128, 512, 4, 4)}
 SKINNY = {(64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)}
 
 
@@ -121,12 +121,12 @@ def test_router_degenerate_shapes_do_not_trap(mx):
 
 def test_router_benchmark_shapes(mx):
     # The plan-time model's picks for the five benchmark workloads; each is the fastest of all
-    # plans (tile x 1..16 segments x A layout) measured on MI355X for that shape.
+    # plans (tile x split choice x A layout) measured on MI355X for that shape.
     want = {
         (256, 256, 1024): ((32, 128, 1, 1), 1),
         (8192, 8192, 8192): ((256, 256, 4, 4), 1),
         (2048, 6144, 16128): ((256, 192, 4, 3), 1),
-        (2048, 1024, 105728): ((256, 256, 4, 4), 8),
+        (2048, 1024, 105728): ((128, 512, 4, 4), 8),   # 163.8 us vs 194.1 on 256x256
         (2048, 5120, 105728): ((256, 256, 4, 4), 3),
     }
     for (M, N, K), exp in want.items():
@@ -150,10 +150,11 @@ def test_router_small_k_plans(mx):
         (1024, 1024, 1024): ((32, 128, 1, 1), 1, False),   # 6.8 us vs 7.3
         (2048, 1024, 1024): ((64, 128, 2, 1), 1, False),   # 7.8 us vs 8.1
         (2048, 256, 2048): ((32, 128, 1, 1), 1, False),    # 8.7 us vs 9.8 (no split)
-        (4096, 4096, 1024): ((256, 256, 4, 4), 1, False),  # 22.7 us vs 27.5 with a repack
-        (2048, 4096, 1024): ((128, 256, 2, 4), 1, False),  # 14.3 us vs 17.9
-        (4096, 2048, 2048): ((128, 256, 2, 4), 1, False),  # 20.8 us vs 26.5
-        (8192, 8192, 2048): ((256, 256, 4, 4), 1, True),   # 117.7 us vs 122.0 unrepacked
+        (4096, 4096, 1024): ((128, 512, 4, 4), 1, False),  # 19.8 us vs 22.7 on 256x256
+        (2048, 4096, 1024): ((128, 256, 2, 4), 1, False),  # 14.3 us vs 16.6 on 128x512
+        (4096, 2048, 2048): ((128, 256, 2, 4), 1, False),  # 20.8 us vs 22.8 on 128x512
+        (6144, 2048, 2048): ((128, 512, 4, 4), 1, False),  # 24.7 us vs 29.1 on 256x256
+        (3072, 3072, 3072): ((128, 512, 4, 4), 1, False),  # 29.7 us vs 34.3 on 128x384
     }
     for (M, N, K), (tile, S, rp) in want.items():
         Kp = _kpad(K)
@@ -165,8 +166,8 @@ def test_router_small_k_plans(mx):
 def test_router_equals_the_tuning_model(mx):
     """The Python model in mxfp6-gemm_amd/tune (the one the constants are fitted with) and the
     library's router make the same choice on every shape of the recorded plan measurements and
-    on a grid of other shapes; and with the committed constants its picks are within 3% of the
-    measured best on average."""
+    on a grid of other shapes; and with the committed constants every pick was measured and the
+    picks are within 3% of the measured best on average."""
     import math
     import os
     import sys
@@ -183,6 +184,7 @@ def test_router_equals_the_tuning_model(mx):
         got = (tuple(mx.choose_tile(M, N, Kp)), mx.splitk_segments(M, N, Kp), mx.repacks_a(M, N, Kp))
         assert got == (tile, S, rp), (M, N, K, got, (tile, S, rp))
     ev = pm.evaluate(pm.CONSTANTS, recs)
+    assert all(g == g for _, g in ev), [s for s, g in ev if g != g]
     big = [g for s, g in ev if s[0] % 128 == 0 and s[1] % 128 == 0]
     skinny = [g for s, g in ev if s[0] % 128 != 0 and s[0] % 32 == 0 and s[1] % 128 == 0]
     ragged = [g for s, g in ev if s[0] % 32 != 0 or s[1] % 128 != 0]
@@ -220,7 +222,7 @@ def test_router_skinny_m(mx):
 
 
 def test_router_ragged_shapes(mx):
-    """M not a multiple of 32 or N not a multiple of 128: any of the nine tiles, the partial
+    """M not a multiple of 32 or N not a multiple of 128: any of the ten tiles, the partial
     last tile row / column masked; the plan covers the shape with ceil(M/MT) x ceil(N/NT)
     workgroups, splits keep >= 1 K-tile per segment, the repacked A holds whole 32-row blocks,
     and the router agrees with the tuning model."""

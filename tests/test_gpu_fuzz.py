@@ -25,14 +25,16 @@ GUARD = 4096
 
 
 # shapes that reach the routes random small shapes rarely do (the router's pick in the comment)
-ROUTES = [(8192, 4096, 4096),   # 256x256, A repacked
-          (2048, 6144, 4096),   # 256x192, A repacked
-          (3072, 3072, 3072),   # 128x384
-          (2048, 1024, 16384),  # 128x256, 4 K segments
-          (1024, 2432, 32768),  # 256x256 over a masked last column, 6 segments, whole segments per XCD
+ROUTES = [(2816, 3072, 1024),   # 128x512
+          (2816, 896, 8192),    # 128x512 over a masked last column, 4 K segments
+          (6016, 10880, 2048),  # 128x512, A repacked, masked last column
+          (3328, 9856, 1024),   # 256x256, A repacked, masked last column
+          (5120, 6528, 1024),   # 256x192, A repacked
+          (4736, 3456, 1024),   # 128x384
+          (1408, 1536, 8192),   # 128x256, 3 K segments
+          (7168, 640, 8192),    # 256x256 over a masked last column, 3 segments, whole segments per XCD
           (2048, 2048, 2048),   # 128x128
-          (2047, 1000, 4096),   # ragged, 64x128
-          (4096, 1152, 32768)]  # 256x256, 3 segments, whole segments per XCD
+          (2047, 1000, 4096)]   # ragged, 64x128
 
 
 def _shapes(n=24, seed=20261201):

@@ -50,7 +50,7 @@ def test_routed_small_shapes(g, orc, out_type, M, N, K):
 
 @pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
                                   (256, 256, 4, 4), (256, 256, 2, 4),
-                                  (256, 192, 4, 3)])
+                                  (256, 192, 4, 3), (128, 512, 4, 4)])
 @pytest.mark.parametrize("out_type", [0, 1, 2])
 def test_forced_tiles(g, orc, tile, out_type):
     M, N, K = 256, 768, 960  # K-tail: kpad(960) = 1152
@@ -190,7 +190,7 @@ def test_preshuffled_a_input(g):
 def test_routed_repack_and_fallback(g, orc):
     """A shape the router repacks A for: full workspace (repack) and none (row-major A) give
     the same bits and pass the oracle."""
-    M, N, K = 768, 6144, 8192   # among the smallest shapes the router repacks A for
+    M, N, K = 640, 3584, 4096   # among the smallest shapes the router repacks A for
     p = mx.make_problem(M, N, K, seed=23)
     assert mx.repacks_a(M, N, p.Kp)
     dp = g.DevProblem(p, mx.choose_tile(M, N, p.Kp))
