@@ -346,7 +346,7 @@ def headline(name, steps, warmup, ref):
     tflops = w.flops / (ms * 1e-3) / 1e12
 
     # dominant kernel: the same launches issued one by one, HIP events around the tile kernel
-    kernel_name = "slab_kernel"
+    kernel_name = "wide_kernel" if tuple(w.tile[:2]) == (128, 512) else "slab_kernel"
     if w.S == 1 and w.repack:
         ash = torch.empty(mx.preshuffled_bytes(M, p.Kp), dtype=torch.uint8, device="cuda:0")
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
