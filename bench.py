@@ -2,8 +2,8 @@
 MFMA peak.
 
 A step is one mxfp6_gemm_async call: the whole hot path the router picks for the shape (for the
-default workload: the repack of A into the preshuffled layout, then the 256x256 tile kernel),
-over operands already resident in HBM, with the plan's whole workspace
+default workload: one launch of the 256x256 tile kernel with four waves side by side, reading
+row-major A), over operands already resident in HBM, with the plan's whole workspace
 (mxfp6_gemm_preferred_workspace_size). Default workload: M = N = K = 8192, FP16 out, A and B
 drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX rule.
 
@@ -73,6 +73,9 @@ CONFIGS = {
            (mx.DIST_STUDENT_T3, 1.0), "A,B ~ Student-t(3)"),
 }
 PROFILES = os.path.join(ROOT, "profiles")
+# the tiles run by wide_kernel (four waves side by side, B loaded into registers); the others by
+# slab_kernel
+WIDE_TILES = {(128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2)}
 METRIC = "MXFP6 GEMM TFLOPs (FP16 out) and % of MXFP6 MFMA peak, 1xMI355X"
 
 
@@ -346,7 +349,7 @@ def headline(name, steps, warmup, ref):
     tflops = w.flops / (ms * 1e-3) / 1e12
 
     # dominant kernel: the same launches issued one by one, HIP events around the tile kernel
-    kernel_name = "wide_kernel" if tuple(w.tile[:2]) == (128, 512) else "slab_kernel"
+    kernel_name = "wide_kernel" if tuple(w.tile) in WIDE_TILES else "slab_kernel"
     if w.S == 1 and w.repack:
         ash = torch.empty(mx.preshuffled_bytes(M, p.Kp), dtype=torch.uint8, device="cuda:0")
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))

@@ -385,14 +385,14 @@ int slab_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     return e == hipSuccess ? 0 : 2;
 }
 
-// The wide tile (128 x 512, B straight to registers): the A repack first when asked, MASK when
-// the tile does not divide M x N. Three LDS chunk buffers, XCD groups of 8 tile rows (4 buffers
-// and groups of 4 or 16 rows measured within run-to-run noise on 8192^3, 2048x1024x105728 and
-// 2048x6144x16128).
-constexpr int WIDE_NB = 3, WIDE_XG = 8;
-template <int NB, int XG, typename KT, bool SPLIT>
+// The wide tiles (four waves side by side, B straight to registers): the A repack first when
+// asked, MASK when the tile does not divide M x N. Three LDS chunk buffers; XCD groups of 8 tile
+// rows for the 128-row tiles (4 buffers and groups of 4 or 16 rows measured within run-to-run
+// noise on 8192^3, 2048x1024x105728 and 2048x6144x16128 for 128 x 512), 4 for 256 x 256.
+constexpr int WIDE_NB = 3;
+template <int MB, int NPW, int XG, typename KT, bool SPLIT>
 int wide_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
-    using G = WideGeom<NB>;
+    using G = WideGeom<MB, NPW, WIDE_NB>;
     static_assert(G::LDS <= 160 * 1024, "LDS budget");
     const bool mask = d->M % G::MT != 0 || d->N % G::NT != 0;
     const uint8_t* A = static_cast<const uint8_t*>(d->A);
@@ -404,11 +404,11 @@ int wide_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     }
     hipError_t e;
     if (d->a_layout == MXFP6_A_ROWS)
-        e = mask ? wide_kernel_launch<NB, XG, KT, SPLIT, false, true>(d, A, st)
-                 : wide_kernel_launch<NB, XG, KT, SPLIT, false, false>(d, A, st);
+        e = mask ? wide_kernel_launch<MB, NPW, WIDE_NB, XG, KT, SPLIT, false, true>(d, A, st)
+                 : wide_kernel_launch<MB, NPW, WIDE_NB, XG, KT, SPLIT, false, false>(d, A, st);
     else
-        e = mask ? wide_kernel_launch<NB, XG, KT, SPLIT, true, true>(d, A, st)
-                 : wide_kernel_launch<NB, XG, KT, SPLIT, true, false>(d, A, st);
+        e = mask ? wide_kernel_launch<MB, NPW, WIDE_NB, XG, KT, SPLIT, true, true>(d, A, st)
+                 : wide_kernel_launch<MB, NPW, WIDE_NB, XG, KT, SPLIT, true, false>(d, A, st);
     return e == hipSuccess ? 0 : 2;
 }
 
@@ -417,7 +417,10 @@ int wide_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
 template <typename KT, bool SPLIT>
 int slab_run(const mxfp6_launch_desc* d, hipStream_t st) {
     if (!tile_supported(d->MT, d->NT, d->mpw, d->npw)) return 1;
-    if (d->MT == 128 && d->NT == 512) return wide_launch_t<WIDE_NB, WIDE_XG, KT, SPLIT>(d, st);
+    // wide tiles: four waves side by side (TileChoice MPW 4 = the A scale group)
+    if (d->MT == 128 && d->NT == 512) return wide_launch_t<4, 4, 8, KT, SPLIT>(d, st);
+    if (d->MT == 128 && d->NT == 256 && d->mpw == 4) return wide_launch_t<4, 2, 8, KT, SPLIT>(d, st);
+    if (d->MT == 256 && d->NT == 256 && d->npw == 2) return wide_launch_t<8, 2, 4, KT, SPLIT>(d, st);
     // skinny tiles: one wave row, four wave columns, a deeper ring
     if (d->MT == 32 && d->NT == 128) return slab_launch_t<32, 128, 1, 4, 4, 8, KT, SPLIT>(d, st);
     if (d->MT == 32 && d->NT == 256) return slab_launch_t<32, 256, 1, 4, 4, 8, KT, SPLIT>(d, st);

@@ -19,6 +19,8 @@ inline bool tile_supported(int MT, int NT, int mpw, int npw) {
            (MT == 128 && NT == 256 && mpw == 2 && npw == 4) ||
            (MT == 128 && NT == 384 && mpw == 4 && npw == 3) ||
            (MT == 128 && NT == 512 && mpw == 4 && npw == 4) ||
+           (MT == 128 && NT == 256 && mpw == 4 && npw == 2) ||
+           (MT == 256 && NT == 256 && mpw == 4 && npw == 2) ||
            (MT == 256 && NT == 256 && mpw == 4 && npw == 4) ||
            (MT == 256 && NT == 192 && mpw == 4 && npw == 3) ||
            (MT == 256 && NT == 256 && mpw == 2 && npw == 4);

@@ -1,25 +1,31 @@
-// Wide tile kernel of libmxfp6gemm for gfx950: a 128 x 512 tile of D, four waves side by side.
+// Wide tile kernels of libmxfp6gemm for gfx950: four waves side by side, B straight into registers.
 //
-// Wave w owns all 128 rows and columns [128 w, 128 w + 128) of the tile: MPW = NPW = 4 blocks of
-// 32, sixteen 32x32 FP32 accumulators in AGPRs, fed by v_mfma_scale_f32_32x32x64_f8f6f4 (FP6
-// E2M3 x FP6 E2M3 with per-lane E8M0 scales). No B block is needed by two waves, so
+// A workgroup computes an MT x NT tile of D with MT = 32 MB and NT = 4 * 32 NPW; wave w owns all
+// MT rows and columns [32 NPW w, 32 NPW (w + 1)) of the tile: MB x NPW blocks of 32x32, FP32
+// accumulators in AGPRs, fed by v_mfma_scale_f32_32x32x64_f8f6f4 (FP6 E2M3 x FP6 E2M3 with per-lane
+// E8M0 scales). Three shapes are built:
+//   128 x 512 (MB 4, NPW 4), 128 x 256 (MB 4, NPW 2) and 256 x 256 (MB 8, NPW 2; A scales in two
+//   groups of four 32-row blocks).
+// No B block is needed by two waves, so
 //   B  streams straight from the preshuffled layout into the wave's MFMA operand registers: per
 //      64-wide K slab and block, one 16-byte load (lane t: bytes 16t) and one 8-byte load (bytes
 //      1024 + 8t) of the block's 1536-byte tile, each a contiguous piece of memory. The operands
 //      sit in a ring of three register slots; slot s holds slab 3c + s of K-tile c, and the loads
 //      of slab q + 3 are issued during slab q, a block's two loads right after the last MFMA that
 //      reads the block. The scales (tiled layout: a lane's three slab dwords of a K-tile are
-//      contiguous) come one K-tile ahead, one 12-byte load per operand at the start of K-tile c for
-//      K-tile c + 1, into registers moved to the current set when K-tile c ends.
-//   A  (the 128 rows, needed by every wave) is staged in LDS one K-tile at a time: a chunk holds,
+//      contiguous) come one K-tile ahead, one 12-byte load per scale group at the start of K-tile
+//      c for K-tile c + 1, into registers moved to the current set when K-tile c ends.
+//   A  (the MT rows, needed by every wave) is staged in LDS one K-tile at a time: a chunk holds,
 //      per row, the K-tile's 144 contiguous bytes of the row-major operand (or, for A repacked
 //      into the preshuffled layout, the K-tile's three 1536-byte tiles of each 32-row block),
-//      18 KiB, copied with direct-to-LDS 16-byte loads (global_load_lds_dwordx4). A row's 144
-//      bytes take 2-3 cache lines where a 64-wide slab copy of 48 bytes takes 1-2 per slab, so
+//      MT x 144 bytes, copied with direct-to-LDS 16-byte loads (global_load_lds_dwordx4). A row's
+//      144 bytes take 2-3 cache lines where a 64-wide slab copy of 48 bytes takes 1-2 per slab, so
 //      row-major A costs about half the L2 requests of a per-slab copy. Chunks go through a ring
-//      of NB LDS buffers: chunk c + NB - 1 is copied during K-tile c (5 copy instructions per wave:
-//      18 KiB is 18 wave copies, two dummies keep the count uniform), and a wave reads each slab's
-//      four A operand blocks during the previous slab into one of three register sets.
+//      of NB LDS buffers: chunk c + NB - 1 is copied during K-tile c (the wave's copies spread over
+//      the K-tile's three slabs; a chunk of 128 rows is 18 wave copies, two dummies keep the count
+//      per wave uniform), and a wave reads each slab's A operand blocks during the previous slab
+//      into a register set: three sets (one per slab of a K-tile) for MB 4, two alternating sets
+//      for MB 8 (the K loop then runs K-tiles in pairs).
 // One workgroup barrier per K-tile, at the start of its last slab: before it, each wave waits for
 // its own copies of the next chunk (vmcnt, exact: the issue order is static) and for its LDS reads
 // (lgkmcnt(0)); after it the next chunk is complete for every wave and the chunk read before the
@@ -30,6 +36,8 @@
 // of the last tile row and column and masks the stores, as in the slab kernel.
 #pragma once
 
+#include <type_traits>
+
 #include "../hip_layer.h"
 #include "device_common.hpp"
 #include "epilogue.hpp"
@@ -37,44 +45,82 @@
 
 namespace mxfp6_dev {
 
-// Vector-memory instructions a wave of the wide kernel issues per slab s of a K-tile, in order:
-// after MFMA 0 of slab 0: the two scale loads of the next K-tile; after MFMA 1: a copy; after
-// MFMA 3: 2 B loads; after MFMA 5: a copy (s < 2); after MFMAs 7, 11 and 15: 2 B loads each.
-constexpr int wide_copies_in_slab(int s) { return s < 2 ? 2 : 1; }
-constexpr int wide_ops_in_slab(int s) { return (s == 0 ? 2 : 0) + 8 + wide_copies_in_slab(s); }
-constexpr int wide_ops_in_ktile() { return wide_ops_in_slab(0) + wide_ops_in_slab(1) + wide_ops_in_slab(2); }
-
-template <int NB_>
+// Static schedule of one wave in slab s (0..2) of a K-tile. In the order a step issues them:
+// MFMA k; (s = 0, k = 0) the scale loads of the next K-tile; the slab's next A copy when k is a
+// copy position; the two loads of B block k / MB when MFMA k was its last use in the slab
+// (k % MB == MB - 1); the LDS read of an A block of the next slab when k is a read position.
+template <int MB_, int NPW_, int NB_>
 struct WideGeom {
-    static constexpr int MT = 128, NT = 512, MPW = 4, NPW = 4, NWAVES = 4, THREADS = 256;
-    static constexpr int NB = NB_;                               // LDS chunk buffers
-    static constexpr int CHUNK = MT * SUBS * SLAB_BYTES;         // 18432: one K-tile of A
-    static constexpr int COPIES = CHUNK / 1024;                  // 18 wave copies of 1 KiB
-    static constexpr int A_ISS = (COPIES + NWAVES - 1) / NWAVES; // 5 per wave per chunk
+    static constexpr int MB = MB_, NPW = NPW_, NB = NB_;
+    static constexpr int MT = 32 * MB, NT = 4 * 32 * NPW, NWAVES = 4, THREADS = 256;
+    static constexpr int GA = MB < 4 ? MB : 4;                   // A scale group (blocks)
+    static constexpr int NGA = MB / GA;                          // A scale groups per tile
+    static constexpr int NMF = MB * NPW;                         // MFMAs per wave per slab
+    static constexpr int NSET = MB <= 4 ? 3 : 2;                 // A operand register sets
+    static constexpr int CHUNK = MT * SUBS * SLAB_BYTES;         // one K-tile of A
+    static constexpr int COPIES = CHUNK / 1024;                  // wave copies of 1 KiB
+    static constexpr int A_ISS = (COPIES + NWAVES - 1) / NWAVES; // copies per wave per chunk
     static constexpr int LDS = NB * CHUNK + 1024;                // + dummy sink
+    // copies of slab s, and the MFMA after which copy j of a slab is issued
+    static constexpr int cps(int s) { return A_ISS / SUBS + (s < A_ISS % SUBS ? 1 : 0); }
+    static constexpr int CSTEP = cps(0) <= 2 ? NMF / 4 : NMF / cps(0);
+    static constexpr int copy_k(int j) { return 1 + j * CSTEP; }
+    static constexpr bool b_load_at(int k) { return k % MB == MB - 1; }
+    // MFMA after which the read of A block i of the next slab is issued
+    static constexpr int read_k(int i) { return NSET == 3 ? NMF / 2 + i : i * (NMF / MB); }
+    static constexpr int ops_in_slab(int s) { return (s == 0 ? NGA + 1 : 0) + cps(s) + 2 * NPW; }
+    static constexpr int ops_in_ktile() { return ops_in_slab(0) + ops_in_slab(1) + ops_in_slab(2); }
+    static constexpr int b_ops_from(int k0) {
+        int n = 0;
+        for (int k = k0; k < NMF; k++) n += b_load_at(k) ? 2 : 0;
+        return n;
+    }
     // Before the barrier at the start of slab 2 of K-tile c, the wave's copies of chunk c + 1
-    // (issued during K-tile c + 2 - NB, the last one after MFMA 1 of its slab 2) must have
-    // landed; issued after that copy: the 8 B loads of the rest of that slab, NB - 3 whole
-    // K-tiles, and slabs 0 and 1 of K-tile c.
-    static constexpr int CHUNK_WAIT =
-        8 + (NB - 3) * wide_ops_in_ktile() + wide_ops_in_slab(0) + wide_ops_in_slab(1);
-    // In the prologue: after chunk 0's copies, those of chunks 1 .. NB - 2, the 2 scale loads of
-    // K-tile 0 and the 24 B loads of its three slabs.
-    static constexpr int PRO_WAIT = (NB - 2) * A_ISS + 2 + SUBS * 2 * NPW;
-    static_assert(NB >= 3, "a chunk is read for a K-tile after its copies were issued");
-    static_assert(A_ISS == wide_copies_in_slab(0) + wide_copies_in_slab(1) + wide_copies_in_slab(2),
-                  "copies");
+    // (issued during K-tile c + 2 - NB, the last one in its slab 2) must have landed; issued
+    // after that copy: the B loads of the rest of that slab, NB - 3 whole K-tiles, and slabs 0
+    // and 1 of K-tile c.
+    static constexpr int CHUNK_WAIT = b_ops_from(copy_k(cps(2) - 1)) + (NB - 3) * ops_in_ktile() +
+                                      ops_in_slab(0) + ops_in_slab(1);
+    // In the prologue: after chunk 0's copies, those of chunks 1 .. NB - 2, the scale loads of
+    // K-tile 0 and the B loads of its three slabs.
+    static constexpr int PRO_WAIT = (NB - 2) * A_ISS + NGA + 1 + SUBS * 2 * NPW;
+    static_assert(MB == 4 || MB == 8, "128 or 256 rows");
+    static_assert(NPW >= 1 && NPW <= 4, "B scale group holds <= 4 blocks");
+    // NB = 3: the prologue issues chunk 1 before the loop, and the count above then holds for
+    // it too (more loads follow chunk 1 in the prologue than in the loop)
+    static_assert(NB == 3, "three chunk buffers");
+    static_assert(cps(0) + cps(1) + cps(2) == A_ISS && cps(2) >= 1, "copies per K-tile");
+    static_assert(copy_k(cps(0) - 1) < NMF, "copy positions");
+    static_assert(read_k(MB - 1) < NMF, "read positions");
     static_assert(CHUNK_WAIT <= 63 && PRO_WAIT <= 63, "vmcnt range");
 };
 
-template <int NB_, int XG, typename OutT, bool SPLIT, bool ASH, bool MASK>
+// acc[mi][ni] += A(mi) * B(ni) with the scale bytes mi % 4 of sa and ni of sb (op_sel must be a
+// constant: mi and ni are known at compile time wherever this is called from an unrolled loop).
+template <int MB, int NPW>
+__device__ __forceinline__ void wide_mfma(v16f (&acc)[MB][NPW], int mi, int ni, const v8i& a,
+                                          const v8i& b, int sa, int sb) {
+    switch (mi * 4 + ni) {
+#define WX_CASE(I, J)                                                                   \
+    case I * 4 + J:                                                                     \
+        if constexpr (I < MB && J < NPW) acc[I][J] = mfma_fp6<I % 4, J>(acc[I][J], a, b, sa, sb); \
+        break;
+#define WX_ROW(I) WX_CASE(I, 0) WX_CASE(I, 1) WX_CASE(I, 2) WX_CASE(I, 3)
+        WX_ROW(0) WX_ROW(1) WX_ROW(2) WX_ROW(3) WX_ROW(4) WX_ROW(5) WX_ROW(6) WX_ROW(7)
+#undef WX_ROW
+#undef WX_CASE
+    }
+}
+
+template <int MB_, int NPW_, int NB_, int XG, typename OutT, bool SPLIT, bool ASH, bool MASK>
 __global__ void __launch_bounds__(256, 1)
     wide_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
                 OutT* __restrict__ D, float* __restrict__ ws, int M, int N, int Kp,
                 int A_row_bytes, int S) {
-    using G = WideGeom<NB_>;
-    constexpr int MT = G::MT, NT = G::NT, MPW = G::MPW, NPW = G::NPW, NB = G::NB;
+    using G = WideGeom<MB_, NPW_, NB_>;
+    constexpr int MT = G::MT, NT = G::NT, MB = G::MB, NPW = G::NPW, NB = G::NB;
+    constexpr int NGA = G::NGA, GA = G::GA, NSET = G::NSET, NMF = G::NMF;
     constexpr int CHUNK = G::CHUNK;
     __shared__ __attribute__((aligned(1024))) char lds[G::LDS];
 
@@ -130,7 +176,7 @@ __global__ void __launch_bounds__(256, 1)
 
     // ---- B operand and scale loads of this wave
     const int b_blk_last = (N + 31) / 32 - 1;
-    const int sa_grp_last = ((M + 31) / 32 + MPW - 1) / MPW - 1;
+    const int sa_grp_last = ((M + 31) / 32 + GA - 1) / GA - 1;
     const int sb_grp_last = ((N + 31) / 32 + NPW - 1) / NPW - 1;
     gbl_cptr b_col[NPW];
 #pragma unroll
@@ -139,10 +185,16 @@ __global__ void __launch_bounds__(256, 1)
         if (MASK) blk = min(blk, b_blk_last);
         b_col[ni] = opaque_gptr(Bsh + (size_t)blk * k64n * OPBLK_BYTES);
     }
-    int ga = wg_m, gb = wg_n * G::NWAVES + wave;
-    if (MASK) ga = min(ga, sa_grp_last), gb = min(gb, sb_grp_last);
-    // lane's scale dwords of K-tile 0 (the dword of slab s at + 4 s)
-    const gbl_cptr sa_lane = opaque_gptr(sA + (size_t)ga * k_tiles * 64 * 12) + lane * 12;
+    // lane's scale dwords of K-tile 0 (the dword of slab s at + 4 s), per A group and for B
+    gbl_cptr sa_lane[NGA];
+#pragma unroll
+    for (int g = 0; g < NGA; g++) {
+        int ga = wg_m * NGA + g;
+        if (MASK) ga = min(ga, sa_grp_last);
+        sa_lane[g] = opaque_gptr(sA + (size_t)ga * k_tiles * 64 * 12) + lane * 12;
+    }
+    int gb = wg_n * G::NWAVES + wave;
+    if (MASK) gb = min(gb, sb_grp_last);
     const gbl_cptr sb_lane = opaque_gptr(sB + (size_t)gb * k_tiles * 64 * 12) + lane * 12;
 
     // slab s of K-tile kt, block ni, into v
@@ -153,9 +205,11 @@ __global__ void __launch_bounds__(256, 1)
         const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
         v = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
     };
-    // the lane's three slab scale dwords of K-tile kt, for A and for B
-    auto load_scales = [&](v3i& a, v3i& b, int kt) {
-        a = *reinterpret_cast<__attribute__((address_space(1))) const v3i_a4*>(sa_lane + (size_t)kt * 768);
+    // the lane's three slab scale dwords of K-tile kt, for each A group and for B
+    auto load_scales = [&](v3i (&a)[NGA], v3i& b, int kt) {
+#pragma unroll
+        for (int g = 0; g < NGA; g++)
+            a[g] = *reinterpret_cast<__attribute__((address_space(1))) const v3i_a4*>(sa_lane[g] + (size_t)kt * 768);
         b = *reinterpret_cast<__attribute__((address_space(1))) const v3i_a4*>(sb_lane + (size_t)kt * 768);
     };
 
@@ -178,16 +232,16 @@ __global__ void __launch_bounds__(256, 1)
         }
     };
 
-    v16f acc[MPW][NPW];
+    v16f acc[MB][NPW];
 #pragma unroll
-    for (int i = 0; i < MPW; i++)
+    for (int i = 0; i < MB; i++)
 #pragma unroll
         for (int j = 0; j < NPW; j++) acc[i][j] = v16f{};
 
     v8i RB[SUBS][NPW];     // B operands, slot s = slab s of a K-tile
-    v8i RA[SUBS][MPW];     // A operands
-    v3i sc_a, sc_b;        // scale dwords of the current K-tile
-    v3i sn_a, sn_b;        // and of the next one
+    v8i RA[NSET][MB];      // A operands
+    v3i sc_a[NGA], sc_b;   // scale dwords of the current K-tile
+    v3i sn_a[NGA], sn_b;   // and of the next one
 
     // prologue: chunks 0 .. NB-2 in flight, then the scales of K-tile 0 and the B operands of its
     // three slabs, in the order the loop issues them (the compiler, which places the B waits,
@@ -211,10 +265,13 @@ __global__ void __launch_bounds__(256, 1)
     wait_vmcnt<G::PRO_WAIT>();  // chunk 0 landed
     ring_barrier();
 #pragma unroll
-    for (int mi = 0; mi < MPW; mi++) read_a(RA[0][mi], 0, 0, mi);
+    for (int mi = 0; mi < MB; mi++) read_a(RA[0][mi], 0, 0, mi);
 
     int buf = 0;  // LDS buffer of K-tile c's chunk
-    for (int c = 0; c < nkt; c++) {
+    // K-tile c; P: its parity in the two-set A rotation (slab s uses set (3 P + s) % 2), 0 with
+    // three sets (slab s uses set s)
+    auto ktile = [&](int c, auto par) {
+        constexpr int P = decltype(par)::value;
         const int nbuf = buf + 1 == NB ? 0 : buf + 1;            // chunk c + 1
         const int cbuf = buf == 0 ? NB - 1 : buf - 1;            // chunk c + NB - 1 (c - 1's)
         const int kt_copy = min(kt0 + c + NB - 1, kt_last);
@@ -228,55 +285,65 @@ __global__ void __launch_bounds__(256, 1)
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 ring_barrier();
             }
-            // slab s + 1 of this K-tile, or slab 0 of the next, goes to RA[(s + 1) % 3]
+            const int cur = NSET == 3 ? s : (3 * P + s) % 2;           // set of slab s
+            const int nxt = NSET == 3 ? (s + 1) % 3 : (3 * P + s + 1) % 2;  // of the next slab
+            // slab s + 1 of this K-tile, or slab 0 of the next, goes to RA[nxt]
             const int rbuf = s + 1 < SUBS ? buf : nbuf;
             const int rs = s + 1 < SUBS ? s + 1 : 0;
-            int ci = s == 0 ? 0 : s == 1 ? 2 : 4;  // first copy index of this slab
-            const int sa = s == 0 ? sc_a.x : s == 1 ? sc_a.y : sc_a.z;
-            const int sb = s == 0 ? sc_b.x : s == 1 ? sc_b.y : sc_b.z;
+            int ci = 0;  // copies of this slab so far
+            const int c0 = s == 0 ? 0 : s == 1 ? G::cps(0) : G::cps(0) + G::cps(1);
 #pragma unroll
-            for (int k = 0; k < MPW * NPW; k++) {
-                const int ni = k / MPW, mi = k % MPW;
-                switch (ni * 4 + mi) {
-#define WX_CASE(J, I)                                                                           \
-    case J * 4 + I:                                                                             \
-        acc[I][J] = mfma_fp6<I, J>(acc[I][J], RA[s][I], RB[s][J], sa, sb);                      \
-        break;
-                    WX_CASE(0, 0) WX_CASE(0, 1) WX_CASE(0, 2) WX_CASE(0, 3)
-                    WX_CASE(1, 0) WX_CASE(1, 1) WX_CASE(1, 2) WX_CASE(1, 3)
-                    WX_CASE(2, 0) WX_CASE(2, 1) WX_CASE(2, 2) WX_CASE(2, 3)
-                    WX_CASE(3, 0) WX_CASE(3, 1) WX_CASE(3, 2) WX_CASE(3, 3)
-#undef WX_CASE
-                }
+            for (int k = 0; k < NMF; k++) {
+                const int ni = k / MB, mi = k % MB;
+                const int g = mi / GA;
+                const int sa = s == 0 ? sc_a[g].x : s == 1 ? sc_a[g].y : sc_a[g].z;
+                const int sb = s == 0 ? sc_b.x : s == 1 ? sc_b.y : sc_b.z;
+                wide_mfma<MB, NPW>(acc, mi, ni, RA[cur][mi], RB[s][ni], sa, sb);
                 if (s == 0 && k == 0) load_scales(sn_a, sn_b, kt_next);
-                if ((k == 1 || k == 5) && ci < (s == 0 ? 2 : s == 1 ? 4 : 5)) a_copy(ci++, kt_copy, cbuf);
-                if (k % MPW == MPW - 1) load_b(RB[s][ni], ni, kt_next, s);
-                if (k >= 8 && k < 8 + MPW) read_a(RA[(s + 1) % SUBS][k - 8], rbuf, rs, k - 8);
+                if (ci < G::cps(s) && k == G::copy_k(ci)) {
+                    a_copy(c0 + ci, kt_copy, cbuf);
+                    ci++;
+                }
+                if (G::b_load_at(k)) load_b(RB[s][ni], ni, kt_next, s);
+#pragma unroll
+                for (int i = 0; i < MB; i++)
+                    if (k == G::read_k(i)) read_a(RA[nxt][i], rbuf, rs, i);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        sc_a = sn_a;
+#pragma unroll
+        for (int g = 0; g < NGA; g++) sc_a[g] = sn_a[g];
         sc_b = sn_b;
         buf = nbuf;
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    int c = 0;
+    if constexpr (NSET == 2) {
+        for (; c + 1 < nkt; c += 2) {
+            ktile(c, P0{});
+            ktile(c + 1, P1{});
+        }
     }
+    for (; c < nkt; c++) ktile(c, P0{});
 
     // epilogue (the clamped prefetches of the last K-tiles are drained first)
     wait_vmcnt0();
-    store_tile<MPW, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N, wg_m * MT + 4 * (lane >> 5),
-                                             wg_n * NT + wave * NPW * 32 + (lane & 31), lane,
-                                             wg_z);
+    store_tile<MB, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N, wg_m * MT + 4 * (lane >> 5),
+                                            wg_n * NT + wave * NPW * 32 + (lane & 31), lane,
+                                            wg_z);
 }
 
-// One launch of the wide kernel (grid ceil(M/128) x ceil(N/512) x splits, 256 threads).
-template <int NB, int XG, typename KT, bool SPLIT, bool ASH, bool MASK>
+// One launch of a wide kernel (grid ceil(M/MT) x ceil(N/NT) x splits, 256 threads).
+template <int MB, int NPW, int NB, int XG, typename KT, bool SPLIT, bool ASH, bool MASK>
 hipError_t wide_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipStream_t st) {
-    using G = WideGeom<NB>;
+    using G = WideGeom<MB, NPW, NB>;
     const dim3 grid((unsigned)((d->M + G::MT - 1) / G::MT), (unsigned)((d->N + G::NT - 1) / G::NT),
                     (unsigned)d->splits);
-    return launch_kernel(wide_kernel<NB, XG, KT, SPLIT, ASH, MASK>, grid, dim3(G::THREADS), st,
-                         A, static_cast<const uint8_t*>(d->Bsh), d->sA, d->sB,
-                         SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr, d->M,
-                         d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1);
+    return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK>, grid,
+                         dim3(G::THREADS), st, A, static_cast<const uint8_t*>(d->Bsh), d->sA,
+                         d->sB, SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr,
+                         d->M, d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1);
 }
 
 }  // namespace mxfp6_dev

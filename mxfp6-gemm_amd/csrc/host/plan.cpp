@@ -3,6 +3,7 @@
 // include/mxfp6_gemm.h). Plain C++17 with no HIP header: every device action goes through the
 // thin launch layer declared in hip_layer.h.
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 
 #include "../hip_layer.h"
@@ -18,11 +19,13 @@ namespace plan {
 // Candidate tiles (4 waves per workgroup):
 //   256x256, waves 2x2, each wave 128x128 -> MPW 4, NPW 4   (16 MFMAs per wave per 64-wide slab)
 //   256x192, waves 2x2, each wave 128x96  -> MPW 4, NPW 3   (12)
-//   128x512, waves 1x4, each wave 128x128 -> MPW 4, NPW 4   (16; the wide kernel: B straight into
-//            registers, A staged in LDS one K-tile at a time)
 //   128x384, waves 1x4, each wave 128x96  -> MPW 4, NPW 3   (12)
 //   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4   (8)
 //   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (4; two workgroups fit a CU's LDS)
+// the wide tiles (waves 1x4, B straight into registers, A staged in LDS one K-tile at a time):
+//   128x512, each wave 128x128            -> MPW 4, NPW 4   (16)
+//   128x256, each wave 128x64             -> MPW 4, NPW 2   (8)
+//   256x256, each wave 256x64             -> MPW 4, NPW 2   (16; A scales in two groups of 4)
 // and the skinny tiles (waves 1x4), the only ones for M not a multiple of 128 (M a multiple of
 // 32), and on small grids faster than the big ones for any M (C1, 256x256x1024: 32x128 6.3 us
 // against 8.2 us on 128x128):
@@ -38,14 +41,15 @@ namespace plan {
 //   per_cu   = ceil(active / CUS) workgroups on the busiest CU;
 //              (CUS: the current device's compute units, 256 on an MI355X)
 //   kb       = KiB a workgroup moves per 64-wide K slab: A (MT * 48 bytes, times 1 + A_ROWS_COST
-//              when read row-major: a copy touches ~3 cache lines per 128 bytes instead of 1) and
+//              when read row-major: a copy touches ~3 cache lines per 128 bytes instead of 1,
+//              plus A_ROWS_LONG per doubling of Kp past 8192: rows further apart cost more) and
 //              B (NT / 32 * 1536 bytes);
 //   t_slab   = max(T_SLAB_MIN, per_cu * (T_MFMA * mfmas + T_COPY_KB * kb),
 //                  active * T_L2_KB * kb) per slab: a latency floor (the ring keeps several slabs
 //              in flight), the CU's MFMA and global->LDS copy work shared by the workgroups
 //              resident on it, and the chip's L2 -> CU delivery shared by every workgroup in
-//              flight; the 128x512 tile loads B into registers (T_BREG_KB per KiB) and copies A
-//              at its own row-major cost (A_ROWS_COST_WIDE: a K-tile row is 144 contiguous bytes);
+//              flight; the wide tiles load B into registers (T_BREG_KB per KiB) and copy A at
+//              their own row-major cost (A_ROWS_COST_WIDE: a K-tile row is 144 contiguous bytes);
 //   t_wg     = T_WG + slabs * t_slab + T_OUT_KB * output KiB * per_cu;
 //   t        = T_LAUNCH + waves * t_wg, plus for a repack T_LAUNCH + its bytes (A read and written)
 //              at REPACK_BYTES_PER_US, and for a split T_LAUNCH + the partials written and read
@@ -56,9 +60,9 @@ namespace plan {
 // model's pick / measured best) over the shapes with M % 128 == 0, the five benchmark workloads
 // weighing 5x, plus 0.1x the log-time least squares of the plans within 1.3x of their shape's
 // best (0.2x weight for the others); the repack rate is the repack kernel's measured one. The
-// pick is then within 1.8% of the measured best on average over the 66 shapes with M % 128 == 0,
-// 26% at worst (2048x2048x8192), and the best on the five benchmark workloads; on the 16 skinny-M
-// and ragged shapes within 1.0% on average, 6% at worst.
+// pick is then within 0.8% of the measured best on average over the 66 shapes with M % 128 == 0,
+// 8% at worst (4096x102272x1024), and the best on the five benchmark workloads; on the 16
+// skinny-M and ragged shapes within 1.3% on average, 9% at worst.
 namespace {
 struct Plan {
     TileChoice tc;
@@ -66,8 +70,16 @@ struct Plan {
     bool repack;
 };
 const TileChoice kCands[] = {{256, 256, 4, 4}, {256, 192, 4, 3}, {128, 384, 4, 3},
-                             {128, 256, 2, 4}, {128, 128, 2, 2}, {128, 512, 4, 4}};
+                             {128, 256, 2, 4}, {128, 128, 2, 2}, {128, 512, 4, 4},
+                             {128, 256, 4, 2}, {256, 256, 4, 2}};
 const TileChoice kSkinny[] = {{64, 256, 2, 2}, {32, 256, 1, 2}, {64, 128, 2, 1}, {32, 128, 1, 1}};
+
+// The tiles of the wide kernel (B loaded into registers, A staged per K-tile).
+bool is_wide(const TileChoice& tc) {
+    return (tc.MT == 128 && tc.NT == 512 && tc.MPW == 4 && tc.NPW == 4) ||
+           (tc.MT == 128 && tc.NT == 256 && tc.MPW == 4 && tc.NPW == 2) ||
+           (tc.MT == 256 && tc.NT == 256 && tc.MPW == 4 && tc.NPW == 2);
+}
 
 double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repack, int CUS) {
     const long wg = (long)((M + tc.MT - 1) / tc.MT) * ((N + tc.NT - 1) / tc.NT) * S;
@@ -76,10 +88,12 @@ double plan_time_us(const TileChoice& tc, int M, int N, int Kp, int S, bool repa
     const long waves = (wg + cap - 1) / cap;
     const long active = std::min(wg, cap);
     const long per_cu = std::max(1L, (active + CUS - 1) / CUS);  // on the busiest CU
-    const int mfmas = tc.MPW * tc.NPW;  // per wave per slab
+    const int mfmas = tc.MT / 32 * (tc.NT / 32) / 4;  // per wave per slab (4 waves)
     const double slabs = (double)(Kp / 64) / S;
-    const bool wide = tc.MT == 128 && tc.NT == 512;
-    const double a_cost = repack ? 1.0 : 1.0 + (wide ? A_ROWS_COST_WIDE : A_ROWS_COST);
+    const bool wide = is_wide(tc);
+    const double long_rows = std::log2(std::max(1.0, Kp / 8192.0));
+    const double a_cost =
+        repack ? 1.0 : 1.0 + (wide ? A_ROWS_COST_WIDE : A_ROWS_COST) + A_ROWS_LONG * long_rows;
     const double a_kb = tc.MT * 48.0 * a_cost / 1024.0, b_kb = tc.NT / 32 * 1536.0 / 1024.0;
     const double work = T_COPY_KB * a_kb + (wide ? T_BREG_KB : T_COPY_KB) * b_kb;
     const double t_slab = std::max({T_SLAB_MIN, (double)per_cu * (T_MFMA * mfmas + work),

@@ -18,15 +18,17 @@ CUS = 256
 K_TILE = 192
 SPLIT_CHOICES = (1, 2, 3, 4, 6, 8, 12, 16)
 TILES = [(256, 256, 4, 4), (256, 192, 4, 3), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2),
-         (128, 512, 4, 4)]
-WIDE = (128, 512)  # the tile whose B goes straight to registers (wide_kernel.hpp)
+         (128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2)]
+# the tiles whose B goes straight to registers (wide_kernel.hpp)
+WIDE = {(128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2)}
 SKINNY = [(64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)]
 NAMES = ["T_LAUNCH", "T_WG", "T_SLAB_MIN", "T_MFMA", "T_COPY_KB", "T_BREG_KB", "T_L2_KB",
-         "T_OUT_KB", "REPACK_BYTES_PER_US", "SPLIT_BYTES_PER_US", "A_ROWS_COST", "A_ROWS_COST_WIDE"]
-CONSTANTS = {"T_LAUNCH": 2.80193, "T_WG": 1.22045, "T_SLAB_MIN": 0.148425, "T_MFMA": 0.0130223,
-             "T_COPY_KB": 0.0130326, "T_BREG_KB": 0.00701515, "T_L2_KB": 7.00392e-05,
-             "T_OUT_KB": 0.014044, "REPACK_BYTES_PER_US": 5.5e6, "SPLIT_BYTES_PER_US": 3.99902e+06,
-             "A_ROWS_COST": 0.746816, "A_ROWS_COST_WIDE": 0.425206}
+         "T_OUT_KB", "REPACK_BYTES_PER_US", "SPLIT_BYTES_PER_US", "A_ROWS_COST", "A_ROWS_COST_WIDE",
+         "A_ROWS_LONG"]
+CONSTANTS = {"T_LAUNCH": 2.62916, "T_WG": 0.906558, "T_SLAB_MIN": 0.150077, "T_MFMA": 0.00503219,
+             "T_COPY_KB": 0.0151656, "T_BREG_KB": 0.00887836, "T_L2_KB": 7.1454e-05,
+             "T_OUT_KB": 0.0164777, "REPACK_BYTES_PER_US": 5.5e6, "SPLIT_BYTES_PER_US": 4.03994e+06,
+             "A_ROWS_COST": 0.698364, "A_ROWS_COST_WIDE": 0.0170449, "A_ROWS_LONG": 0.158971}
 # the repack rate is the repack kernel's measured one, not fitted
 FIXED = {"REPACK_BYTES_PER_US": 5.5e6}
 # the fit: summed log(measured time of the pick / measured best) per shape (the benchmark
@@ -46,10 +48,11 @@ def _features(tile, M, N, Kp, S, repack):
     cap = CUS * occ
     active = min(wg, cap)
     return dict(waves=(wg + cap - 1) // cap, active=active, per_cu=max(1, -(-active // CUS)),
-                mfmas=tile[2] * tile[3], slabs=(Kp // 64) / S, wide=(MT, NT) == WIDE,
+                mfmas=MT // 32 * (NT // 32) // 4, slabs=(Kp // 64) / S, wide=tuple(tile) in WIDE,
                 repack=bool(repack), akb=MT * 48.0 / 1024.0, bkb=NT // 32 * 1536.0 / 1024.0,
                 out_kb=MT * NT * (4.0 if S > 1 else 2.0) / 1024.0, split=S > 1,
                 rep_bytes=2.0 * (-(-M // 32) * 32) * (Kp // 4 * 3.0),
+                long_rows=math.log2(max(1.0, Kp / 8192.0)),
                 split_bytes=4.0 * S * M * N + 2.0 * M * N)
 
 
@@ -57,7 +60,8 @@ def _time(c, f, xp=None):
     """plan.cpp plan_time_us over one plan's features (scalars) or arrays of them (xp = numpy)."""
     where = (lambda q, a, b: a if q else b) if xp is None else xp.where
     mx = max if xp is None else xp.maximum
-    a_cost = where(f["repack"], 1.0, 1.0 + where(f["wide"], c["A_ROWS_COST_WIDE"], c["A_ROWS_COST"]))
+    a_cost = where(f["repack"], 1.0, 1.0 + where(f["wide"], c["A_ROWS_COST_WIDE"], c["A_ROWS_COST"]) +
+                   c["A_ROWS_LONG"] * f["long_rows"])
     a_kb = f["akb"] * a_cost
     work = c["T_COPY_KB"] * a_kb + where(f["wide"], c["T_BREG_KB"], c["T_COPY_KB"]) * f["bkb"]
     t_slab = mx(mx(c["T_SLAB_MIN"], f["per_cu"] * (c["T_MFMA"] * f["mfmas"] + work)),

@@ -23,7 +23,8 @@ import torch  # noqa: E402
 import mxfp6_amd as mx  # noqa: E402
 
 TILES = [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3), (256, 256, 4, 4), (256, 192, 4, 3),
-         (128, 512, 4, 4), (64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)]
+         (128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2), (64, 256, 2, 2), (32, 256, 1, 2),
+         (64, 128, 2, 1), (32, 128, 1, 1)]
 SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
 
 

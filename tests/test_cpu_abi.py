@@ -120,7 +120,7 @@ def test_noalloc_rejects_before_device_work(mx):
     p = 0x1000  # never dereferenced
     Kp = mx.kpad(105728)
     rb = Kp // 4 * 3
-    assert mx.gemm_noalloc(0, 8192, 13312, Kp, 0, p, p, p, p, rb) == 1     # null A
-    assert mx.gemm_noalloc(5, 8192, 13312, Kp, p, p, p, p, p, rb) == 3     # bad out type
-    assert mx.workspace_size(8192, 13312, Kp) > mx.NOALLOC_SCRATCH_BYTES
-    assert mx.gemm_noalloc(1, 8192, 13312, Kp, p, p, p, p, p, rb) == 7     # partials too large
+    assert mx.gemm_noalloc(0, 4096, 6144, Kp, 0, p, p, p, p, rb) == 1      # null A
+    assert mx.gemm_noalloc(5, 4096, 6144, Kp, p, p, p, p, p, rb) == 3      # bad out type
+    assert mx.workspace_size(4096, 6144, Kp) > mx.NOALLOC_SCRATCH_BYTES
+    assert mx.gemm_noalloc(1, 4096, 6144, Kp, p, p, p, p, p, rb) == 7      # partials too large

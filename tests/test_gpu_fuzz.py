@@ -25,15 +25,19 @@ GUARD = 4096
 
 
 # shapes that reach the routes random small shapes rarely do (the router's pick in the comment)
-ROUTES = [(2816, 3072, 1024),   # 128x512
-          (2816, 896, 8192),    # 128x512 over a masked last column, 4 K segments
-          (6016, 10880, 2048),  # 128x512, A repacked, masked last column
-          (3328, 9856, 1024),   # 256x256, A repacked, masked last column
-          (5120, 6528, 1024),   # 256x192, A repacked
-          (4736, 3456, 1024),   # 128x384
-          (1408, 1536, 8192),   # 128x256, 3 K segments
-          (7168, 640, 8192),    # 256x256 over a masked last column, 3 segments, whole segments per XCD
-          (2048, 2048, 2048),   # 128x128
+ROUTES = [(5504, 1536, 1024),   # 128x512
+          (5504, 384, 16384),   # 128x512 over a masked last column, 4 K segments
+          (896, 4352, 1024),    # 128x256, four waves side by side
+          (384, 10112, 1024),   # 128x256 (four waves side by side), masked last column
+          (128, 5504, 8192),    # 128x256 (four waves side by side), masked, 6 K segments
+          (768, 11008, 1024),   # 256x256, four waves side by side
+          (6656, 1152, 1024),   # 256x256 (four waves side by side), masked last column
+          (4608, 384, 16384),   # 256x256 (side by side), masked, 6 segments, whole segments per XCD
+          (768, 10880, 16384),  # 256x256 (side by side), A repacked, masked last column
+          (2304, 7296, 1024),   # 256x192, A repacked
+          (6016, 2688, 1024),   # 128x384
+          (384, 5504, 1024),    # 128x128
+          (5504, 128, 8192),    # 128x128, 4 K segments
           (2047, 1000, 4096)]   # ragged, 64x128
 
 

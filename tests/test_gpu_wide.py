@@ -1,8 +1,9 @@
-"""The wide tile (128 x 512, four waves side by side, B streamed straight into registers, A staged
-in LDS one K-tile per row): bit for bit equal to the direct kernel (same MFMAs, same K order) with
-row-major and repacked A, unsplit and split on both XCD maps; equal to the 256x256 slab kernel on
-ragged (masked) shapes, which groups scales the same way; all output types against the FP64
-oracle."""
+"""The wide tiles (four waves side by side, B streamed straight into registers, A staged in LDS one
+K-tile per row): 128 x 512, 128 x 256 and 256 x 256 (scale groups of 4 A blocks and 2 B blocks).
+Each is bit for bit equal to the direct kernel (same MFMAs, same K order) with row-major and
+repacked A, unsplit and split on both XCD maps; equal to the 256x256 slab kernel on ragged
+(masked) shapes (the same MFMA sequence per output block, whatever the scale grouping of the
+layouts); all output types against the FP64 oracle."""
 import numpy as np
 import pytest
 
@@ -12,12 +13,16 @@ import gpu_util as g
 
 pytestmark = pytest.mark.gpu
 
-WIDE = (128, 512, 4, 4)
+WIDE_TILES = [(128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2)]
 
 
-@pytest.mark.parametrize("M,N,K", [(512, 1024, 2112), (128, 512, 192), (256, 2048, 4224)])
+@pytest.mark.parametrize("WIDE", WIDE_TILES)
+@pytest.mark.parametrize("M,N,K", [(512, 1024, 2112), (256, 512, 192), (256, 2048, 4224),
+                                   (768, 1536, 3456)])
 @pytest.mark.parametrize("a_layout", [0, 1])
-def test_wide_bitwise_equals_direct(M, N, K, a_layout):
+def test_wide_bitwise_equals_direct(WIDE, M, N, K, a_layout):
+    """The K-tile counts 11, 1, 22 and 18: the 256 x 256 tile's K loop runs K-tiles in pairs,
+    so odd counts take its single-K-tile tail."""
     p = mx.make_problem(M, N, K, seed=M + N + K + a_layout)
     dp = g.DevProblem(p, WIDE)
     Dw = g.run_explicit(dp, mx.OUT_F32, a_layout=a_layout)
@@ -25,9 +30,10 @@ def test_wide_bitwise_equals_direct(M, N, K, a_layout):
     assert np.array_equal(Dw.view(np.uint32), Dd.view(np.uint32))
 
 
+@pytest.mark.parametrize("WIDE", WIDE_TILES)
 @pytest.mark.parametrize("S", [2, 3, 8])
 @pytest.mark.parametrize("M,N", [(512, 1024), (2048, 1024)])
-def test_wide_split_bitwise_equals_direct_split(M, N, S):
+def test_wide_split_bitwise_equals_direct_split(WIDE, M, N, S):
     """Split grids: at most 128 tiles hand each XCD whole K segments, more use the grid order;
     every partial lands in its segment's slot either way."""
     K = 4224  # 22 K-tiles: uneven segments
@@ -39,9 +45,10 @@ def test_wide_split_bitwise_equals_direct_split(M, N, S):
         assert np.array_equal(Dw.view(np.uint32), Dd.view(np.uint32)), a_layout
 
 
+@pytest.mark.parametrize("WIDE", WIDE_TILES)
 @pytest.mark.parametrize("M,N,K", [(300, 700, 960), (97, 1000, 2112), (129, 513, 384),
                                    (1, 33, 192)])
-def test_wide_masked_equals_slab_masked(M, N, K):
+def test_wide_masked_equals_slab_masked(WIDE, M, N, K):
     """Ragged shapes run the wide tile masked; its FP32 output equals the masked 256x256 slab
     kernel's (same scale grouping, same K order) bit for bit, and both meet the oracle bar."""
     p = mx.make_problem(M, N, K, seed=M * 7 + N)
@@ -58,8 +65,9 @@ def test_wide_masked_equals_slab_masked(M, N, K):
     checks.check(Dw, R, ab, mx.OUT_F32)
 
 
+@pytest.mark.parametrize("WIDE", WIDE_TILES)
 @pytest.mark.parametrize("out_type", [0, 1, 2])
-def test_wide_output_types_against_oracle(out_type):
+def test_wide_output_types_against_oracle(WIDE, out_type):
     import oracle
     M, N, K = 256, 1024, 960  # K-tail: kpad(960) = 1152
     p = mx.make_problem(M, N, K, dist_a=mx.DIST_STUDENT_T3, dist_b=mx.DIST_STUDENT_T3, seed=13)

@@ -15,8 +15,8 @@ pytestmark = pytest.mark.gpu
 SEQUENCES = {
     # split-K: the 2048x1024x105728 workload (8 segments, 64 MiB of partials), then a smaller split
     "split": [(2048, 1024, 105728, 1), (512, 1024, 32768, 0)],
-    # A repacked into the scratch (256x256 tile), then a smaller repacking plan (128x128 tile)
-    "repack": [(2048, 8192, 4096, 2), (1024, 4096, 8192, 1)],
+    # A repacked into the scratch (48 MiB), then a plan that repacks a smaller A (12 MiB)
+    "repack": [(2048, 5120, 32768, 2), (1024, 16384, 16384, 1)],
     # 3 segments of partials (120 MiB) fit, the repacked A beside them does not: A read row-major
     "split_no_room_for_repack": [(2048, 5120, 105728, 2), (256, 256, 1024, 0)],
 }
@@ -56,6 +56,8 @@ def test_noalloc_equals_workspace_path_twice(kind):
         say(f"  no-alloc call {i + 1} ({kind}): {M}x{N}x{K} out {mx.OUT_NAMES[ot]} tile {dp.tile} "
             f"S {S} repack {rp} partials {mx.workspace_size(M, N, p.Kp)} B")
         assert mx.workspace_size(M, N, p.Kp) <= mx.NOALLOC_SCRATCH_BYTES
+        if kind == "repack":
+            assert rp, "the repack sequence needs plans that repack A"
         want = _with_workspace(dp, ot)
         got, free0, free1 = _no_alloc(dp, ot)
         assert torch.equal(got, want), f"{kind} call {i + 1}: outputs differ"
