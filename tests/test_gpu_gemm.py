@@ -360,8 +360,9 @@ def test_reference_library_same_inputs(g, orc, ref_lib, M, N, K, out_type):
 @pytest.mark.parametrize("tile", [(256, 256, 4, 4), (256, 256, 2, 4), (256, 192, 4, 3),
                                   (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2),
                                   (64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1),
-                                  (32, 128, 1, 1)])
-@pytest.mark.parametrize("M,N", [(256, 768), (289, 418), (97, 419)])
+                                  (32, 128, 1, 1), (128, 512, 4, 4), (128, 256, 4, 2),
+                                  (256, 256, 4, 2)])
+@pytest.mark.parametrize("M,N", [(256, 768), (512, 1536), (289, 418), (97, 419)])
 def test_lowp_output_is_rounded_f32(g, tile, M, N):
     """Every tile, unsplit: the FP16 and BF16 outputs equal the FP32 output of the same plan
     rounded to nearest-even on the host, bit for bit (the lane-pair exchange of the 16-bit
