@@ -75,7 +75,7 @@ CONFIGS = {
 PROFILES = os.path.join(ROOT, "profiles")
 # the tiles run by wide_kernel (four waves side by side, B loaded into registers); the others by
 # slab_kernel
-WIDE_TILES = {(128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2)}
+WIDE_TILES = {(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4, 2)}
 METRIC = "MXFP6 GEMM TFLOPs (FP16 out) and % of MXFP6 MFMA peak, 1xMI355X"
 
 

@@ -421,6 +421,7 @@ int slab_run(const mxfp6_launch_desc* d, hipStream_t st) {
     if (d->MT == 128 && d->NT == 512) return wide_launch_t<4, 4, 8, KT, SPLIT>(d, st);
     if (d->MT == 128 && d->NT == 256 && d->mpw == 4) return wide_launch_t<4, 2, 8, KT, SPLIT>(d, st);
     if (d->MT == 256 && d->NT == 256 && d->npw == 2) return wide_launch_t<8, 2, 4, KT, SPLIT>(d, st);
+    if (d->MT == 128 && d->NT == 384) return wide_launch_t<4, 3, 8, KT, SPLIT>(d, st);
     // skinny tiles: one wave row, four wave columns, a deeper ring
     if (d->MT == 32 && d->NT == 128) return slab_launch_t<32, 128, 1, 4, 4, 8, KT, SPLIT>(d, st);
     if (d->MT == 32 && d->NT == 256) return slab_launch_t<32, 256, 1, 4, 4, 8, KT, SPLIT>(d, st);
@@ -428,7 +429,6 @@ int slab_run(const mxfp6_launch_desc* d, hipStream_t st) {
     if (d->MT == 64 && d->NT == 256) return slab_launch_t<64, 256, 1, 4, 4, 8, KT, SPLIT>(d, st);
     if (d->MT == 128 && d->NT == 128) return slab_launch_t<128, 128, 2, 2, 4, 6, KT, SPLIT>(d, st);
     if (d->MT == 128 && d->NT == 256) return slab_launch_t<128, 256, 2, 2, 4, 8, KT, SPLIT>(d, st);
-    if (d->MT == 128 && d->NT == 384) return slab_launch_t<128, 384, 1, 4, 4, 6, KT, SPLIT>(d, st);
     if (d->MT == 256 && d->NT == 192) return slab_launch_t<256, 192, 2, 2, 4, 6, KT, SPLIT>(d, st);
     if (d->mpw == 2) return slab_launch_t<256, 256, 4, 2, 4, 6, KT, SPLIT>(d, st);
     return slab_launch_t<256, 256, 2, 2, 4, 6, KT, SPLIT>(d, st);

@@ -3,9 +3,9 @@
 // A workgroup computes an MT x NT tile of D with MT = 32 MB and NT = 4 * 32 NPW; wave w owns all
 // MT rows and columns [32 NPW w, 32 NPW (w + 1)) of the tile: MB x NPW blocks of 32x32, FP32
 // accumulators in AGPRs, fed by v_mfma_scale_f32_32x32x64_f8f6f4 (FP6 E2M3 x FP6 E2M3 with per-lane
-// E8M0 scales). Three shapes are built:
-//   128 x 512 (MB 4, NPW 4), 128 x 256 (MB 4, NPW 2) and 256 x 256 (MB 8, NPW 2; A scales in two
-//   groups of four 32-row blocks).
+// E8M0 scales). Four shapes are built:
+//   128 x 512 (MB 4, NPW 4), 128 x 384 (MB 4, NPW 3), 128 x 256 (MB 4, NPW 2) and 256 x 256 (MB 8,
+//   NPW 2; A scales in two groups of four 32-row blocks).
 // No B block is needed by two waves, so
 //   B  streams straight from the preshuffled layout into the wave's MFMA operand registers: per
 //      64-wide K slab and block, one 16-byte load (lane t: bytes 16t) and one 8-byte load (bytes
@@ -87,7 +87,8 @@ struct WideGeom {
     static_assert(MB == 4 || MB == 8, "128 or 256 rows");
     static_assert(NPW >= 1 && NPW <= 4, "B scale group holds <= 4 blocks");
     // NB = 3: the prologue issues chunk 1 before the loop, and the count above then holds for
-    // it too (more loads follow chunk 1 in the prologue than in the loop)
+    // it too (more loads follow chunk 1 in the prologue, the B loads of slabs 1 and 2, than
+    // follow a chunk's last copy in the loop)
     static_assert(NB == 3, "three chunk buffers");
     static_assert(cps(0) + cps(1) + cps(2) == A_ISS && cps(2) >= 1, "copies per K-tile");
     static_assert(copy_k(cps(0) - 1) < NMF, "copy positions");
@@ -243,25 +244,33 @@ __global__ void __launch_bounds__(256, 1)
     v3i sc_a[NGA], sc_b;   // scale dwords of the current K-tile
     v3i sn_a[NGA], sn_b;   // and of the next one
 
-    // prologue: chunks 0 .. NB-2 in flight, then the scales of K-tile 0 and the B operands of its
-    // three slabs, in the order the loop issues them (the compiler, which places the B waits,
-    // then sees the same count of loads in flight on entry to the loop as around it; the empty
-    // asm statements keep it from merging or reordering the loads)
+    // prologue: what the first MFMAs need first (chunk 0, the scales of K-tile 0, the B operands
+    // of its slab 0), then chunks 1 .. NB-2 and the B operands of slabs 1 and 2 (the compiler,
+    // which places the B waits, then sees at least the count of loads in flight on entry to the
+    // loop that it sees around it; the empty asm statements keep it from merging or reordering the
+    // loads). PRO_WAIT counts the same operations after chunk 0 in either order.
 #pragma unroll
-    for (int c = 0; c < NB - 1; c++)
-#pragma unroll
-        for (int i = 0; i < G::A_ISS; i++) a_copy(i, min(kt0 + c, kt_last), c);
+    for (int i = 0; i < G::A_ISS; i++) a_copy(i, kt0, 0);
     load_scales(sc_a, sc_b, kt0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = 0; s < SUBS; s++)
+    for (int s = 0; s < SUBS; s++) {
 #pragma unroll
         for (int ni = 0; ni < NPW; ni++) {
             load_b(RB[s][ni], ni, kt0, s);
             asm volatile("" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
         }
+        if (s == 0) {
+#pragma unroll
+            for (int c = 1; c < NB - 1; c++)
+#pragma unroll
+                for (int i = 0; i < G::A_ISS; i++) a_copy(i, min(kt0 + c, kt_last), c);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
     wait_vmcnt<G::PRO_WAIT>();  // chunk 0 landed
     ring_barrier();
 #pragma unroll

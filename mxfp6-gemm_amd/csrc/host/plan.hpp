@@ -13,19 +13,19 @@ namespace plan {
 constexpr int DEFAULT_CUS = 256;
 // Plan-time model of the router (plan.cpp): fitted on MI355X measurements, microseconds.
 constexpr int SPLIT_CHOICES[] = {1, 2, 3, 4, 6, 8, 12, 16};  // K segments considered
-constexpr double T_LAUNCH = 2.62916;       // one kernel launch (and its ramp), back to back
-constexpr double T_WG = 0.906558;           // fixed cost of one workgroup
-constexpr double T_SLAB_MIN = 0.150077;      // latency floor of one 64-wide K slab
-constexpr double T_MFMA = 0.00503219;        // per MFMA per wave per slab, per workgroup on the busiest CU
-constexpr double T_COPY_KB = 0.0151656;      // per KiB copied global->LDS per slab, per workgroup
-constexpr double T_BREG_KB = 0.00887836;     // per KiB of B loaded into registers per slab (wide tiles)
-constexpr double T_L2_KB = 7.1454e-05;     // per KiB per slab of every workgroup in flight (L2 -> CUs)
-constexpr double T_OUT_KB = 0.0164777;      // per KiB of output (FP16 tile or FP32 partial) per workgroup
+constexpr double T_LAUNCH = 2.40452;       // one kernel launch (and its ramp), back to back
+constexpr double T_WG = 0.806055;           // fixed cost of one workgroup
+constexpr double T_SLAB_MIN = 0.183313;      // latency floor of one 64-wide K slab
+constexpr double T_MFMA = 0.00394993;        // per MFMA per wave per slab, per workgroup on the busiest CU
+constexpr double T_COPY_KB = 0.0165642;      // per KiB copied global->LDS per slab, per workgroup
+constexpr double T_BREG_KB = 0.00831597;     // per KiB of B loaded into registers per slab (wide tiles)
+constexpr double T_L2_KB = 7.1085e-05;     // per KiB per slab of every workgroup in flight (L2 -> CUs)
+constexpr double T_OUT_KB = 0.0216756;      // per KiB of output (FP16 tile or FP32 partial) per workgroup
 constexpr double REPACK_BYTES_PER_US = 5.5e6;        // A repack traffic (measured kernel rate)
-constexpr double SPLIT_BYTES_PER_US = 4039940.0;   // split-K partials written and read back
-constexpr double A_ROWS_COST = 0.698364;    // extra copy cost per byte of a row-major A slab
-constexpr double A_ROWS_COST_WIDE = 0.0170449;  // the same for the wide tiles' K-tile chunks
-constexpr double A_ROWS_LONG = 0.158971;    // more per doubling of Kp past 8192 (row-major A)
+constexpr double SPLIT_BYTES_PER_US = 4059650.0;   // split-K partials written and read back
+constexpr double A_ROWS_COST = 0.572519;    // extra copy cost per byte of a row-major A slab
+constexpr double A_ROWS_COST_WIDE = 0.0675946;  // the same for the wide tiles' K-tile chunks
+constexpr double A_ROWS_LONG = 0.158036;    // more per doubling of Kp past 8192 (row-major A)
 constexpr double PLAN_MIN_GAIN = 0.01;     // lead a more complex plan needs over a simpler one
 
 TileChoice route(int M, int N, int Kp);

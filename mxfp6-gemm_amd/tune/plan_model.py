@@ -20,15 +20,15 @@ SPLIT_CHOICES = (1, 2, 3, 4, 6, 8, 12, 16)
 TILES = [(256, 256, 4, 4), (256, 192, 4, 3), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2),
          (128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2)]
 # the tiles whose B goes straight to registers (wide_kernel.hpp)
-WIDE = {(128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2)}
+WIDE = {(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4, 2)}
 SKINNY = [(64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)]
 NAMES = ["T_LAUNCH", "T_WG", "T_SLAB_MIN", "T_MFMA", "T_COPY_KB", "T_BREG_KB", "T_L2_KB",
          "T_OUT_KB", "REPACK_BYTES_PER_US", "SPLIT_BYTES_PER_US", "A_ROWS_COST", "A_ROWS_COST_WIDE",
          "A_ROWS_LONG"]
-CONSTANTS = {"T_LAUNCH": 2.62916, "T_WG": 0.906558, "T_SLAB_MIN": 0.150077, "T_MFMA": 0.00503219,
-             "T_COPY_KB": 0.0151656, "T_BREG_KB": 0.00887836, "T_L2_KB": 7.1454e-05,
-             "T_OUT_KB": 0.0164777, "REPACK_BYTES_PER_US": 5.5e6, "SPLIT_BYTES_PER_US": 4.03994e+06,
-             "A_ROWS_COST": 0.698364, "A_ROWS_COST_WIDE": 0.0170449, "A_ROWS_LONG": 0.158971}
+CONSTANTS = {"T_LAUNCH": 2.40452, "T_WG": 0.806055, "T_SLAB_MIN": 0.183313, "T_MFMA": 0.00394993,
+             "T_COPY_KB": 0.0165642, "T_BREG_KB": 0.00831597, "T_L2_KB": 7.1085e-05,
+             "T_OUT_KB": 0.0216756, "REPACK_BYTES_PER_US": 5.5e6, "SPLIT_BYTES_PER_US": 4.05965e+06,
+             "A_ROWS_COST": 0.572519, "A_ROWS_COST_WIDE": 0.0675946, "A_ROWS_LONG": 0.158036}
 # the repack rate is the repack kernel's measured one, not fitted
 FIXED = {"REPACK_BYTES_PER_US": 5.5e6}
 # the fit: summed log(measured time of the pick / measured best) per shape (the benchmark

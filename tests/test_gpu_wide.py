@@ -13,16 +13,17 @@ import gpu_util as g
 
 pytestmark = pytest.mark.gpu
 
-WIDE_TILES = [(128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2)]
+WIDE_TILES = [(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4, 2)]
 
 
 @pytest.mark.parametrize("WIDE", WIDE_TILES)
-@pytest.mark.parametrize("M,N,K", [(512, 1024, 2112), (256, 512, 192), (256, 2048, 4224),
-                                   (768, 1536, 3456)])
+@pytest.mark.parametrize("tm,tn,K", [(2, 2, 2112), (1, 1, 192), (1, 4, 4224), (3, 3, 3456)])
 @pytest.mark.parametrize("a_layout", [0, 1])
-def test_wide_bitwise_equals_direct(WIDE, M, N, K, a_layout):
-    """The K-tile counts 11, 1, 22 and 18: the 256 x 256 tile's K loop runs K-tiles in pairs,
-    so odd counts take its single-K-tile tail."""
+def test_wide_bitwise_equals_direct(WIDE, tm, tn, K, a_layout):
+    """tm x tn tiles (M, N multiples of 256 and of the tile); the K-tile counts 11, 1, 22 and 18:
+    the 256 x 256 tile's K loop runs K-tiles in pairs, so odd counts take its single-K-tile
+    tail."""
+    M, N = 256 * tm, WIDE[1] * tn
     p = mx.make_problem(M, N, K, seed=M + N + K + a_layout)
     dp = g.DevProblem(p, WIDE)
     Dw = g.run_explicit(dp, mx.OUT_F32, a_layout=a_layout)
@@ -32,10 +33,11 @@ def test_wide_bitwise_equals_direct(WIDE, M, N, K, a_layout):
 
 @pytest.mark.parametrize("WIDE", WIDE_TILES)
 @pytest.mark.parametrize("S", [2, 3, 8])
-@pytest.mark.parametrize("M,N", [(512, 1024), (2048, 1024)])
-def test_wide_split_bitwise_equals_direct_split(WIDE, M, N, S):
+@pytest.mark.parametrize("M,tn", [(512, 2), (2048, 2)])
+def test_wide_split_bitwise_equals_direct_split(WIDE, M, tn, S):
     """Split grids: at most 128 tiles hand each XCD whole K segments, more use the grid order;
     every partial lands in its segment's slot either way."""
+    N = WIDE[1] * tn
     K = 4224  # 22 K-tiles: uneven segments
     p = mx.make_problem(M, N, K, seed=S * 7 + M)
     dp = g.DevProblem(p, WIDE)
