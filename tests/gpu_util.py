@@ -15,6 +15,18 @@ def say(msg):
     sys.stdout.flush()
 
 
+def routed_shape(cands, want):
+    """The first (M, N, K) of cands whose routed plan (tile, K segments, A repacked) satisfies
+    want(tile, S, repack): tests that need a given route search for it, so that a refit of the
+    router's model cannot silently move them off it."""
+    for M, N, K in cands:
+        Kp = mx.kpad(K)
+        if want(tuple(mx.choose_tile(M, N, Kp)), mx.splitk_segments(M, N, Kp),
+                mx.repacks_a(M, N, Kp)):
+            return M, N, K
+    raise AssertionError("no candidate shape reaches the route")
+
+
 class DevProblem:
     """Device copies of a Problem's operands laid out for one tile's scale grouping."""
 

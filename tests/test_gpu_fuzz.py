@@ -24,21 +24,15 @@ pytestmark = pytest.mark.gpu
 GUARD = 4096
 
 
-# shapes that reach the routes random small shapes rarely do (the router's pick in the comment)
-ROUTES = [(5504, 1536, 1024),   # 128x512
-          (5504, 384, 16384),   # 128x512 over a masked last column, 4 K segments
-          (896, 4352, 1024),    # 128x256, four waves side by side
-          (384, 10112, 1024),   # 128x256 (four waves side by side), masked last column
-          (128, 5504, 8192),    # 128x256 (four waves side by side), masked, 6 K segments
-          (768, 11008, 1024),   # 256x256, four waves side by side
-          (6656, 1152, 1024),   # 256x256 (four waves side by side), masked last column
-          (4608, 384, 16384),   # 256x256 (side by side), masked, 6 segments, whole segments per XCD
-          (768, 10880, 16384),  # 256x256 (side by side), A repacked, masked last column
-          (2304, 7296, 1024),   # 256x192, A repacked
-          (6016, 2688, 1024),   # 128x384
-          (384, 5504, 1024),    # 128x128
-          (5504, 128, 8192),    # 128x128, 4 K segments
-          (2047, 1000, 4096)]   # ragged, 64x128
+# shapes that reach routes random small shapes rarely do: the wide tiles (256x256, 128x512,
+# 128x384, 128x256) unsplit and split, with and without a masked last column, the 128x128 tile
+# split and not, and a ragged skinny one (the router's picks move when its model is refitted, so
+# the list is wide rather than one shape per route)
+ROUTES = [(5504, 1536, 1024), (5504, 384, 16384), (896, 4352, 1024), (384, 10112, 1024),
+          (128, 5504, 8192), (768, 11008, 1024), (6656, 1152, 1024), (4608, 384, 16384),
+          (768, 10880, 16384), (2304, 7296, 1024), (6016, 2688, 1024), (384, 5504, 1024),
+          (5504, 128, 8192), (2047, 1000, 4096), (3072, 4096, 2048), (1536, 1536, 24576),
+          (1024, 16384, 16384)]
 
 
 def _shapes(n=24, seed=20261201):

@@ -190,7 +190,10 @@ def test_preshuffled_a_input(g):
 def test_routed_repack_and_fallback(g, orc):
     """A shape the router repacks A for: full workspace (repack) and none (row-major A) give
     the same bits and pass the oracle."""
-    M, N, K = 640, 5248, 8192   # among the smallest shapes the router repacks A for
+    # among the smallest shapes the router repacks A for
+    M, N, K = g.routed_shape([(M, N, K) for K in (8192, 16384) for M in (384, 512, 640, 768, 1024)
+                              for N in (4096, 5120, 5504, 6144, 6784, 8192)],
+                             lambda t, S, rp: rp)
     p = mx.make_problem(M, N, K, seed=23)
     assert mx.repacks_a(M, N, p.Kp)
     dp = g.DevProblem(p, mx.choose_tile(M, N, p.Kp))

@@ -15,8 +15,9 @@ pytestmark = pytest.mark.gpu
 SEQUENCES = {
     # split-K: the 2048x1024x105728 workload (8 segments, 64 MiB of partials), then a smaller split
     "split": [(2048, 1024, 105728, 1), (512, 1024, 32768, 0)],
-    # A repacked into the scratch (48 MiB), then a plan that repacks a smaller A (12 MiB)
-    "repack": [(2048, 5120, 32768, 2), (1024, 16384, 16384, 1)],
+    # A repacked into the scratch (24 MiB), then a plan that repacks a smaller A (12 MiB); the
+    # shapes are the first of short lists that the router repacks A for
+    "repack": [(1024, 16384, 32768, 2), (1024, 16384, 16384, 1)],
     # 3 segments of partials (120 MiB) fit, the repacked A beside them does not: A read row-major
     "split_no_room_for_repack": [(2048, 5120, 105728, 2), (256, 256, 1024, 0)],
 }
@@ -47,9 +48,20 @@ def _no_alloc(dp, ot):
     return D, free0, torch.cuda.mem_get_info()[0]
 
 
+def _sequence(kind):
+    if kind != "repack":
+        return SEQUENCES[kind]
+    from gpu_util import routed_shape
+    big = routed_shape([(1024, N, K) for K in (32768, 65536) for N in (16384, 8192, 5120)],
+                       lambda t, S, rp: rp and S == 1)
+    small = routed_shape([(M, N, 16384) for M in (1024, 2048) for N in (16384, 8192, 5120)],
+                         lambda t, S, rp: rp and S == 1)
+    return [big + (2,), small + (1,)]
+
+
 @pytest.mark.parametrize("kind", sorted(SEQUENCES))
 def test_noalloc_equals_workspace_path_twice(kind):
-    for i, (M, N, K, ot) in enumerate(SEQUENCES[kind]):
+    for i, (M, N, K, ot) in enumerate(_sequence(kind)):
         p = mx.make_problem(M, N, K, seed=M + 3 * N + 7 * K)
         dp = DevProblem(p, mx.choose_tile(M, N, p.Kp))
         S, rp = mx.splitk_segments(M, N, p.Kp), mx.repacks_a(M, N, p.Kp)
