@@ -10,6 +10,8 @@ drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--all] [--no-cpu]
                   [--no-ref]
   python bench.py --prep      (device operand preparation: float -> MXFP6 device layouts, GB/s)
+  python bench.py --power S   (board power and clocks over S seconds of back-to-back GEMMs of the
+                               workload, this library then the reference library; amd-smi)
 
 Prints one JSON line per workload (only the default one unless --all). The headline `value` is
 the mean over exactly K timed steps after W warm-up steps (no extra warm-up: an idle MI355X sits
@@ -42,7 +44,9 @@ import argparse
 import json
 import os
 import re
+import subprocess
 import sys
+import threading
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -526,6 +530,87 @@ def run_prep(steps, warmup):
     }
 
 
+def smi_power_clock():
+    """amd-smi's socket power (W) and the mean graphics clock over the XCDs (MHz) of the one
+    visible GPU, or None (no amd-smi, no reading, or more than one GPU listed)."""
+    try:
+        out = subprocess.run(["amd-smi", "metric", "--power", "--clock"], capture_output=True,
+                             text=True, timeout=30).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    if len(re.findall(r"^GPU:", out, re.M)) != 1:
+        return None
+    pw = re.search(r"SOCKET_POWER:\s*([0-9.]+)\s*W", out)
+    clks = [int(x) for x in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*(\d+)\s*MHz", out)]
+    if not pw:
+        return None
+    return float(pw.group(1)), (sum(clks) / len(clks) if clks else None)
+
+
+def power_cap_w():
+    """The board's power cap (W) as rocm-smi reports it, or None."""
+    try:
+        out = subprocess.run(["rocm-smi", "--showmaxpower"], capture_output=True, text=True,
+                             timeout=30).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    caps = re.findall(r"Max Graphics Package Power \(W\):\s*([0-9.]+)", out)
+    return float(caps[0]) if len(caps) == 1 else None
+
+
+def run_power(name, seconds):
+    """Back-to-back GEMMs of one workload for `seconds` (after 2 s of the same), this library and
+    then the reference library on the same operands, sampling amd-smi's socket power and clocks
+    every 0.25 s in a thread: where the board sits against its power limit while each runs."""
+    import torch
+    ref = reference_library()
+    w = Workload(name, ref)
+    stream = torch.cuda.current_stream()
+    out = {"metric": "board power and clocks during back-to-back MXFP6 GEMMs, 1xMI355X",
+           "workload": workload_name(w.M, w.N, w.K, w.ot), "seconds": seconds,
+           "power_cap_w": power_cap_w()}
+    runs = [("this_library", lambda: w.ours(stream))]
+    if ref is not None:
+        runs.append(("reference_library", lambda: w.theirs(stream)))
+    for label, fn in runs:
+        t0 = time.time()
+        while time.time() - t0 < 2.0:
+            for _ in range(20):
+                fn()
+            torch.cuda.synchronize()
+        samples, done = [], threading.Event()
+
+        def sample():
+            while not done.is_set():
+                r = smi_power_clock()
+                if r is not None:
+                    samples.append(r)
+                done.wait(0.25)
+        th = threading.Thread(target=sample)
+        th.start()
+        calls, t1 = 0, time.time()
+        while time.time() - t1 < seconds:
+            for _ in range(20):
+                fn()
+            torch.cuda.synchronize()
+            calls += 20
+        el = time.time() - t1
+        done.set()
+        th.join()
+        pw = [s[0] for s in samples]
+        ck = [s[1] for s in samples if s[1] is not None]
+        out[label] = {"calls": calls, "us_per_call": round(el / calls * 1e6, 1),
+                      "tflops": round(w.flops * calls / el / 1e12, 1),
+                      "socket_power_w_mean": round(sum(pw) / len(pw), 1) if pw else None,
+                      "socket_power_w_max": max(pw) if pw else None,
+                      "gfx_clock_mhz_mean": round(sum(ck) / len(ck), 1) if ck else None,
+                      "samples": len(samples)}
+        if pw and out[label]["gfx_clock_mhz_mean"]:
+            out[label]["joules_per_pflop"] = round(
+                out[label]["socket_power_w_mean"] / (out[label]["tflops"] / 1000.0), 1)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -543,6 +628,8 @@ def main():
                     help="only run the 256 MiB copy kernel that calibrates the HBM byte counters")
     ap.add_argument("--prep", action="store_true",
                     help="time the device operand preparation (quantize + layouts) instead")
+    ap.add_argument("--power", type=float, default=0.0, metavar="SECONDS",
+                    help="board power and clocks over SECONDS of back-to-back GEMMs instead")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on exactly one GPU; --gpus {a.gpus} is not supported (the MXFP6 "
@@ -554,6 +641,9 @@ def main():
         return
     if a.prep:
         print(json.dumps(run_prep(a.steps, a.warmup)), flush=True)
+        return
+    if a.power > 0:
+        print(json.dumps(run_power(a.config, a.power)), flush=True)
         return
     names = sorted(CONFIGS, key=lambda n: n != a.config) if a.all else [a.config]
     run(names, a.steps, a.warmup, not a.no_cpu, not a.no_ref, not a.no_per_config and not a.all)
