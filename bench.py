@@ -12,6 +12,8 @@ drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX 
   python bench.py --prep      (device operand preparation: float -> MXFP6 device layouts, GB/s)
   python bench.py --power S   (board power and clocks over S seconds of back-to-back GEMMs of the
                                workload, this library then the reference library; amd-smi)
+  python bench.py --map [SHAPES]  (this library against the reference library, shape by shape:
+                               MxNxK,... or the default map of 154 shapes, FP16 out)
 
 Prints one JSON line per workload (only the default one unless --all). The headline `value` is
 the mean over exactly K timed steps after W warm-up steps (no extra warm-up: an idle MI355X sits
@@ -234,12 +236,19 @@ class Workload:
     """Device operands of one workload for this library's route and, when the reference library
     is given, for the reference library's own route (its scale grouping and workspace)."""
 
-    def __init__(self, name, ref=None):
+    def __init__(self, name, ref=None, shape=None):
+        """name: a CONFIGS workload; or shape = (M, N, K): FP16 out, A and B from N(0,1)."""
         import torch
-        M, N, K, ot, (da, sa_), (db, sb_), desc = CONFIGS[name]
+        if shape is None:
+            M, N, K, ot, (da, sa_), (db, sb_), desc = CONFIGS[name]
+            seed = SEED ^ int(name[1:])
+        else:
+            (M, N, K), ot = shape, mx.OUT_F16
+            (da, sa_), (db, sb_), desc = (mx.DIST_NORMAL, 1.0), (mx.DIST_NORMAL, 1.0), "A,B ~ N(0,1)"
+            seed = SEED ^ (M * 7 + N * 3 + K)
         self.name, self.M, self.N, self.K, self.ot, self.desc = name, M, N, K, ot, desc
         t0 = time.perf_counter()
-        p = mx.make_problem(M, N, K, da, sa_, db, sb_, seed=SEED ^ int(name[1:]))
+        p = mx.make_problem(M, N, K, da, sa_, db, sb_, seed=seed)
         self.p = p
         dev = torch.device("cuda:0")
         self.tile = mx.choose_tile(M, N, p.Kp)
@@ -530,6 +539,57 @@ def run_prep(steps, warmup):
     }
 
 
+def default_map():
+    """154 shapes: M in {1024, 2048, 4096, 8192} x N in {1024, 4096, 8192} x K in {1024 ... 16384},
+    four more (the reference's weakest bands: short K on a wide grid, N a multiple of 128 but
+    not of 256, a small square), and 90 drawn with a fixed seed (M, N multiples of 128, K from 256 to 65536,
+    between 1 GFLOP and 1.2 TFLOP)."""
+    import random
+    shapes = [(M, N, K) for M in (1024, 2048, 4096, 8192) for N in (1024, 4096, 8192)
+              for K in (1024, 2048, 4096, 8192, 16384)]
+    shapes += [(2048, 102272, 1024), (8192, 896, 8192), (4096, 2432, 8192), (2048, 2048, 2048)]
+    rng = random.Random(20261202)
+    ms = [128, 256, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 3072, 4096, 6144]
+    ns = [128, 256, 384, 640, 896, 1152, 1536, 2176, 2560, 3072, 3584, 5120, 6144, 7168, 10240,
+          14336]
+    ks = [256, 512, 768, 1536, 2048, 3072, 5120, 6144, 12288, 24576, 32768, 65536]
+    drawn = set()
+    while len(drawn) < 90:
+        M, N, K = rng.choice(ms), rng.choice(ns), rng.choice(ks)
+        if 1e9 <= 2.0 * M * N * K <= 1.2e12:
+            drawn.add((M, N, K))
+    return shapes + [s for s in sorted(drawn) if s not in shapes]
+
+
+def run_map(spec):
+    """This library and the reference library on the same operands, shape by shape, by the
+    reference's timing method (compare()); one JSON line per shape, then a summary line."""
+    import torch
+    ref = reference_library()
+    if ref is None:
+        raise SystemExit("--map needs the reference library (oracle/_ref/libmxfp6ref.so)")
+    if spec:
+        txt = open(spec).read() if os.path.exists(spec) else spec
+        shapes = [tuple(int(v) for v in t.strip().split("x")) for t in txt.split(",") if t.strip()]
+    else:
+        shapes = default_map()
+    stream = torch.cuda.current_stream()
+    ratios = []
+    for i, sh in enumerate(shapes):
+        w = Workload(f"{sh[0]}x{sh[1]}x{sh[2]}", ref, shape=sh)
+        c = compare(w, stream)
+        ratios.append(c["ratio"])
+        print(json.dumps({"shape": list(sh), "tile": c["tile"], "splitk": c["splitk"],
+                          "a_repacked": c["a_repacked"], "us": c["us"], "ref_tile": c["ref_tile"],
+                          "ref_us": c["ref_us"], "ratio": c["ratio"]}), flush=True)
+        del w
+        torch.cuda.empty_cache()
+    gm = float(np.exp(np.mean(np.log(ratios))))
+    print(json.dumps({"shapes": len(ratios), "geomean_ratio": round(gm, 3),
+                      "min_ratio": min(ratios), "max_ratio": max(ratios),
+                      "below_1": int(sum(r < 1.0 for r in ratios))}), flush=True)
+
+
 def smi_power_clock():
     """amd-smi's socket power (W) and the mean graphics clock over the XCDs (MHz) of the one
     visible GPU, or None (no amd-smi, no reading, or more than one GPU listed)."""
@@ -630,6 +690,9 @@ def main():
                     help="time the device operand preparation (quantize + layouts) instead")
     ap.add_argument("--power", type=float, default=0.0, metavar="SECONDS",
                     help="board power and clocks over SECONDS of back-to-back GEMMs instead")
+    ap.add_argument("--map", nargs="?", const="", default=None, metavar="SHAPES",
+                    help="this library against the reference library shape by shape instead "
+                         "(MxNxK,... or a file of them; default: 154 shapes)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on exactly one GPU; --gpus {a.gpus} is not supported (the MXFP6 "
@@ -644,6 +707,9 @@ def main():
         return
     if a.power > 0:
         print(json.dumps(run_power(a.config, a.power)), flush=True)
+        return
+    if a.map is not None:
+        run_map(a.map)
         return
     names = sorted(CONFIGS, key=lambda n: n != a.config) if a.all else [a.config]
     run(names, a.steps, a.warmup, not a.no_cpu, not a.no_ref, not a.no_per_config and not a.all)
