@@ -125,6 +125,12 @@ int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int tile[4], i
  * reference (its kernels read A row-major). */
 int mxfp6_gemm_repacks_a(int M, int N, int Kp);
 
+/* Whether gemm()'s plan for (out_type, M, N, Kp, A_row_bytes) writes D with nontemporal stores
+ * (unsplit plans whose operands fit in MI355X's 256 MiB last-level cache but whose operands and D
+ * together do not). No counterpart in the reference (its epilogue stores are plain); D's values
+ * are the same either way. */
+int mxfp6_gemm_streams_output(int out_type, int M, int N, int Kp, int A_row_bytes);
+
 /* Workspace bytes of an explicit plan (0 when splits == 1 and a_repack == 0). */
 size_t mxfp6_plan_workspace_size(int M, int N, int Kp, int splits, int a_repack);
 

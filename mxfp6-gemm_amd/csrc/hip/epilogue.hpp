@@ -2,13 +2,25 @@
 // FP16 or BF16, row-major, ld = N) or, for a split-K segment, to its FP32 partials ws[z][M][N].
 // Lane l of block (mi, ni) holds column n_w + 32 ni and rows m_w + 32 mi + 8 g + r in
 // acc[mi][ni][4 g + r], with m_w = (first row of the wave) + 4 (l / 32) and n_w = (first column of
-// the wave) + l % 32. MASK stores only rows < M and columns < N.
+// the wave) + l % 32. MASK stores only rows < M and columns < N. NT writes D with nontemporal
+// stores (streamed past the caches: the plan's operands and D exceed the last-level cache).
 #pragma once
 #include "device_common.hpp"
 
 namespace mxfp6_dev {
 
-template <int MPW, int NPW, typename OutT, bool SPLIT, bool MASK>
+// *p = v, nontemporal when NT
+template <bool NT, typename T>
+__device__ __forceinline__ void store_out(T* p, T v) {
+    if constexpr (!NT)
+        *p = v;
+    else if constexpr (sizeof(T) == 2)
+        __builtin_nontemporal_store((uint16_t)half_bits(v), reinterpret_cast<uint16_t*>(p));
+    else
+        __builtin_nontemporal_store(v, p);
+}
+
+template <int MPW, int NPW, typename OutT, bool SPLIT, bool MASK, bool NT = false>
 __device__ __forceinline__ void store_tile(const v16f (&acc)[MPW][NPW], OutT* __restrict__ D,
                                            float* __restrict__ ws, int M, int N, int m_w, int n_w,
                                            int lane, int wg_z) {
@@ -42,8 +54,9 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[MPW][NPW], OutT* __
                         const int m = m_p + mi * 32 + 8 * g, n = n_p + ni * 32;
                         if (MASK && n >= N) continue;  // n even and N even: n + 1 < N as well
                         uint32_t* d0 = reinterpret_cast<uint32_t*>(D + (size_t)m * N + n);
-                        if (!MASK || m < M) *d0 = oa;
-                        if (!MASK || m + 2 < M) *reinterpret_cast<uint32_t*>(D + (size_t)(m + 2) * N + n) = ob;
+                        if (!MASK || m < M) store_out<NT>(d0, oa);
+                        if (!MASK || m + 2 < M)
+                            store_out<NT>(reinterpret_cast<uint32_t*>(D + (size_t)(m + 2) * N + n), ob);
                     }
             return;
         }
@@ -62,7 +75,7 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[MPW][NPW], OutT* __
                     if (SPLIT)
                         ws[(size_t)wg_z * M * N + idx] = acc[mi][ni][4 * g + r];
                     else
-                        D[idx] = cvt_out<OutT>(acc[mi][ni][4 * g + r]);
+                        store_out<NT>(D + idx, cvt_out<OutT>(acc[mi][ni][4 * g + r]));
                 }
 }
 

@@ -82,7 +82,7 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
     slab_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
                 OutT* __restrict__ D, float* __restrict__ ws, int M, int N, int Kp,
-                int A_row_bytes, int S) {
+                int A_row_bytes, int S, int out_nt) {
     using G = SlabGeom<MT, NT, WM, WN, NS>;
     constexpr int MPW = G::MPW, NPW = G::NPW, THREADS = G::THREADS, STAGE = G::STAGE;
     static_assert(G::NWAVES == 4 || G::NWAVES == 8, "4 or 8 waves per workgroup");
@@ -333,11 +333,14 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
         if (q + 1 < nq) tail_step(q + 1, R1, R0);
     }
 
-    // epilogue
+    // epilogue; out_nt: D streamed
     wait_vmcnt0();
-    store_tile<MPW, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N,
-                                             wg_m * MT + wm * MPW * 32 + 4 * (lane >> 5),
-                                             wg_n * NT + wn * NPW * 32 + (lane & 31), lane, wg_z);
+    const int m_w = wg_m * MT + wm * MPW * 32 + 4 * (lane >> 5);
+    const int n_w = wg_n * NT + wn * NPW * 32 + (lane & 31);
+    if (!SPLIT && out_nt)
+        store_tile<MPW, NPW, OutT, SPLIT, MASK, true>(acc, D, ws, M, N, m_w, n_w, lane, wg_z);
+    else
+        store_tile<MPW, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N, m_w, n_w, lane, wg_z);
 }
 
 // ---- launch ----------------------------------------------------------------------------------
@@ -352,7 +355,7 @@ hipError_t slab_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipS
                          dim3(64 * WM * WN), st, A, static_cast<const uint8_t*>(d->Bsh), d->sA,
                          d->sB, SPLIT ? nullptr : static_cast<KT*>(d->D),
                          SPLIT ? d->ws : nullptr, d->M, d->N, d->Kp, d->A_row_bytes,
-                         SPLIT ? d->splits : 1);
+                         SPLIT ? d->splits : 1, SPLIT ? 0 : d->out_stream);
 }
 
 // Ring depth per tile: as many slabs as fit 160 KiB of LDS (128 x 128 and 32 x 128: half of it,

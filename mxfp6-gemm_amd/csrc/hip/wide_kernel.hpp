@@ -118,7 +118,7 @@ __global__ void __launch_bounds__(256, 1)
     wide_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
                 OutT* __restrict__ D, float* __restrict__ ws, int M, int N, int Kp,
-                int A_row_bytes, int S) {
+                int A_row_bytes, int S, int out_nt) {
     using G = WideGeom<MB_, NPW_, NB_>;
     constexpr int MT = G::MT, NT = G::NT, MB = G::MB, NPW = G::NPW, NB = G::NB;
     constexpr int NGA = G::NGA, GA = G::GA, NSET = G::NSET, NMF = G::NMF;
@@ -336,11 +336,13 @@ __global__ void __launch_bounds__(256, 1)
     }
     for (; c < nkt; c++) ktile(c, P0{});
 
-    // epilogue (the clamped prefetches of the last K-tiles are drained first)
+    // epilogue (the clamped prefetches of the last K-tiles are drained first); out_nt: D streamed
     wait_vmcnt0();
-    store_tile<MB, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N, wg_m * MT + 4 * (lane >> 5),
-                                            wg_n * NT + wave * NPW * 32 + (lane & 31), lane,
-                                            wg_z);
+    const int m_w = wg_m * MT + 4 * (lane >> 5), n_w = wg_n * NT + wave * NPW * 32 + (lane & 31);
+    if (!SPLIT && out_nt)
+        store_tile<MB, NPW, OutT, SPLIT, MASK, true>(acc, D, ws, M, N, m_w, n_w, lane, wg_z);
+    else
+        store_tile<MB, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N, m_w, n_w, lane, wg_z);
 }
 
 // One launch of a wide kernel (grid ceil(M/MT) x ceil(N/NT) x splits, 256 threads).
@@ -352,7 +354,8 @@ hipError_t wide_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipS
     return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK>, grid,
                          dim3(G::THREADS), st, A, static_cast<const uint8_t*>(d->Bsh), d->sA,
                          d->sB, SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr,
-                         d->M, d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1);
+                         d->M, d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1,
+                         SPLIT ? 0 : d->out_stream);
 }
 
 }  // namespace mxfp6_dev

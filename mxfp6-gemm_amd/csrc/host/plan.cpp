@@ -252,6 +252,15 @@ const char* status_text(int st) {
 
 // ---- launch ----------------------------------------------------------------------------------
 
+bool streams_output(int out_type, int M, int N, int Kp, int S, bool repack, int A_row_bytes) {
+    if (S > 1) return false;  // the split-K partials are read back; the reduce writes D
+    const double packed = Kp / 4 * 3.0;
+    const double in = (double)M * A_row_bytes + (repack ? ((M + 31) / 32 * 32) * packed : 0.0) +
+                      (double)N * packed + (double)(M + N) * (Kp / 32);
+    const double out = (double)M * N * (out_type == 0 ? 4 : 2);  // FP32 or a 16-bit type
+    return in <= LLC_BYTES && in + out > STREAM_FOOTPRINT_BYTES;
+}
+
 // ws: the workspace of the plan (S, a_layout): split partials first, then (MXFP6_A_REPACK) the
 // repacked A at the next 256-byte boundary.
 int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, int a_layout, int kernel,
@@ -279,6 +288,8 @@ int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, int a_l
     d.Ash = a_layout == MXFP6_A_REPACK
                 ? static_cast<uint8_t*>(ws) + (split_bytes(M, N, S) + 255) / 256 * 256
                 : nullptr;
+    d.out_stream =
+        streams_output(out_type, M, N, Kp, S, a_layout == MXFP6_A_REPACK, A_row_bytes) ? 1 : 0;
     d.stream = stream;
     const int rc = mxfp6_hip_launch(&d);
     return rc == 0 ? MXFP6_OK : rc == 1 ? MXFP6_ERR_TILE : MXFP6_ERR_HIP;
@@ -484,6 +495,14 @@ extern "C" int mxfp6_gemm_direct(int out_type, int M, int N, int Kp, int mpw, in
 
 extern "C" int mxfp6_gemm_repacks_a(int M, int N, int Kp) {
     return plan::route_repacks(M, N, Kp) ? 1 : 0;
+}
+
+extern "C" int mxfp6_gemm_streams_output(int out_type, int M, int N, int Kp, int A_row_bytes) {
+    if (M <= 0 || N <= 0 || Kp <= 0 || Kp % K_TILE != 0) return 0;
+    return plan::streams_output(out_type, M, N, Kp, plan::splitk_segments(M, N, Kp),
+                                plan::route_repacks(M, N, Kp), A_row_bytes)
+               ? 1
+               : 0;
 }
 
 extern "C" size_t mxfp6_plan_workspace_size(int M, int N, int Kp, int splits, int a_repack) {

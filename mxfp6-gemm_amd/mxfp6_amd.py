@@ -55,6 +55,7 @@ SIGNATURES = {
                                       C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, _vp,
                                       C.c_size_t, _vp]),
     "mxfp6_gemm_repacks_a": (C.c_int, [C.c_int, C.c_int, C.c_int]),
+    "mxfp6_gemm_streams_output": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "mxfp6_plan_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "mxfp6_preshuffle_rows_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "mxfp6_quantize_async": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_size_t, _vp, C.c_int, _vp]),
@@ -197,6 +198,11 @@ def gemm_explicit(out_type, M, N, Kp, tile, splits, dA, dBsh, dsA, dsB, dD, A_ro
 def repacks_a(M, N, Kp):
     """Whether gemm() repacks A into the preshuffled layout for this shape."""
     return bool(lib().mxfp6_gemm_repacks_a(M, N, Kp))
+
+
+def streams_output(out_type, M, N, Kp, A_row_bytes):
+    """Whether gemm()'s plan writes D with nontemporal stores for this call."""
+    return bool(lib().mxfp6_gemm_streams_output(out_type, M, N, Kp, A_row_bytes))
 
 
 def plan_workspace_size(M, N, Kp, splits, a_repack):

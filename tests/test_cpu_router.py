@@ -278,3 +278,18 @@ def test_plan_cache_is_per_thread_and_transparent(mx):
     for t in threads:
         t.join()
     assert not bad, bad[:3]
+
+
+def test_streaming_rule(mx):
+    """D is written with nontemporal stores only by unsplit plans whose operands fit in the
+    256 MiB last-level cache while the operands and D together do not."""
+    cases = [((8192, 8192, 8192), 1, False),     # everything fits
+             ((2048, 1024, 105728), 1, False),   # split K: the reduce writes D
+             ((2048, 51200, 1024), 1, False),    # 253 MB in all: fits
+             ((2048, 102272, 4096), 1, False),   # the operands alone exceed the cache
+             ((2048, 102272, 1024), 1, True),
+             ((8192, 16384, 2048), 1, True),
+             ((4096, 16384, 1024), 0, True)]     # FP32 D
+    for (M, N, K), ot, want in cases:
+        Kp = mx.kpad(K)
+        assert mx.streams_output(ot, M, N, Kp, mx.packed_bytes(K)) == want, (M, N, K)
