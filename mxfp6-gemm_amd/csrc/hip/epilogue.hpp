@@ -3,7 +3,7 @@
 // Lane l of block (mi, ni) holds column n_w + 32 ni and rows m_w + 32 mi + 8 g + r in
 // acc[mi][ni][4 g + r], with m_w = (first row of the wave) + 4 (l / 32) and n_w = (first column of
 // the wave) + l % 32. MASK stores only rows < M and columns < N. NT writes D with nontemporal
-// stores (streamed past the caches: the plan's operands and D exceed the last-level cache).
+// stores (streamed past the caches, for plans whose D would evict the operands the tiles re-read).
 #pragma once
 #include "device_common.hpp"
 

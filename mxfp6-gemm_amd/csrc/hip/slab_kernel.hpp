@@ -82,7 +82,7 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
     slab_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
                 OutT* __restrict__ D, float* __restrict__ ws, int M, int N, int Kp,
-                int A_row_bytes, int S, int out_nt) {
+                int A_row_bytes, int S) {
     using G = SlabGeom<MT, NT, WM, WN, NS>;
     constexpr int MPW = G::MPW, NPW = G::NPW, THREADS = G::THREADS, STAGE = G::STAGE;
     static_assert(G::NWAVES == 4 || G::NWAVES == 8, "4 or 8 waves per workgroup");
@@ -333,14 +333,11 @@ __global__ void __launch_bounds__(64 * WM * WN, 1)
         if (q + 1 < nq) tail_step(q + 1, R1, R0);
     }
 
-    // epilogue; out_nt: D streamed
+    // epilogue
     wait_vmcnt0();
-    const int m_w = wg_m * MT + wm * MPW * 32 + 4 * (lane >> 5);
-    const int n_w = wg_n * NT + wn * NPW * 32 + (lane & 31);
-    if (!SPLIT && out_nt)
-        store_tile<MPW, NPW, OutT, SPLIT, MASK, true>(acc, D, ws, M, N, m_w, n_w, lane, wg_z);
-    else
-        store_tile<MPW, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N, m_w, n_w, lane, wg_z);
+    store_tile<MPW, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N,
+                                             wg_m * MT + wm * MPW * 32 + 4 * (lane >> 5),
+                                             wg_n * NT + wn * NPW * 32 + (lane & 31), lane, wg_z);
 }
 
 // ---- launch ----------------------------------------------------------------------------------
@@ -355,7 +352,7 @@ hipError_t slab_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipS
                          dim3(64 * WM * WN), st, A, static_cast<const uint8_t*>(d->Bsh), d->sA,
                          d->sB, SPLIT ? nullptr : static_cast<KT*>(d->D),
                          SPLIT ? d->ws : nullptr, d->M, d->N, d->Kp, d->A_row_bytes,
-                         SPLIT ? d->splits : 1, SPLIT ? 0 : d->out_stream);
+                         SPLIT ? d->splits : 1);
 }
 
 // Ring depth per tile: as many slabs as fit 160 KiB of LDS (128 x 128 and 32 x 128: half of it,
@@ -393,6 +390,17 @@ int slab_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
 // rows for the 128-row tiles (4 buffers and groups of 4 or 16 rows measured within run-to-run
 // noise on 8192^3, 2048x1024x105728 and 2048x6144x16128 for 128 x 512), 4 for 256 x 256.
 constexpr int WIDE_NB = 3;
+// an unsplit plan may write D with nontemporal stores (d->out_stream): its own instantiation, so
+// that the kernels with plain stores keep a single epilogue
+template <int MB, int NPW, int XG, typename KT, bool SPLIT, bool ASH, bool MASK>
+hipError_t wide_launch_st(const mxfp6_launch_desc* d, const uint8_t* A, hipStream_t st) {
+    if constexpr (!SPLIT) {
+        if (d->out_stream)
+            return wide_kernel_launch<MB, NPW, WIDE_NB, XG, KT, SPLIT, ASH, MASK, true>(d, A, st);
+    }
+    return wide_kernel_launch<MB, NPW, WIDE_NB, XG, KT, SPLIT, ASH, MASK, false>(d, A, st);
+}
+
 template <int MB, int NPW, int XG, typename KT, bool SPLIT>
 int wide_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     using G = WideGeom<MB, NPW, WIDE_NB>;
@@ -407,11 +415,11 @@ int wide_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     }
     hipError_t e;
     if (d->a_layout == MXFP6_A_ROWS)
-        e = mask ? wide_kernel_launch<MB, NPW, WIDE_NB, XG, KT, SPLIT, false, true>(d, A, st)
-                 : wide_kernel_launch<MB, NPW, WIDE_NB, XG, KT, SPLIT, false, false>(d, A, st);
+        e = mask ? wide_launch_st<MB, NPW, XG, KT, SPLIT, false, true>(d, A, st)
+                 : wide_launch_st<MB, NPW, XG, KT, SPLIT, false, false>(d, A, st);
     else
-        e = mask ? wide_kernel_launch<MB, NPW, WIDE_NB, XG, KT, SPLIT, true, true>(d, A, st)
-                 : wide_kernel_launch<MB, NPW, WIDE_NB, XG, KT, SPLIT, true, false>(d, A, st);
+        e = mask ? wide_launch_st<MB, NPW, XG, KT, SPLIT, true, true>(d, A, st)
+                 : wide_launch_st<MB, NPW, XG, KT, SPLIT, true, false>(d, A, st);
     return e == hipSuccess ? 0 : 2;
 }
 

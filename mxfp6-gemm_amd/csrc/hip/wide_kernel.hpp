@@ -113,12 +113,13 @@ __device__ __forceinline__ void wide_mfma(v16f (&acc)[MB][NPW], int mi, int ni, 
     }
 }
 
-template <int MB_, int NPW_, int NB_, int XG, typename OutT, bool SPLIT, bool ASH, bool MASK>
+template <int MB_, int NPW_, int NB_, int XG, typename OutT, bool SPLIT, bool ASH, bool MASK,
+          bool STREAM>
 __global__ void __launch_bounds__(256, 1)
     wide_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
                 OutT* __restrict__ D, float* __restrict__ ws, int M, int N, int Kp,
-                int A_row_bytes, int S, int out_nt) {
+                int A_row_bytes, int S) {
     using G = WideGeom<MB_, NPW_, NB_>;
     constexpr int MT = G::MT, NT = G::NT, MB = G::MB, NPW = G::NPW, NB = G::NB;
     constexpr int NGA = G::NGA, GA = G::GA, NSET = G::NSET, NMF = G::NMF;
@@ -336,26 +337,25 @@ __global__ void __launch_bounds__(256, 1)
     }
     for (; c < nkt; c++) ktile(c, P0{});
 
-    // epilogue (the clamped prefetches of the last K-tiles are drained first); out_nt: D streamed
+    // epilogue (the clamped prefetches of the last K-tiles are drained first); STREAM: D written
+    // with nontemporal stores
     wait_vmcnt0();
-    const int m_w = wg_m * MT + 4 * (lane >> 5), n_w = wg_n * NT + wave * NPW * 32 + (lane & 31);
-    if (!SPLIT && out_nt)
-        store_tile<MB, NPW, OutT, SPLIT, MASK, true>(acc, D, ws, M, N, m_w, n_w, lane, wg_z);
-    else
-        store_tile<MB, NPW, OutT, SPLIT, MASK>(acc, D, ws, M, N, m_w, n_w, lane, wg_z);
+    store_tile<MB, NPW, OutT, SPLIT, MASK, STREAM>(acc, D, ws, M, N, wg_m * MT + 4 * (lane >> 5),
+                                                wg_n * NT + wave * NPW * 32 + (lane & 31), lane,
+                                                wg_z);
 }
 
 // One launch of a wide kernel (grid ceil(M/MT) x ceil(N/NT) x splits, 256 threads).
-template <int MB, int NPW, int NB, int XG, typename KT, bool SPLIT, bool ASH, bool MASK>
+template <int MB, int NPW, int NB, int XG, typename KT, bool SPLIT, bool ASH, bool MASK,
+          bool STREAM>
 hipError_t wide_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipStream_t st) {
     using G = WideGeom<MB, NPW, NB>;
     const dim3 grid((unsigned)((d->M + G::MT - 1) / G::MT), (unsigned)((d->N + G::NT - 1) / G::NT),
                     (unsigned)d->splits);
-    return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK>, grid,
+    return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK, STREAM>, grid,
                          dim3(G::THREADS), st, A, static_cast<const uint8_t*>(d->Bsh), d->sA,
                          d->sB, SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr,
-                         d->M, d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1,
-                         SPLIT ? 0 : d->out_stream);
+                         d->M, d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1);
 }
 
 }  // namespace mxfp6_dev

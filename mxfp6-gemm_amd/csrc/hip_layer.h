@@ -38,8 +38,8 @@ typedef struct mxfp6_launch_desc {
                           MXFP6_A_REPACK: repack A into Ash first, the kernel reads Ash;
                           MXFP6_A_PRESHUFFLED: A is already in the preshuffled operand layout */
     void* Ash;         /* MXFP6_A_REPACK: M * packed(Kp) bytes */
-    int out_stream;    /* 1: the tile kernel writes D with nontemporal stores (unsplit plans whose
-                          operands and D exceed the last-level cache) */
+    int out_stream;    /* 1: the wide tile kernel writes D with nontemporal stores (unsplit plans
+                          whose D would evict the operands from the last-level cache) */
     void* stream;      /* hipStream_t */
 } mxfp6_launch_desc;
 

@@ -252,8 +252,11 @@ const char* status_text(int st) {
 
 // ---- launch ----------------------------------------------------------------------------------
 
-bool streams_output(int out_type, int M, int N, int Kp, int S, bool repack, int A_row_bytes) {
-    if (S > 1) return false;  // the split-K partials are read back; the reduce writes D
+bool streams_output(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, bool repack,
+                    int A_row_bytes) {
+    // the split-K partials are read back and the reduce writes D; the other tiles' kernel keeps
+    // plain stores
+    if (S > 1 || !is_wide(tc)) return false;
     const double packed = Kp / 4 * 3.0;
     const double in = (double)M * A_row_bytes + (repack ? ((M + 31) / 32 * 32) * packed : 0.0) +
                       (double)N * packed + (double)(M + N) * (Kp / 32);
@@ -288,8 +291,11 @@ int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, int a_l
     d.Ash = a_layout == MXFP6_A_REPACK
                 ? static_cast<uint8_t*>(ws) + (split_bytes(M, N, S) + 255) / 256 * 256
                 : nullptr;
-    d.out_stream =
-        streams_output(out_type, M, N, Kp, S, a_layout == MXFP6_A_REPACK, A_row_bytes) ? 1 : 0;
+    d.out_stream = kernel == MXFP6_KERNEL_TILE &&
+                           streams_output(out_type, M, N, Kp, tc, S, a_layout == MXFP6_A_REPACK,
+                                          A_row_bytes)
+                       ? 1
+                       : 0;
     d.stream = stream;
     const int rc = mxfp6_hip_launch(&d);
     return rc == 0 ? MXFP6_OK : rc == 1 ? MXFP6_ERR_TILE : MXFP6_ERR_HIP;
@@ -499,8 +505,9 @@ extern "C" int mxfp6_gemm_repacks_a(int M, int N, int Kp) {
 
 extern "C" int mxfp6_gemm_streams_output(int out_type, int M, int N, int Kp, int A_row_bytes) {
     if (M <= 0 || N <= 0 || Kp <= 0 || Kp % K_TILE != 0) return 0;
-    return plan::streams_output(out_type, M, N, Kp, plan::splitk_segments(M, N, Kp),
-                                plan::route_repacks(M, N, Kp), A_row_bytes)
+    return plan::streams_output(out_type, M, N, Kp, plan::route(M, N, Kp),
+                                plan::splitk_segments(M, N, Kp), plan::route_repacks(M, N, Kp),
+                                A_row_bytes)
                ? 1
                : 0;
 }

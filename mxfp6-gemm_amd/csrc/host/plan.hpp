@@ -27,7 +27,7 @@ constexpr double A_ROWS_COST = 0.572519;    // extra copy cost per byte of a row
 constexpr double A_ROWS_COST_WIDE = 0.0675946;  // the same for the wide tiles' K-tile chunks
 constexpr double A_ROWS_LONG = 0.158036;    // more per doubling of Kp past 8192 (row-major A)
 constexpr double PLAN_MIN_GAIN = 0.01;     // lead a more complex plan needs over a simpler one
-// An unsplit plan writes D with nontemporal stores when the bytes it reads (operands, scales, the
+// An unsplit plan on a wide tile writes D with nontemporal stores when the bytes it reads (operands, scales, the
 // repacked A) fit in MI355X's 256 MiB last-level cache (Infinity Cache) but those and D together
 // exceed STREAM_FOOTPRINT_BYTES: D then no longer evicts the operands the tiles re-read. Measured:
 // streaming D 6-22% faster above the footprint (8192x16384x2048, 4096x51200x1024,
@@ -42,7 +42,8 @@ int splitk_segments(int M, int N, int Kp);
 size_t workspace_bytes(int M, int N, int Kp);
 size_t preferred_workspace_bytes(int M, int N, int Kp);
 bool route_repacks(int M, int N, int Kp);
-bool streams_output(int out_type, int M, int N, int Kp, int S, bool repack, int A_row_bytes);
+bool streams_output(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, bool repack,
+                    int A_row_bytes);
 size_t plan_bytes(int M, int N, int Kp, int S, bool repack);
 int check_common(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
                  const void* dsA, const void* dsB, const void* dD, int A_row_bytes);
