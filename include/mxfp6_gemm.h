@@ -125,6 +125,29 @@ int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int tile[4], i
  * reference (its kernels read A row-major). */
 int mxfp6_gemm_repacks_a(int M, int N, int Kp);
 
+/* Measured plan selection. No counterpart in the reference (its router is a fixed rule).
+ *
+ * mxfp6_gemm_tune times up to `candidates` of the router's best-predicted plans for (out_type, M,
+ * N, Kp) -- those with choose_tile's scale grouping (the operands' scales are tiled for it) whose
+ * workspace fits ws_bytes -- on the caller's operands (D is overwritten), and keeps the fastest for
+ * the process: later gemm() calls of the shape and output type run it whenever their workspace
+ * holds it (else the router's plan). It waits for `stream`, so it must not be called during graph
+ * capture. The chosen plan is returned in tile, *splits and *a_repack (each may be NULL). A
+ * different plan may sum K in another order: D stays within the same tolerance of the exact
+ * result, but its low bits may differ from the router's plan. */
+int mxfp6_gemm_tune(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
+                    const uint8_t* dsA, const uint8_t* dsB, void* dD, int A_row_bytes, void* ws,
+                    size_t ws_bytes, int candidates, void* stream, int tile[4], int* splits,
+                    int* a_repack);
+
+/* The measured plan of (out_type, M, N, Kp): 1 and the plan in tile, *splits, *a_repack (each may
+ * be NULL) if mxfp6_gemm_tune chose one, else 0. */
+int mxfp6_gemm_tuned_plan(int out_type, int M, int N, int Kp, int tile[4], int* splits,
+                          int* a_repack);
+
+/* Forgets every measured plan (gemm() runs the router's plans again). */
+void mxfp6_gemm_tune_reset(void);
+
 /* Whether gemm()'s plan for (out_type, M, N, Kp, A_row_bytes) writes D with nontemporal stores
  * (unsplit plans whose operands fit in MI355X's 256 MiB last-level cache but whose operands and D
  * together do not). No counterpart in the reference (its epilogue stores are plain); D's values

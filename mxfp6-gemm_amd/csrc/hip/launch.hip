@@ -117,6 +117,29 @@ extern "C" int mxfp6_hip_clock_sample(uint64_t* out, int nwg, void* stream) {
                                    static_cast<hipStream_t>(stream), out));
 }
 
+extern "C" int mxfp6_hip_time(int (*launch)(void* ctx), void* ctx, void* stream, int warm, int reps,
+                              float* ms) {
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    hipEvent_t a = nullptr, b = nullptr;
+    if (hipEventCreate(&a) != hipSuccess) return 2;
+    if (hipEventCreate(&b) != hipSuccess) {
+        (void)hipEventDestroy(a);
+        return 2;
+    }
+    int rc = 0;
+    for (int i = 0; i < warm && rc == 0; i++) rc = launch(ctx);
+    if (rc == 0 && hipEventRecord(a, st) != hipSuccess) rc = 2;
+    for (int i = 0; i < reps && rc == 0; i++) rc = launch(ctx);
+    if (rc == 0 && hipEventRecord(b, st) != hipSuccess) rc = 2;
+    float t = 0.0f;
+    if (rc == 0 && (hipEventSynchronize(b) != hipSuccess || hipEventElapsedTime(&t, a, b) != hipSuccess))
+        rc = 2;
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    if (rc == 0) *ms = t / (float)(reps > 0 ? reps : 1);
+    return rc;
+}
+
 extern "C" int mxfp6_hip_device_cus(void) {
     // per device: 0 = not read yet, -1 = the query failed
     static std::atomic<int> cus[64];

@@ -63,6 +63,11 @@ int mxfp6_hip_clock_sample(uint64_t* out, int nwg, void* stream);
  * device), or 0 when the runtime reports no device. */
 int mxfp6_hip_device_cus(void);
 
+/* Calls launch(ctx) `warm` times, then `reps` times between two events recorded on `stream`, and
+ * waits for the second: *ms = the mean time per call. Returns 0, 2 on a HIP error, or launch's
+ * own nonzero status. */
+int mxfp6_hip_time(int (*launch)(void* ctx), void* ctx, void* stream, int warm, int reps, float* ms);
+
 /* Whether the tile kernel has an instantiation for MT x NT with scale grouping (mpw, npw). */
 int mxfp6_hip_has_tile(int MT, int NT, int mpw, int npw);
 

@@ -3,8 +3,11 @@
 // include/mxfp6_gemm.h). Plain C++17 with no HIP header: every device action goes through the
 // thin launch layer declared in hip_layer.h.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
+#include <mutex>
+#include <vector>
 
 #include "../hip_layer.h"
 #include "mxfp6/gemm.hpp"
@@ -129,15 +132,14 @@ const int kNSkinny = (int)(sizeof(kSkinny) / sizeof(kSkinny[0]));
 // src/kernel.hpp:144-154, for any tile: N = 102272 runs 256x256 over ceil(N/256) columns instead
 // of 128x128); ragged shapes any of the ten, big tiles first. Shapes gemm() rejects get the
 // trivial plan.
-Plan best_plan(int M, int N, int Kp, int cus) {
-    Plan best = {{128, 128, 2, 2}, 1, false};
-    if (!shape_ok(M, N, Kp)) return best;
-    double best_t = -1.0;
+// Calls f(tile, S, repack) for every plan the router considers for (M, N, Kp), in its visiting
+// order: big tiles first, then the skinny ones; on regular shapes only the tiles whose MT divides
+// M (so M % 128 != 0 leaves the skinny ones), the dividing tiles first, then (pass 1) the
+// N-masked ones.
+template <typename F>
+void visit_plans(int M, int N, int Kp, F&& f) {
     const int k_tiles = Kp / K_TILE;
     const bool reg = regular(M, N);
-    // big tiles first, then the skinny ones; on regular shapes only the tiles whose MT divides M
-    // (so M % 128 != 0 leaves the skinny ones), the dividing tiles first, then (pass 1) the
-    // N-masked ones
     for (int pass = 0; pass < (reg ? 2 : 1); pass++)
         for (int rp = 0; rp < 2; rp++)
             for (const int S : SPLIT_CHOICES)
@@ -148,12 +150,21 @@ Plan best_plan(int M, int N, int Kp, int cus) {
                     // holds floor(dim / (32 * group)) whole groups: the grouping must divide the
                     // shape (an N-masked 256x192 or 128x384, NPW 3, needs (N / 32) % 3 == 0)
                     if (reg && ((M / 32) % tc.MPW != 0 || (N / 32) % tc.NPW != 0)) continue;
-                    const double t = plan_time_us(tc, M, N, Kp, S, rp != 0, cus);
-                    if (best_t < 0 || t < best_t * (1.0 - PLAN_MIN_GAIN)) {
-                        best = {tc, S, rp != 0};
-                        best_t = t;
-                    }
+                    f(tc, S, rp != 0);
                 }
+}
+
+Plan best_plan(int M, int N, int Kp, int cus) {
+    Plan best = {{128, 128, 2, 2}, 1, false};
+    if (!shape_ok(M, N, Kp)) return best;
+    double best_t = -1.0;
+    visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
+        const double t = plan_time_us(tc, M, N, Kp, S, rp, cus);
+        if (best_t < 0 || t < best_t * (1.0 - PLAN_MIN_GAIN)) {
+            best = {tc, S, rp};
+            best_t = t;
+        }
+    });
     return best;
 }
 
@@ -176,6 +187,40 @@ Plan cached_plan(int M, int N, int Kp) {
     if (!e.valid || e.M != M || e.N != N || e.Kp != Kp || e.cus != cus)
         e = {M, N, Kp, cus, best_plan(M, N, Kp, cus), true};
     return e.plan;
+}
+
+// ---- measured plans (mxfp6_gemm_tune) ----------------------------------------------------------
+// tune() times the router's best-predicted plans of a shape on the caller's operands and keeps the
+// fastest for the process; gemm() then runs it whenever the call's workspace holds it. The table
+// is shared by all threads (a mutex, skipped while it is empty).
+struct Tuned {
+    int out_type, M, N, Kp;
+    Plan plan;
+};
+std::mutex g_tuned_mu;
+std::vector<Tuned> g_tuned;
+std::atomic<int> g_n_tuned{0};
+
+bool find_tuned(int out_type, int M, int N, int Kp, Plan* out) {
+    if (g_n_tuned.load(std::memory_order_acquire) == 0) return false;
+    std::lock_guard<std::mutex> lk(g_tuned_mu);
+    for (const Tuned& t : g_tuned)
+        if (t.out_type == out_type && t.M == M && t.N == N && t.Kp == Kp) {
+            *out = t.plan;
+            return true;
+        }
+    return false;
+}
+
+void store_tuned(int out_type, int M, int N, int Kp, const Plan& p) {
+    std::lock_guard<std::mutex> lk(g_tuned_mu);
+    for (Tuned& t : g_tuned)
+        if (t.out_type == out_type && t.M == M && t.N == N && t.Kp == Kp) {
+            t.plan = p;
+            return;
+        }
+    g_tuned.push_back({out_type, M, N, Kp, p});
+    g_n_tuned.store((int)g_tuned.size(), std::memory_order_release);
 }
 }  // namespace
 
@@ -311,14 +356,18 @@ int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void*
                  size_t ws_bytes, void* stream) {
     const int st = check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
     if (st != MXFP6_OK) return st;
-    const Plan pl = cached_plan(M, N, Kp);
+    if (ws == nullptr) ws_bytes = 0;
+    Plan pl = cached_plan(M, N, Kp);
+    Plan tuned;  // a measured plan of the shape, when the workspace holds it
+    if (find_tuned(out_type, M, N, Kp, &tuned) &&
+        ws_bytes >= ((tuned.S > 1 || tuned.repack) ? plan_bytes(M, N, Kp, tuned.S, tuned.repack) : 0))
+        pl = tuned;
     const TileChoice tc = pl.tc;
     int S = pl.S;
     bool rp = pl.repack;
     const int kernel = kernel_for(tc);
     if (kernel != MXFP6_KERNEL_TILE) rp = false;
     if (kernel != MXFP6_KERNEL_TILE && (M % 64 != 0 || N % 64 != 0)) return MXFP6_ERR_TILE;
-    if (ws == nullptr) ws_bytes = 0;
     // A workspace too small for the repacked A (gemm_workspace_size's, the partials only) drops
     // the repack, a pure speed choice with the same output bits; one too small for the split-K
     // partials as well runs unsplit, with the reference's warning.
@@ -332,6 +381,97 @@ int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void*
     }
     return run(out_type, M, N, Kp, tc, S, rp ? MXFP6_A_REPACK : MXFP6_A_ROWS, kernel, dA, dBsh, dsA,
                dsB, dD, A_row_bytes, ws, stream);
+}
+
+namespace {
+struct TuneCall {
+    int out_type, M, N, Kp, A_row_bytes;
+    Plan plan;
+    const void *dA, *dBsh;
+    const uint8_t *dsA, *dsB;
+    void *dD, *ws, *stream;
+};
+
+int tune_launch(void* ctx) {
+    const TuneCall& c = *static_cast<const TuneCall*>(ctx);
+    return run(c.out_type, c.M, c.N, c.Kp, c.plan.tc, c.plan.S,
+               c.plan.repack ? MXFP6_A_REPACK : MXFP6_A_ROWS, kernel_for(c.plan.tc), c.dA, c.dBsh,
+               c.dsA, c.dsB, c.dD, c.A_row_bytes, c.ws, c.stream);
+}
+}  // namespace
+
+int tune(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh, const uint8_t* dsA,
+         const uint8_t* dsB, void* dD, int A_row_bytes, void* ws, size_t ws_bytes,
+         int candidates, void* stream, int tile_out[4], int* splits_out, int* repack_out) {
+    const int st = check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
+    if (st != MXFP6_OK) return st;
+    if (candidates < 1) return MXFP6_ERR_ARG;
+    if (ws == nullptr) ws_bytes = 0;
+    const Plan routed = cached_plan(M, N, Kp);
+    if (kernel_for(routed.tc) != MXFP6_KERNEL_TILE) return MXFP6_ERR_TILE;
+    const int reported = mxfp6_hip_device_cus();
+    const int cus = reported > 0 ? reported : DEFAULT_CUS;
+    // the candidates: the plans with the routed tile's scale grouping (the caller's scales are
+    // tiled for it) whose workspace fits, by predicted time
+    struct Ranked {
+        double t;
+        Plan plan;
+    };
+    std::vector<Ranked> ranked;
+    visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
+        if (tc.MPW != routed.tc.MPW || tc.NPW != routed.tc.NPW) return;
+        if (kernel_for(tc) != MXFP6_KERNEL_TILE) return;
+        if ((S > 1 || rp) && ws_bytes < plan_bytes(M, N, Kp, S, rp)) return;
+        ranked.push_back({plan_time_us(tc, M, N, Kp, S, rp, cus), {tc, S, rp}});
+    });
+    std::stable_sort(ranked.begin(), ranked.end(),
+                     [](const Ranked& a, const Ranked& b) { return a.t < b.t; });
+    if (ranked.size() > (size_t)candidates) ranked.resize((size_t)candidates);
+    if (ranked.empty()) return MXFP6_ERR_ARG;
+    Plan best = ranked[0].plan;
+    float best_ms = -1.0f;
+    for (const Ranked& r : ranked) {
+        TuneCall c = {out_type, M, N, Kp, A_row_bytes, r.plan, dA, dBsh, dsA, dsB, dD, ws, stream};
+        // about 2 ms of launches per candidate, at least 3
+        const int reps = std::max(3, std::min(50, (int)(2000.0 / std::max(1.0, r.t))));
+        float ms = 0.0f;
+        const int rc = mxfp6_hip_time(tune_launch, &c, stream, 2, reps, &ms);
+        if (rc != 0) return rc == 2 ? MXFP6_ERR_HIP : rc;
+        if (best_ms < 0 || ms < best_ms) {
+            best_ms = ms;
+            best = r.plan;
+        }
+    }
+    store_tuned(out_type, M, N, Kp, best);
+    if (tile_out) {
+        tile_out[0] = best.tc.MT;
+        tile_out[1] = best.tc.NT;
+        tile_out[2] = best.tc.MPW;
+        tile_out[3] = best.tc.NPW;
+    }
+    if (splits_out) *splits_out = best.S;
+    if (repack_out) *repack_out = best.repack ? 1 : 0;
+    return MXFP6_OK;
+}
+
+int tuned(int out_type, int M, int N, int Kp, int tile_out[4], int* splits_out, int* repack_out) {
+    Plan p;
+    if (!find_tuned(out_type, M, N, Kp, &p)) return 0;
+    if (tile_out) {
+        tile_out[0] = p.tc.MT;
+        tile_out[1] = p.tc.NT;
+        tile_out[2] = p.tc.MPW;
+        tile_out[3] = p.tc.NPW;
+    }
+    if (splits_out) *splits_out = p.S;
+    if (repack_out) *repack_out = p.repack ? 1 : 0;
+    return 1;
+}
+
+void tune_reset() {
+    std::lock_guard<std::mutex> lk(g_tuned_mu);
+    g_tuned.clear();
+    g_n_tuned.store(0, std::memory_order_release);
 }
 
 bool tile_divides(const int tile[4], int M, int N) {
@@ -510,6 +650,23 @@ extern "C" int mxfp6_gemm_streams_output(int out_type, int M, int N, int Kp, int
                                 A_row_bytes)
                ? 1
                : 0;
+}
+
+extern "C" int mxfp6_gemm_tune(int out_type, int M, int N, int Kp, const void* dA,
+                               const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
+                               int A_row_bytes, void* ws, size_t ws_bytes, int candidates,
+                               void* stream, int tile[4], int* splits, int* a_repack) {
+    return plan::tune(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws, ws_bytes,
+                      candidates, stream, tile, splits, a_repack);
+}
+
+extern "C" int mxfp6_gemm_tuned_plan(int out_type, int M, int N, int Kp, int tile[4], int* splits,
+                                     int* a_repack) {
+    return plan::tuned(out_type, M, N, Kp, tile, splits, a_repack);
+}
+
+extern "C" void mxfp6_gemm_tune_reset(void) {
+    plan::tune_reset();
 }
 
 extern "C" size_t mxfp6_plan_workspace_size(int M, int N, int Kp, int splits, int a_repack) {

@@ -44,6 +44,11 @@ size_t preferred_workspace_bytes(int M, int N, int Kp);
 bool route_repacks(int M, int N, int Kp);
 bool streams_output(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, bool repack,
                     int A_row_bytes);
+int tune(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh, const uint8_t* dsA,
+         const uint8_t* dsB, void* dD, int A_row_bytes, void* ws, size_t ws_bytes,
+         int candidates, void* stream, int tile_out[4], int* splits_out, int* repack_out);
+int tuned(int out_type, int M, int N, int Kp, int tile_out[4], int* splits_out, int* repack_out);
+void tune_reset();
 size_t plan_bytes(int M, int N, int Kp, int S, bool repack);
 int check_common(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
                  const void* dsA, const void* dsB, const void* dD, int A_row_bytes);

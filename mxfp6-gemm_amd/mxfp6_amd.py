@@ -56,6 +56,13 @@ SIGNATURES = {
                                       C.c_size_t, _vp]),
     "mxfp6_gemm_repacks_a": (C.c_int, [C.c_int, C.c_int, C.c_int]),
     "mxfp6_gemm_streams_output": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "mxfp6_gemm_tune": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                  C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                  C.c_size_t, C.c_int, C.c_void_p, C.POINTER(C.c_int),
+                                  C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "mxfp6_gemm_tuned_plan": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
+                                        C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "mxfp6_gemm_tune_reset": (None, []),
     "mxfp6_plan_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "mxfp6_preshuffle_rows_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "mxfp6_quantize_async": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_size_t, _vp, C.c_int, _vp]),
@@ -198,6 +205,30 @@ def gemm_explicit(out_type, M, N, Kp, tile, splits, dA, dBsh, dsA, dsB, dD, A_ro
 def repacks_a(M, N, Kp):
     """Whether gemm() repacks A into the preshuffled layout for this shape."""
     return bool(lib().mxfp6_gemm_repacks_a(M, N, Kp))
+
+
+def gemm_tune(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws=0, ws_bytes=0,
+              candidates=4, stream=None):
+    """Times the router's best-predicted plans on these operands and keeps the fastest for later
+    gemm() calls of the shape; returns (status, (tile, splits, a_repack))."""
+    t = (C.c_int * 4)()
+    s, r = C.c_int(0), C.c_int(0)
+    rc = lib().mxfp6_gemm_tune(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws or None,
+                               ws_bytes, candidates, stream, t, C.byref(s), C.byref(r))
+    return rc, (tuple(t), s.value, bool(r.value))
+
+
+def tuned_plan(out_type, M, N, Kp):
+    """(tile, splits, a_repack) chosen by gemm_tune for this shape, or None."""
+    t = (C.c_int * 4)()
+    s, r = C.c_int(0), C.c_int(0)
+    if not lib().mxfp6_gemm_tuned_plan(out_type, M, N, Kp, t, C.byref(s), C.byref(r)):
+        return None
+    return tuple(t), s.value, bool(r.value)
+
+
+def tune_reset():
+    lib().mxfp6_gemm_tune_reset()
 
 
 def streams_output(out_type, M, N, Kp, A_row_bytes):
