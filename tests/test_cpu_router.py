@@ -293,3 +293,11 @@ def test_streaming_rule(mx):
     for (M, N, K), ot, want in cases:
         Kp = mx.kpad(K)
         assert mx.streams_output(ot, M, N, Kp, mx.packed_bytes(K)) == want, (M, N, K)
+
+
+def test_no_measured_plan_without_tuning(mx):
+    """The measured-plan table starts empty and the reset empties it (mxfp6_gemm_tune, which
+    fills it, needs a GPU)."""
+    mx.tune_reset()
+    assert mx.tuned_plan(1, 1024, 1024, 1152) is None
+    assert mx.tuned_plan(0, 8192, 8192, 8256) is None
