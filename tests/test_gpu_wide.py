@@ -17,12 +17,13 @@ WIDE_TILES = [(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4
 
 
 @pytest.mark.parametrize("WIDE", WIDE_TILES)
-@pytest.mark.parametrize("tm,tn,K", [(2, 2, 2112), (1, 1, 192), (1, 4, 4224), (3, 3, 3456)])
+@pytest.mark.parametrize("tm,tn,K", [(2, 2, 2112), (1, 1, 192), (1, 4, 4224), (3, 3, 3456),
+                                     (2, 1, 384), (1, 2, 576)])
 @pytest.mark.parametrize("a_layout", [0, 1])
 def test_wide_bitwise_equals_direct(WIDE, tm, tn, K, a_layout):
-    """tm x tn tiles (M, N multiples of 256 and of the tile); the K-tile counts 11, 1, 22 and 18:
-    the 256 x 256 tile's K loop runs K-tiles in pairs, so odd counts take its single-K-tile
-    tail."""
+    """tm x tn tiles (M, N multiples of 256 and of the tile); the K-tile counts 11, 1, 22, 18, 2
+    and 3: the 256 x 256 tile's K loop runs K-tiles in pairs, so odd counts take its
+    single-K-tile tail; with 2 and 3 K-tiles most prefetches are clamped to the last K-tile."""
     M, N = 256 * tm, WIDE[1] * tn
     p = mx.make_problem(M, N, K, seed=M + N + K + a_layout)
     dp = g.DevProblem(p, WIDE)
