@@ -12,8 +12,9 @@ drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX 
   python bench.py --prep      (device operand preparation: float -> MXFP6 device layouts, GB/s)
   python bench.py --power S   (board power and clocks over S seconds of back-to-back GEMMs of the
                                workload, this library then the reference library; amd-smi)
-  python bench.py --map [SHAPES]  (this library against the reference library, shape by shape:
-                               MxNxK,... or the default map of 154 shapes, FP16 out)
+  python bench.py --map [SHAPES] [--repeat R]  (this library against the reference library,
+                               shape by shape: MxNxK,... or the default map of 154 shapes, FP16
+                               out; R > 1: R more runs per library, alternating their order)
 
 Prints one JSON line per workload (only the default one unless --all). The headline `value` is
 the mean over exactly K timed steps after W warm-up steps (no extra warm-up: an idle MI355X sits
@@ -561,9 +562,11 @@ def default_map():
     return shapes + [s for s in sorted(drawn) if s not in shapes]
 
 
-def run_map(spec):
+def run_map(spec, repeat=1):
     """This library and the reference library on the same operands, shape by shape, by the
-    reference's timing method (compare()); one JSON line per shape, then a summary line."""
+    reference's timing method (compare()); one JSON line per shape, then a summary line. With
+    repeat > 1 each shape is timed `repeat` more times per library, alternating which library
+    runs first, and the line also carries both series and the ratio of their medians."""
     import torch
     ref = reference_library()
     if ref is None:
@@ -578,10 +581,22 @@ def run_map(spec):
     for i, sh in enumerate(shapes):
         w = Workload(f"{sh[0]}x{sh[1]}x{sh[2]}", ref, shape=sh)
         c = compare(w, stream)
-        ratios.append(c["ratio"])
-        print(json.dumps({"shape": list(sh), "tile": c["tile"], "splitk": c["splitk"],
-                          "a_repacked": c["a_repacked"], "us": c["us"], "ref_tile": c["ref_tile"],
-                          "ref_us": c["ref_us"], "ratio": c["ratio"]}), flush=True)
+        line = {"shape": list(sh), "tile": c["tile"], "splitk": c["splitk"],
+                "a_repacked": c["a_repacked"], "us": c["us"], "ref_tile": c["ref_tile"],
+                "ref_us": c["ref_us"], "ratio": c["ratio"]}
+        if repeat > 1:
+            null = torch.cuda.default_stream()
+            runs = {"ours": [], "ref": []}
+            for r in range(repeat):
+                order = [("ours", lambda: w.ours(stream), stream),
+                         ("ref", lambda: w.theirs(null), null)]
+                for tag, fn, s in (order if r % 2 == 0 else order[::-1]):
+                    runs[tag].append(round(best_of(fn, s)[0] * 1e3, 2))
+            line.update({"repeat_us": runs["ours"], "repeat_ref_us": runs["ref"],
+                         "ratio_median": round(float(np.median(runs["ref"])) /
+                                               float(np.median(runs["ours"])), 3)})
+        ratios.append(line.get("ratio_median", c["ratio"]))
+        print(json.dumps(line), flush=True)
         del w
         torch.cuda.empty_cache()
     gm = float(np.exp(np.mean(np.log(ratios))))
@@ -693,6 +708,9 @@ def main():
     ap.add_argument("--map", nargs="?", const="", default=None, metavar="SHAPES",
                     help="this library against the reference library shape by shape instead "
                          "(MxNxK,... or a file of them; default: 154 shapes)")
+    ap.add_argument("--repeat", type=int, default=1, metavar="R",
+                    help="with --map: time each shape R more times per library, alternating "
+                         "which runs first, and summarise by the ratio of the medians")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on exactly one GPU; --gpus {a.gpus} is not supported (the MXFP6 "
@@ -709,7 +727,7 @@ def main():
         print(json.dumps(run_power(a.config, a.power)), flush=True)
         return
     if a.map is not None:
-        run_map(a.map)
+        run_map(a.map, a.repeat)
         return
     names = sorted(CONFIGS, key=lambda n: n != a.config) if a.all else [a.config]
     run(names, a.steps, a.warmup, not a.no_cpu, not a.no_ref, not a.no_per_config and not a.all)

@@ -32,7 +32,10 @@
 // current one is free for the copies of K-tile c + NB - 1. The B loads and scale loads are
 // ordinary loads whose waits the compiler places before the MFMAs that use them.
 // Prefetches past the workgroup's last K-tile are clamped to that K-tile (valid addresses, data
-// never used), so the K loop has no branch. MASK (ragged M or N) clamps the copy and load sources
+// never used), so the K loop has no branch. A 128 x 256 workgroup with exactly two K-tiles
+// (K <= 384, or a split segment of two) takes a short path instead: both K-tiles' chunks, scales
+// and B operands (a second register set) are requested before the first MFMA, so K-tile 1 does
+// not wait out a memory latency for B loads issued during K-tile 0. MASK (ragged M or N) clamps the copy and load sources
 // of the last tile row and column and masks the stores, as in the slab kernel.
 #pragma once
 
@@ -84,6 +87,14 @@ struct WideGeom {
     // In the prologue: after chunk 0's copies, those of chunks 1 .. NB - 2, the scale loads of
     // K-tile 0 and the B loads of its three slabs.
     static constexpr int PRO_WAIT = (NB - 2) * A_ISS + NGA + 1 + SUBS * 2 * NPW;
+    // Two K-tiles (wide_kernel's short path): everything is loaded up front, chunk 0, the scales
+    // and B operands of K-tile 0, chunk 1, the scales and B operands of K-tile 1; issued after
+    // chunk 1, and after chunk 0
+    static constexpr int TWO_CHUNK1_WAIT = NGA + 1 + SUBS * 2 * NPW;
+    static constexpr int TWO_PRO_WAIT = NGA + 1 + SUBS * 2 * NPW + A_ISS + TWO_CHUNK1_WAIT;
+    // the short path holds a second set of B operands: built for the 128 x 256 tile only (the
+    // others have no registers to spare)
+    static constexpr bool TWO_PATH = MB == 4 && NPW == 2;
     static_assert(MB == 4 || MB == 8, "128 or 256 rows");
     static_assert(NPW >= 1 && NPW <= 4, "B scale group holds <= 4 blocks");
     // NB = 3: the prologue issues chunk 1 before the loop, and the count above then holds for
@@ -93,7 +104,7 @@ struct WideGeom {
     static_assert(cps(0) + cps(1) + cps(2) == A_ISS && cps(2) >= 1, "copies per K-tile");
     static_assert(copy_k(cps(0) - 1) < NMF, "copy positions");
     static_assert(read_k(MB - 1) < NMF, "read positions");
-    static_assert(CHUNK_WAIT <= 63 && PRO_WAIT <= 63, "vmcnt range");
+    static_assert(CHUNK_WAIT <= 63 && PRO_WAIT <= 63 && TWO_PRO_WAIT <= 63, "vmcnt range");
 };
 
 // acc[mi][ni] += A(mi) * B(ni) with the scale bytes mi % 4 of sa and ni of sb (op_sel must be a
@@ -244,6 +255,86 @@ __global__ void __launch_bounds__(256, 1)
     v8i RA[NSET][MB];      // A operands
     v3i sc_a[NGA], sc_b;   // scale dwords of the current K-tile
     v3i sn_a[NGA], sn_b;   // and of the next one
+
+    if constexpr (G::TWO_PATH) {
+        if (nkt == 2) {
+            // Two K-tiles (K <= 384, or a split segment of two): both K-tiles' chunks, scales and
+            // B operands are requested before the first MFMA, so K-tile 1 does not wait for loads
+            // issued during K-tile 0; no K-tile follows, so nothing is clamped and K-tile 1 needs
+            // no barrier.
+            v8i RB1[SUBS][NPW];
+            v3i s1_a[NGA], s1_b;
+#pragma unroll
+            for (int i = 0; i < G::A_ISS; i++) a_copy(i, kt0, 0);
+            load_scales(sc_a, sc_b, kt0);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < SUBS; s++)
+#pragma unroll
+                for (int ni = 0; ni < NPW; ni++) {
+                    load_b(RB[s][ni], ni, kt0, s);
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+            for (int i = 0; i < G::A_ISS; i++) a_copy(i, kt0 + 1, 1);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            load_scales(s1_a, s1_b, kt0 + 1);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < SUBS; s++)
+#pragma unroll
+                for (int ni = 0; ni < NPW; ni++) {
+                    load_b(RB1[s][ni], ni, kt0 + 1, s);
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            wait_vmcnt<G::TWO_PRO_WAIT>();  // chunk 0 landed
+            ring_barrier();
+#pragma unroll
+            for (int mi = 0; mi < MB; mi++) read_a(RA[0][mi], 0, 0, mi);
+            // K-tile F (0 or 1) from LDS buffer F; slab s uses A set s (three sets)
+            auto two_ktile = [&](auto first) {
+                constexpr bool F0 = decltype(first)::value;
+#pragma unroll
+                for (int s = 0; s < SUBS; s++) {
+                    if (F0 && s == SUBS - 1) {
+                        wait_vmcnt<G::TWO_CHUNK1_WAIT>();  // chunk 1 complete for every wave
+                        ring_barrier();
+                    }
+                    const int nxt = (s + 1) % SUBS;
+                    const int rbuf = s + 1 < SUBS ? (F0 ? 0 : 1) : 1;
+                    const int rs = s + 1 < SUBS ? s + 1 : 0;
+#pragma unroll
+                    for (int k = 0; k < NMF; k++) {
+                        const int ni = k / MB, mi = k % MB;
+                        const int g = mi / GA;
+                        const v3i& xa = F0 ? sc_a[g] : s1_a[g];
+                        const v3i& xb = F0 ? sc_b : s1_b;
+                        const int sa = s == 0 ? xa.x : s == 1 ? xa.y : xa.z;
+                        const int sb = s == 0 ? xb.x : s == 1 ? xb.y : xb.z;
+                        wide_mfma<MB, NPW>(acc, mi, ni, RA[s][mi], F0 ? RB[s][ni] : RB1[s][ni],
+                                           sa, sb);
+#pragma unroll
+                        for (int i = 0; i < MB; i++)
+                            if (k == G::read_k(i) && (F0 || s + 1 < SUBS))
+                                read_a(RA[nxt][i], rbuf, rs, i);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+            };
+            two_ktile(std::true_type{});
+            two_ktile(std::false_type{});
+            store_tile<MB, NPW, OutT, SPLIT, MASK, STREAM>(acc, D, ws, M, N,
+                                                        wg_m * MT + 4 * (lane >> 5),
+                                                        wg_n * NT + wave * NPW * 32 + (lane & 31),
+                                                        lane, wg_z);
+            return;
+        }
+    }
 
     // prologue: what the first MFMAs need first (chunk 0, the scales of K-tile 0, the B operands
     // of its slab 0), then chunks 1 .. NB-2 and the B operands of slabs 1 and 2 (the compiler,
