@@ -148,6 +148,16 @@ int mxfp6_gemm_tuned_plan(int out_type, int M, int N, int Kp, int tile[4], int* 
 /* Forgets every measured plan (gemm() runs the router's plans again). */
 void mxfp6_gemm_tune_reset(void);
 
+/* The plan gemm() runs for (out_type, M, N, Kp) with a workspace of ws_bytes: tile {MT, NT, MPW,
+ * NPW}, K segments and whether A is repacked first. A measured plan when the workspace holds it,
+ * else the routed plan when the workspace holds it, else the fastest predicted plan with the
+ * routed scale grouping (the tile choose_tile returns fixes the scale layout) that fits
+ * gemm_workspace_size's workspace when ws_bytes holds that, or else one that needs none. Unsplit
+ * plans of one scale grouping give the same output bits. No counterpart in the reference (its
+ * dispatch runs choose_tile's tile, unsplit when the workspace is short, src/dispatch.hpp:74-87). */
+int mxfp6_gemm_plan(int out_type, int M, int N, int Kp, size_t ws_bytes, int tile[4], int* splits,
+                    int* a_repack);
+
 /* Whether gemm()'s plan for (out_type, M, N, Kp, A_row_bytes) writes D with nontemporal stores
  * (unsplit plans whose operands fit in MI355X's 256 MiB last-level cache but whose operands and D
  * together do not). No counterpart in the reference (its epilogue stores are plain); D's values

@@ -68,15 +68,28 @@ namespace plan {
 // the best on four of the five benchmark workloads (2048x6144x16128: 6% behind the 128x384
 // tile on the sweep's machine); on the 16 skinny-M and ragged shapes within 2.3% on average,
 // 10% at worst.
+size_t split_bytes(int M, int N, int S);
+size_t plan_bytes(int M, int N, int Kp, int S, bool repack);
+
+// Whether a workspace of ws_bytes holds a plan's buffers: the split-K partials (exactly
+// gemm_workspace_size's bytes for the routed split), or the partials rounded to 256 bytes and the
+// repacked A after them.
+bool plan_fits(int M, int N, int Kp, int S, bool repack, size_t ws_bytes) {
+    return ws_bytes >= (repack ? plan_bytes(M, N, Kp, S, true) : split_bytes(M, N, S));
+}
+
 namespace {
 struct Plan {
     TileChoice tc;
     int S;
     bool repack;
 };
-const TileChoice kCands[] = {{256, 256, 4, 4}, {256, 192, 4, 3}, {128, 384, 4, 3},
-                             {128, 256, 2, 4}, {128, 128, 2, 2}, {128, 512, 4, 4},
-                             {128, 256, 4, 2}, {256, 256, 4, 2}};
+// 256x192 (slab kernel) is implemented but not routed: the best measured plan on 1 of 194 swept
+// shapes (by 3.5%), while the model picked it, repacked, on shapes where 128x384 on row-major A
+// is 4-10% faster (2048x12288x4096, 3072x6144x8192, 6144x6144x8192, 2048x9216x16384)
+const TileChoice kCands[] = {{256, 256, 4, 4}, {128, 384, 4, 3}, {128, 256, 2, 4},
+                             {128, 128, 2, 2}, {128, 512, 4, 4}, {128, 256, 4, 2},
+                             {256, 256, 4, 2}};
 const TileChoice kSkinny[] = {{64, 256, 2, 2}, {32, 256, 1, 2}, {64, 128, 2, 1}, {32, 128, 1, 1}};
 
 // The tiles of the wide kernel (B loaded into registers, A staged per K-tile).
@@ -168,15 +181,40 @@ Plan best_plan(int M, int N, int Kp, int cus) {
     return best;
 }
 
+// The least-time plan with the scale grouping of `grouping` whose workspace fits ws_bytes: what
+// gemm() runs when the caller's workspace does not hold the routed plan (gemm_workspace_size's
+// workspace, the split-K partials only, or none). The unsplit row-major plans always fit, and any
+// unsplit plan of a grouping gives the same output bits (same MFMAs in the same K order).
+Plan best_fitting_plan(int M, int N, int Kp, int cus, const TileChoice& grouping, size_t ws_bytes) {
+    Plan best = {grouping, 1, false};
+    double best_t = -1.0;
+    visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
+        if (tc.MPW != grouping.MPW || tc.NPW != grouping.NPW) return;
+        if (!plan_fits(M, N, Kp, S, rp, ws_bytes)) return;
+        const double t = plan_time_us(tc, M, N, Kp, S, rp, cus);
+        if (best_t < 0 || t < best_t * (1.0 - PLAN_MIN_GAIN)) {
+            best = {tc, S, rp};
+            best_t = t;
+        }
+    });
+    return best;
+}
+
 // best_plan evaluates the model for every (tile, split, layout): a few microseconds of host time,
 // as long as a small GEMM runs on the GPU. gemm() and the routing queries look the plan up in a
 // per-thread cache of the last shapes instead (16 entries indexed by a hash of the shape; no
 // lock, and the plan of a shape on a device never changes). The key includes the compute-unit
 // count of the current device, which the HIP layer reads once per device.
-Plan cached_plan(int M, int N, int Kp) {
+// The cached entry of a shape: the routed plan, and the plans gemm() falls back to with
+// gemm_workspace_size's workspace (ref_ws) and with none (no_ws).
+struct Routed {
+    Plan plan, ref_ws, no_ws;
+};
+
+const Routed& cached_routes(int M, int N, int Kp) {
     struct Entry {
         int M, N, Kp, cus;
-        Plan plan;
+        Routed r;
         bool valid;
     };
     thread_local Entry cache[16] = {};
@@ -184,9 +222,18 @@ Plan cached_plan(int M, int N, int Kp) {
     const int cus = reported > 0 ? reported : DEFAULT_CUS;
     const unsigned h = ((unsigned)M * 73856093u ^ (unsigned)N * 19349663u ^ (unsigned)Kp * 83492791u) >> 4;
     Entry& e = cache[h % 16];
-    if (!e.valid || e.M != M || e.N != N || e.Kp != Kp || e.cus != cus)
-        e = {M, N, Kp, cus, best_plan(M, N, Kp, cus), true};
-    return e.plan;
+    if (!e.valid || e.M != M || e.N != N || e.Kp != Kp || e.cus != cus) {
+        const Plan pl = best_plan(M, N, Kp, cus);
+        const Plan none = best_fitting_plan(M, N, Kp, cus, pl.tc, 0);
+        const Plan ref = pl.S > 1 ? best_fitting_plan(M, N, Kp, cus, pl.tc, split_bytes(M, N, pl.S))
+                                  : none;
+        e = {M, N, Kp, cus, {pl, ref, none}, true};
+    }
+    return e.r;
+}
+
+Plan cached_plan(int M, int N, int Kp) {
+    return cached_routes(M, N, Kp).plan;
 }
 
 // ---- measured plans (mxfp6_gemm_tune) ----------------------------------------------------------
@@ -351,36 +398,46 @@ int kernel_for(const TileChoice& tc) {
                                                             : MXFP6_KERNEL_DIRECT;
 }
 
+Plan plan_for(int out_type, int M, int N, int Kp, size_t ws_bytes, bool* unsplit);
+
 int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh,
                  const uint8_t* dsA, const uint8_t* dsB, void* dD, int A_row_bytes, void* ws,
                  size_t ws_bytes, void* stream) {
     const int st = check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
     if (st != MXFP6_OK) return st;
     if (ws == nullptr) ws_bytes = 0;
-    Plan pl = cached_plan(M, N, Kp);
-    Plan tuned;  // a measured plan of the shape, when the workspace holds it
-    if (find_tuned(out_type, M, N, Kp, &tuned) &&
-        ws_bytes >= ((tuned.S > 1 || tuned.repack) ? plan_bytes(M, N, Kp, tuned.S, tuned.repack) : 0))
-        pl = tuned;
-    const TileChoice tc = pl.tc;
-    int S = pl.S;
-    bool rp = pl.repack;
-    const int kernel = kernel_for(tc);
-    if (kernel != MXFP6_KERNEL_TILE) rp = false;
-    if (kernel != MXFP6_KERNEL_TILE && (M % 64 != 0 || N % 64 != 0)) return MXFP6_ERR_TILE;
-    // A workspace too small for the repacked A (gemm_workspace_size's, the partials only) drops
-    // the repack, a pure speed choice with the same output bits; one too small for the split-K
-    // partials as well runs unsplit, with the reference's warning.
-    if (rp && ws_bytes < plan_bytes(M, N, Kp, S, true)) rp = false;
-    if (S > 1 && ws_bytes < plan_bytes(M, N, Kp, S, false)) {
+    bool unsplit = false;
+    const Plan pl = plan_for(out_type, M, N, Kp, ws_bytes, &unsplit);
+    if (unsplit)
         std::fprintf(stderr,
                      "[mxfp6] %dx%dx%d: split-K over %d segments needs a %zu-byte workspace, "
                      "got %zu; running unsplit. Size it with gemm_workspace_size().\n",
-                     M, N, Kp, S, split_bytes(M, N, S), ws_bytes);
-        S = 1;
-    }
-    return run(out_type, M, N, Kp, tc, S, rp ? MXFP6_A_REPACK : MXFP6_A_ROWS, kernel, dA, dBsh, dsA,
-               dsB, dD, A_row_bytes, ws, stream);
+                     M, N, Kp, splitk_segments(M, N, Kp), workspace_bytes(M, N, Kp), ws_bytes);
+    const int kernel = kernel_for(pl.tc);
+    const bool rp = pl.repack && kernel == MXFP6_KERNEL_TILE;
+    if (kernel != MXFP6_KERNEL_TILE && (M % 64 != 0 || N % 64 != 0)) return MXFP6_ERR_TILE;
+    return run(out_type, M, N, Kp, pl.tc, pl.S, rp ? MXFP6_A_REPACK : MXFP6_A_ROWS, kernel, dA,
+               dBsh, dsA, dsB, dD, A_row_bytes, ws, stream);
+}
+
+// The plan gemm() runs for a workspace of ws_bytes: a measured plan of the shape when the
+// workspace holds it; else the routed plan when the workspace holds it; else the fastest
+// predicted plan with the routed scale grouping that fits gemm_workspace_size's workspace (the
+// split-K partials only) when ws_bytes holds that, or else one that needs none (*unsplit set when
+// the routed plan was split: the reference's warning case). Falling back changes neither the
+// scale layout the caller prepared nor, for an unsplit plan, the output bits.
+Plan plan_for(int out_type, int M, int N, int Kp, size_t ws_bytes, bool* unsplit) {
+    if (unsplit != nullptr) *unsplit = false;
+    Plan tuned;
+    if (find_tuned(out_type, M, N, Kp, &tuned) &&
+        plan_fits(M, N, Kp, tuned.S, tuned.repack, ws_bytes))
+        return tuned;
+    const Routed& r = cached_routes(M, N, Kp);
+    const Plan& pl = r.plan;
+    if (plan_fits(M, N, Kp, pl.S, pl.repack, ws_bytes)) return pl;
+    if (ws_bytes >= split_bytes(M, N, pl.S)) return r.ref_ws;
+    if (unsplit != nullptr) *unsplit = pl.S > 1;
+    return r.no_ws;
 }
 
 namespace {
@@ -421,7 +478,7 @@ int tune(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh, c
     visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
         if (tc.MPW != routed.tc.MPW || tc.NPW != routed.tc.NPW) return;
         if (kernel_for(tc) != MXFP6_KERNEL_TILE) return;
-        if ((S > 1 || rp) && ws_bytes < plan_bytes(M, N, Kp, S, rp)) return;
+        if (!plan_fits(M, N, Kp, S, rp, ws_bytes)) return;
         ranked.push_back({plan_time_us(tc, M, N, Kp, S, rp, cus), {tc, S, rp}});
     });
     std::stable_sort(ranked.begin(), ranked.end(),
@@ -466,6 +523,18 @@ int tuned(int out_type, int M, int N, int Kp, int tile_out[4], int* splits_out, 
     if (splits_out) *splits_out = p.S;
     if (repack_out) *repack_out = p.repack ? 1 : 0;
     return 1;
+}
+
+int plan_info(int out_type, int M, int N, int Kp, size_t ws_bytes, int tile_out[4],
+              int* splits_out, int* repack_out) {
+    const Plan pl = plan_for(out_type, M, N, Kp, ws_bytes, nullptr);
+    tile_out[0] = pl.tc.MT;
+    tile_out[1] = pl.tc.NT;
+    tile_out[2] = pl.tc.MPW;
+    tile_out[3] = pl.tc.NPW;
+    *splits_out = pl.S;
+    *repack_out = pl.repack && kernel_for(pl.tc) == MXFP6_KERNEL_TILE ? 1 : 0;
+    return MXFP6_OK;
 }
 
 void tune_reset() {
@@ -667,6 +736,14 @@ extern "C" int mxfp6_gemm_tuned_plan(int out_type, int M, int N, int Kp, int til
 
 extern "C" void mxfp6_gemm_tune_reset(void) {
     plan::tune_reset();
+}
+
+extern "C" int mxfp6_gemm_plan(int out_type, int M, int N, int Kp, size_t ws_bytes, int tile[4],
+                               int* splits, int* a_repack) {
+    if (out_type < 0 || out_type > 2 || M <= 0 || N <= 0 || Kp <= 0 || Kp % K_TILE != 0)
+        return MXFP6_ERR_ARG;
+    if (tile == nullptr || splits == nullptr || a_repack == nullptr) return MXFP6_ERR_NULL;
+    return plan::plan_info(out_type, M, N, Kp, ws_bytes, tile, splits, a_repack);
 }
 
 extern "C" size_t mxfp6_plan_workspace_size(int M, int N, int Kp, int splits, int a_repack) {

@@ -63,6 +63,8 @@ SIGNATURES = {
     "mxfp6_gemm_tuned_plan": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
                                         C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "mxfp6_gemm_tune_reset": (None, []),
+    "mxfp6_gemm_plan": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_size_t,
+                                  C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "mxfp6_plan_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "mxfp6_preshuffle_rows_async": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "mxfp6_quantize_async": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_size_t, _vp, C.c_int, _vp]),
@@ -229,6 +231,16 @@ def tuned_plan(out_type, M, N, Kp):
 
 def tune_reset():
     lib().mxfp6_gemm_tune_reset()
+
+
+def gemm_plan(out_type, M, N, Kp, ws_bytes):
+    """(tile, splits, a_repack) that gemm() runs for this shape with a workspace of ws_bytes."""
+    t = (C.c_int * 4)()
+    s, r = C.c_int(0), C.c_int(0)
+    rc = lib().mxfp6_gemm_plan(out_type, M, N, Kp, ws_bytes, t, C.byref(s), C.byref(r))
+    if rc != 0:
+        raise ValueError(f"mxfp6_gemm_plan: {STATUS.get(rc, rc)}")
+    return tuple(t), s.value, bool(r.value)
 
 
 def streams_output(out_type, M, N, Kp, A_row_bytes):

@@ -17,8 +17,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CUS = 256
 K_TILE = 192
 SPLIT_CHOICES = (1, 2, 3, 4, 6, 8, 12, 16)
-TILES = [(256, 256, 4, 4), (256, 192, 4, 3), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2),
-         (128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2)]
+# the routed tiles (256x192 is implemented but not routed: plan.cpp kCands)
+TILES = [(256, 256, 4, 4), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2), (128, 512, 4, 4),
+         (128, 256, 4, 2), (256, 256, 4, 2)]
 # the tiles whose B goes straight to registers (wide_kernel.hpp)
 WIDE = {(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4, 2)}
 SKINNY = [(64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)]

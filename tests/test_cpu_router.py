@@ -301,3 +301,40 @@ def test_no_measured_plan_without_tuning(mx):
     mx.tune_reset()
     assert mx.tuned_plan(1, 1024, 1024, 1152) is None
     assert mx.tuned_plan(0, 8192, 8192, 8256) is None
+
+
+def test_plan_for_every_workspace(mx):
+    """mxfp6_gemm_plan: the plan gemm() runs keeps choose_tile's scale grouping (the caller's
+    scales are tiled for it), fits the workspace it is given, is the routed plan itself with the
+    preferred workspace, and with none is unsplit on row-major A; 256x192 is never routed."""
+    shapes = [(M, N, K) for M in (128, 1024, 2048, 3072, 6144) for N in (1024, 6144, 9216, 12288)
+              for K in (256, 4096, 16128, 105728)] + [(97, 1000, 2112), (300, 700, 960),
+                                                       (2048, 1024, 105728), (2048, 5120, 105728)]
+    for M, N, K in shapes:
+        Kp = _kpad(K)
+        t = tuple(mx.choose_tile(M, N, Kp))
+        assert t != (256, 192, 4, 3), (M, N, K)
+        S, rp = mx.splitk_segments(M, N, Kp), mx.repacks_a(M, N, Kp)
+        pref = mx.preferred_workspace_size(M, N, Kp)
+        ref = mx.workspace_size(M, N, Kp)
+        assert mx.gemm_plan(1, M, N, Kp, pref) == (t, S, rp), (M, N, K)
+        for ws in (0, ref, pref, max(ref - 1, 0)):
+            pt, ps, prp = mx.gemm_plan(1, M, N, Kp, ws)
+            assert pt[2:] == t[2:], (M, N, K, ws, pt, t)
+            assert mx.plan_workspace_size(M, N, Kp, ps, int(prp)) <= ws or (not prp and
+                   ps * M * N * 4 <= ws) or (ps == 1 and not prp), (M, N, K, ws, ps, prp)
+        pt, ps, prp = mx.gemm_plan(1, M, N, Kp, 0)
+        assert ps == 1 and not prp, (M, N, K)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 12288, 4096), (3072, 6144, 8192), (6144, 6144, 8192),
+                                   (2048, 9216, 16384)])
+def test_former_256x192_routes(mx, M, N, K):
+    """Shapes the router once sent to 256x192 with a repacked A (measured 4-10% slower than
+    128x384 on row-major A, and 25-45% slower when gemm_workspace_size's workspace dropped the
+    repack): a wide tile now, and row-major unsplit with the reference-sized workspace."""
+    Kp = _kpad(K)
+    t = tuple(mx.choose_tile(M, N, Kp))
+    assert t in {(128, 384, 4, 3), (256, 256, 4, 2), (128, 512, 4, 4), (128, 256, 4, 2)}, t
+    pt, ps, prp = mx.gemm_plan(1, M, N, Kp, mx.workspace_size(M, N, Kp))
+    assert pt[2:] == t[2:] and not prp

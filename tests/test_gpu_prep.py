@@ -249,10 +249,12 @@ def test_prepare_a_preshuffled(mx, M, K, group):
     ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=DEV)
     assert mx.gemm(0, M, N, Kp, rows.data_ptr(), db.data_ptr(), t_rows.data_ptr(), dsb.data_ptr(),
                    D1.data_ptr(), rb, ws.data_ptr(), wsb) == 0
-    S = mx.splitk_segments(M, N, Kp)
+    # the plan gemm() runs with that workspace (the routed scale grouping, row-major A)
+    ftile, S, _ = mx.gemm_plan(0, M, N, Kp, wsb)
+    assert ftile[2:] == tuple(tile)[2:]
     wse = mx.plan_workspace_size(M, N, Kp, S, 0)
     wsx = torch.empty(max(wse, 4), dtype=torch.uint8, device=DEV)
-    assert mx.gemm_explicit(0, M, N, Kp, tile, S, ash.data_ptr(), db.data_ptr(), t_sh.data_ptr(),
+    assert mx.gemm_explicit(0, M, N, Kp, ftile, S, ash.data_ptr(), db.data_ptr(), t_sh.data_ptr(),
                             dsb.data_ptr(), D2.data_ptr(), rb, wsx.data_ptr() if wse else 0, wse,
                             a_layout=2) == 0
     assert np.array_equal(host(D1), host(D2))

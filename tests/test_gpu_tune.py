@@ -66,13 +66,16 @@ def test_tuned_plan_is_used_and_correct(orc, M, N, K):
     checks.check(got[rows], R, ab, ot)
 
     # gemm_workspace_size's workspace (the router's partials only), too small for the measured
-    # plan: the router's plan on row-major A
+    # plan: the plan mxfp6_gemm_plan names for it (routed scale grouping, fits the workspace)
     small = mx.workspace_size(M, N, p.Kp)
     if mx.plan_workspace_size(M, N, p.Kp, S, int(rp)) > small:
+        ft, fs, frp = mx.gemm_plan(ot, M, N, p.Kp, small)
+        assert ft[2:] == routed[2:] and not frp
         got_small = _gemm(dp, ot, small)
-        want_r = run_explicit(dp, ot, splits=mx.splitk_segments(M, N, p.Kp), a_layout=0)
+        dp_f = DevProblem(p, ft) if ft != routed else dp
+        want_r = run_explicit(dp_f, ot, splits=fs, a_layout=0)
         assert (got_small.view("u4") == want_r.view("u4")).all(), "no fallback to the router"
-        say("    with the router's workspace: the router's plan")
+        say(f"    with the router's workspace: {ft} S {fs}")
 
     mx.tune_reset()
     assert mx.tuned_plan(ot, M, N, p.Kp) is None
