@@ -21,7 +21,7 @@ namespace plan {
 //
 // Candidate tiles (4 waves per workgroup):
 //   256x256, waves 2x2, each wave 128x128 -> MPW 4, NPW 4   (16 MFMAs per wave per 64-wide slab)
-//   256x192, waves 2x2, each wave 128x96  -> MPW 4, NPW 3   (12)
+//   256x192, waves 2x2, each wave 128x96  -> MPW 4, NPW 3   (12; built, not routed: kCands)
 //   128x256, waves 2x2, each wave  64x128 -> MPW 2, NPW 4   (8)
 //   128x128, waves 2x2, each wave  64x64  -> MPW 2, NPW 2   (4; two workgroups fit a CU's LDS)
 // the wide tiles (waves 1x4, B straight into registers, A staged in LDS one K-tile at a time):
