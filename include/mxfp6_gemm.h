@@ -90,7 +90,8 @@ int mxfp6_gemm_async(int out_type, int M, int N, int Kp, const void* dA, const v
  * fits beside them, go to a device array of MXFP6_NOALLOC_SCRATCH_BYTES that the library holds
  * per GPU from the first such call on that GPU until the process ends. Same plan and the same
  * output bits as mxfp6_gemm_async with mxfp6_gemm_preferred_workspace_size bytes, except that a
- * repacked A that does not fit is read row-major instead (same bits). A shape whose split-K
+ * repacked A that does not fit is read row-major instead (with the routed split, possibly on
+ * another tile of the routed scale grouping: the same bits). A shape whose split-K
  * partials (mxfp6_gemm_workspace_size) exceed the scratch is rejected with MXFP6_ERR_SCRATCH,
  * before any device work. Every call on a GPU shares that GPU's scratch: calls that overlap on one
  * GPU (concurrent streams or host threads) race; serialise them. No counterpart in the reference:
@@ -150,10 +151,10 @@ void mxfp6_gemm_tune_reset(void);
 
 /* The plan gemm() runs for (out_type, M, N, Kp) with a workspace of ws_bytes: tile {MT, NT, MPW,
  * NPW}, K segments and whether A is repacked first. A measured plan when the workspace holds it,
- * else the routed plan when the workspace holds it, else the fastest predicted plan with the
- * routed scale grouping (the tile choose_tile returns fixes the scale layout) that fits
- * gemm_workspace_size's workspace when ws_bytes holds that, or else one that needs none. Unsplit
- * plans of one scale grouping give the same output bits. No counterpart in the reference (its
+ * else the routed plan when the workspace holds it, else, on row-major A, the fastest predicted
+ * tile with the routed scale grouping (the tile choose_tile returns fixes the scale layout) for the
+ * routed split when ws_bytes holds its partials (gemm_workspace_size's bytes), or unsplit. For a
+ * given split, the tiles of one scale grouping give the same output bits. No counterpart in the reference (its
  * dispatch runs choose_tile's tile, unsplit when the workspace is short, src/dispatch.hpp:74-87). */
 int mxfp6_gemm_plan(int out_type, int M, int N, int Kp, size_t ws_bytes, int tile[4], int* splits,
                     int* a_repack);

@@ -181,16 +181,15 @@ Plan best_plan(int M, int N, int Kp, int cus) {
     return best;
 }
 
-// The least-time plan with the scale grouping of `grouping` whose workspace fits ws_bytes: what
-// gemm() runs when the caller's workspace does not hold the routed plan (gemm_workspace_size's
-// workspace, the split-K partials only, or none). The unsplit row-major plans always fit, and any
-// unsplit plan of a grouping gives the same output bits (same MFMAs in the same K order).
-Plan best_fitting_plan(int M, int N, int Kp, int cus, const TileChoice& grouping, size_t ws_bytes) {
-    Plan best = {grouping, 1, false};
+// The least-time row-major plan with the scale grouping of `grouping` and S K segments: what
+// gemm() runs when the caller's workspace does not hold the routed plan (S = the routed split
+// with gemm_workspace_size's workspace, 1 with none). For a given S every tile of a grouping gives
+// the same output bits (each K segment's MFMAs in the same K order, the same reduction).
+Plan best_fitting_plan(int M, int N, int Kp, int cus, const TileChoice& grouping, int S_fixed) {
+    Plan best = {grouping, S_fixed, false};
     double best_t = -1.0;
     visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
-        if (tc.MPW != grouping.MPW || tc.NPW != grouping.NPW) return;
-        if (!plan_fits(M, N, Kp, S, rp, ws_bytes)) return;
+        if (tc.MPW != grouping.MPW || tc.NPW != grouping.NPW || S != S_fixed || rp) return;
         const double t = plan_time_us(tc, M, N, Kp, S, rp, cus);
         if (best_t < 0 || t < best_t * (1.0 - PLAN_MIN_GAIN)) {
             best = {tc, S, rp};
@@ -224,9 +223,8 @@ const Routed& cached_routes(int M, int N, int Kp) {
     Entry& e = cache[h % 16];
     if (!e.valid || e.M != M || e.N != N || e.Kp != Kp || e.cus != cus) {
         const Plan pl = best_plan(M, N, Kp, cus);
-        const Plan none = best_fitting_plan(M, N, Kp, cus, pl.tc, 0);
-        const Plan ref = pl.S > 1 ? best_fitting_plan(M, N, Kp, cus, pl.tc, split_bytes(M, N, pl.S))
-                                  : none;
+        const Plan none = best_fitting_plan(M, N, Kp, cus, pl.tc, 1);
+        const Plan ref = pl.S > 1 ? best_fitting_plan(M, N, Kp, cus, pl.tc, pl.S) : none;
         e = {M, N, Kp, cus, {pl, ref, none}, true};
     }
     return e.r;
@@ -421,11 +419,11 @@ int gemm_checked(int out_type, int M, int N, int Kp, const void* dA, const void*
 }
 
 // The plan gemm() runs for a workspace of ws_bytes: a measured plan of the shape when the
-// workspace holds it; else the routed plan when the workspace holds it; else the fastest
-// predicted plan with the routed scale grouping that fits gemm_workspace_size's workspace (the
-// split-K partials only) when ws_bytes holds that, or else one that needs none (*unsplit set when
-// the routed plan was split: the reference's warning case). Falling back changes neither the
-// scale layout the caller prepared nor, for an unsplit plan, the output bits.
+// workspace holds it; else the routed plan when the workspace holds it; else, on row-major A, the
+// fastest predicted tile with the routed scale grouping for the routed split when ws_bytes holds
+// its partials (gemm_workspace_size's workspace), or unsplit (*unsplit set when the routed plan
+// was split: the reference's warning case). Falling back changes neither the scale layout the
+// caller prepared nor the output bits of the routed plan when the split is kept.
 Plan plan_for(int out_type, int M, int N, int Kp, size_t ws_bytes, bool* unsplit) {
     if (unsplit != nullptr) *unsplit = false;
     Plan tuned;
@@ -645,8 +643,9 @@ extern "C" int mxfp6_gemm_noalloc_async(int out_type, int M, int N, int Kp, cons
     (void)B_row_bytes;
     const int st = plan::check_common(out_type, M, N, Kp, dA, dBsh, dsA, dsB, dD, A_row_bytes);
     if (st != MXFP6_OK) return st;
-    // the plan's split-K partials must fit; the repacked A is used only when it fits beside them
-    // (gemm_checked drops it otherwise)
+    // the plan's split-K partials must fit; a plan that also repacks A runs as planned only when
+    // the repacked A fits beside them (gemm_checked runs the fastest plan of the routed scale
+    // grouping that fits the partials otherwise)
     if (plan::workspace_bytes(M, N, Kp) > MXFP6_NOALLOC_SCRATCH_BYTES) return MXFP6_ERR_SCRATCH;
     size_t cap = 0;
     void* scratch = mxfp6_hip_scratch(&cap);

@@ -325,6 +325,8 @@ def test_plan_for_every_workspace(mx):
                    ps * M * N * 4 <= ws) or (ps == 1 and not prp), (M, N, K, ws, ps, prp)
         pt, ps, prp = mx.gemm_plan(1, M, N, Kp, 0)
         assert ps == 1 and not prp, (M, N, K)
+        if pref > ref:  # the reference-sized workspace keeps the routed split (same bits)
+            assert mx.gemm_plan(1, M, N, Kp, ref)[1:] == (S, False), (M, N, K)
 
 
 @pytest.mark.parametrize("M,N,K", [(2048, 12288, 4096), (3072, 6144, 8192), (6144, 6144, 8192),
