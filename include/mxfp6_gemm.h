@@ -149,6 +149,16 @@ int mxfp6_gemm_tuned_plan(int out_type, int M, int N, int Kp, int tile[4], int* 
 /* Forgets every measured plan (gemm() runs the router's plans again). */
 void mxfp6_gemm_tune_reset(void);
 
+/* Writes the measured plans to a text file (a comment line, then one plan per line: out_type M N
+ * Kp MT NT MPW NPW S repack) and their number to *count (may be NULL); MXFP6_ERR_ARG when the
+ * file cannot be written. mxfp6_gemm_tune_load adds such a file's plans to the table, so that a
+ * serving process can start with the plans an earlier run measured: a plan is taken only if its
+ * tile is implemented, its split fits the shape and its scale grouping is the one choose_tile
+ * returns for the shape on this device; *loaded and *skipped (may be NULL) count the lines taken
+ * and left. MXFP6_ERR_ARG when the file cannot be read. No counterpart in the reference. */
+int mxfp6_gemm_tune_save(const char* path, int* count);
+int mxfp6_gemm_tune_load(const char* path, int* loaded, int* skipped);
+
 /* The plan gemm() runs for (out_type, M, N, Kp) with a workspace of ws_bytes: tile {MT, NT, MPW,
  * NPW}, K segments and whether A is repacked first. A measured plan when the workspace holds it,
  * else the routed plan when the workspace holds it, else, on row-major A, the fastest predicted

@@ -541,6 +541,65 @@ void tune_reset() {
     g_n_tuned.store(0, std::memory_order_release);
 }
 
+// The measured plans as text, one per line after a comment line:
+//   out_type M N Kp MT NT MPW NPW S repack
+int tune_save(const char* path, int* count) {
+    std::vector<Tuned> copy;
+    {
+        std::lock_guard<std::mutex> lk(g_tuned_mu);
+        copy = g_tuned;
+    }
+    FILE* f = std::fopen(path, "w");
+    if (f == nullptr) return MXFP6_ERR_ARG;
+    bool ok = std::fprintf(f, "# libmxfp6gemm measured plans: out_type M N Kp MT NT MPW NPW S "
+                              "repack\n") > 0;
+    for (const Tuned& t : copy)
+        ok = ok && std::fprintf(f, "%d %d %d %d %d %d %d %d %d %d\n", t.out_type, t.M, t.N, t.Kp,
+                                t.plan.tc.MT, t.plan.tc.NT, t.plan.tc.MPW, t.plan.tc.NPW,
+                                t.plan.S, t.plan.repack ? 1 : 0) > 0;
+    ok = std::fclose(f) == 0 && ok;
+    if (count != nullptr) *count = ok ? (int)copy.size() : 0;
+    return ok ? MXFP6_OK : MXFP6_ERR_ARG;
+}
+
+// Adds the plans of a tune_save file to the table. A line is taken only if it names a tile the
+// kernels implement, a split the shape allows, and the scale grouping choose_tile returns for the
+// shape on this device (the caller's scales are tiled for that grouping); others are counted as
+// skipped, as are malformed lines.
+int tune_load(const char* path, int* loaded, int* skipped) {
+    FILE* f = std::fopen(path, "r");
+    if (f == nullptr) return MXFP6_ERR_ARG;
+    int n_ok = 0, n_skip = 0;
+    char line[256];
+    while (std::fgets(line, sizeof line, f) != nullptr) {
+        if (line[0] == '#' || line[0] == '\n') continue;
+        int v[10];
+        if (std::sscanf(line, "%d %d %d %d %d %d %d %d %d %d", &v[0], &v[1], &v[2], &v[3], &v[4],
+                        &v[5], &v[6], &v[7], &v[8], &v[9]) != 10) {
+            n_skip++;
+            continue;
+        }
+        const int ot = v[0], M = v[1], N = v[2], Kp = v[3], S = v[8], rp = v[9];
+        const TileChoice tc = {v[4], v[5], v[6], v[7]};
+        bool ok = ot >= 0 && ot <= 2 && shape_ok(M, N, Kp) && S >= 1 && S <= Kp / K_TILE &&
+                  (rp == 0 || rp == 1) && kernel_for(tc) == MXFP6_KERNEL_TILE;
+        if (ok) {
+            const TileChoice r = route(M, N, Kp);
+            ok = r.MPW == tc.MPW && r.NPW == tc.NPW;
+        }
+        if (!ok) {
+            n_skip++;
+            continue;
+        }
+        store_tuned(ot, M, N, Kp, {tc, S, rp != 0});
+        n_ok++;
+    }
+    std::fclose(f);
+    if (loaded != nullptr) *loaded = n_ok;
+    if (skipped != nullptr) *skipped = n_skip;
+    return MXFP6_OK;
+}
+
 bool tile_divides(const int tile[4], int M, int N) {
     return tile[0] > 0 && tile[1] > 0 && M % tile[0] == 0 && N % tile[1] == 0 &&
            tile[2] >= 1 && tile[2] <= 4 && tile[3] >= 1 && tile[3] <= 4 &&
@@ -735,6 +794,16 @@ extern "C" int mxfp6_gemm_tuned_plan(int out_type, int M, int N, int Kp, int til
 
 extern "C" void mxfp6_gemm_tune_reset(void) {
     plan::tune_reset();
+}
+
+extern "C" int mxfp6_gemm_tune_save(const char* path, int* count) {
+    if (path == nullptr) return MXFP6_ERR_NULL;
+    return plan::tune_save(path, count);
+}
+
+extern "C" int mxfp6_gemm_tune_load(const char* path, int* loaded, int* skipped) {
+    if (path == nullptr) return MXFP6_ERR_NULL;
+    return plan::tune_load(path, loaded, skipped);
 }
 
 extern "C" int mxfp6_gemm_plan(int out_type, int M, int N, int Kp, size_t ws_bytes, int tile[4],

@@ -49,6 +49,8 @@ int tune(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh, c
          int candidates, void* stream, int tile_out[4], int* splits_out, int* repack_out);
 int tuned(int out_type, int M, int N, int Kp, int tile_out[4], int* splits_out, int* repack_out);
 void tune_reset();
+int tune_save(const char* path, int* count);
+int tune_load(const char* path, int* loaded, int* skipped);
 int plan_info(int out_type, int M, int N, int Kp, size_t ws_bytes, int tile_out[4],
               int* splits_out, int* repack_out);
 size_t plan_bytes(int M, int N, int Kp, int S, bool repack);

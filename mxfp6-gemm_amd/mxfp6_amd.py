@@ -63,6 +63,8 @@ SIGNATURES = {
     "mxfp6_gemm_tuned_plan": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
                                         C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "mxfp6_gemm_tune_reset": (None, []),
+    "mxfp6_gemm_tune_save": (C.c_int, [C.c_char_p, C.POINTER(C.c_int)]),
+    "mxfp6_gemm_tune_load": (C.c_int, [C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "mxfp6_gemm_plan": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_size_t,
                                   C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "mxfp6_plan_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
@@ -231,6 +233,24 @@ def tuned_plan(out_type, M, N, Kp):
 
 def tune_reset():
     lib().mxfp6_gemm_tune_reset()
+
+
+def tune_save(path):
+    """Writes the measured plans to `path`; returns how many."""
+    n = C.c_int(0)
+    rc = lib().mxfp6_gemm_tune_save(os.fsencode(path), C.byref(n))
+    if rc != 0:
+        raise OSError(f"mxfp6_gemm_tune_save({path}): {STATUS.get(rc, rc)}")
+    return n.value
+
+
+def tune_load(path):
+    """Adds the plans of a tune_save file; returns (loaded, skipped)."""
+    a, b = C.c_int(0), C.c_int(0)
+    rc = lib().mxfp6_gemm_tune_load(os.fsencode(path), C.byref(a), C.byref(b))
+    if rc != 0:
+        raise OSError(f"mxfp6_gemm_tune_load({path}): {STATUS.get(rc, rc)}")
+    return a.value, b.value
 
 
 def gemm_plan(out_type, M, N, Kp, ws_bytes):

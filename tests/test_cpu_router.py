@@ -340,3 +340,38 @@ def test_former_256x192_routes(mx, M, N, K):
     assert t in {(128, 384, 4, 3), (256, 256, 4, 2), (128, 512, 4, 4), (128, 256, 4, 2)}, t
     pt, ps, prp = mx.gemm_plan(1, M, N, Kp, mx.workspace_size(M, N, Kp))
     assert pt[2:] == t[2:] and not prp
+
+
+def test_measured_plans_file(mx, tmp_path):
+    """mxfp6_gemm_tune_save / _load: a plan file's valid lines enter the measured-plan table (and
+    gemm()'s plan), lines with another scale grouping than choose_tile's, an impossible split, an
+    unimplemented tile, a bad output type or no numbers are skipped; saving and loading again gives
+    the same table."""
+    mx.tune_reset()
+    M, N, K = 2048, 2048, 16384
+    Kp = _kpad(K)
+    t = tuple(mx.choose_tile(M, N, Kp))
+    assert t[2:] == (4, 2)
+    src = tmp_path / "plans.txt"
+    src.write_text("\n".join([
+        "# measured plans",
+        f"1 {M} {N} {Kp} 128 256 4 2 1 0",                # taken
+        f"1 {M} {N} {Kp} 128 384 4 3 1 0",                # another scale grouping
+        f"0 {M} {N} {Kp} 256 256 4 2 {Kp // 192 + 1} 0",  # more segments than K-tiles
+        f"2 {M} {N} {Kp} 256 128 4 2 1 0",                # no such tile
+        f"5 {M} {N} {Kp} 256 256 4 2 1 0",                # no such output type
+        "not a plan",
+    ]) + "\n")
+    assert mx.tune_load(str(src)) == (1, 5)
+    assert mx.tuned_plan(1, M, N, Kp) == ((128, 256, 4, 2), 1, False)
+    assert mx.tuned_plan(0, M, N, Kp) is None
+    assert mx.gemm_plan(1, M, N, Kp, 0) == ((128, 256, 4, 2), 1, False)
+    out = tmp_path / "saved.txt"
+    assert mx.tune_save(str(out)) == 1
+    mx.tune_reset()
+    assert mx.tuned_plan(1, M, N, Kp) is None
+    assert mx.tune_load(str(out)) == (1, 0)
+    assert mx.tuned_plan(1, M, N, Kp) == ((128, 256, 4, 2), 1, False)
+    mx.tune_reset()
+    with pytest.raises(OSError):
+        mx.tune_load(str(tmp_path / "missing.txt"))
