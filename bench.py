@@ -12,7 +12,7 @@ drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX 
   python bench.py --prep      (device operand preparation: float -> MXFP6 device layouts, GB/s)
   python bench.py --power S   (board power and clocks over S seconds of back-to-back GEMMs of the
                                workload, this library then the reference library; amd-smi)
-  python bench.py --map [SHAPES] [--repeat R]  (this library against the reference library,
+  python bench.py --map [SHAPES|second] [--repeat R]  (this library against the reference library,
                                shape by shape: MxNxK,... or the default map of 154 shapes, FP16
                                out; R > 1: R more runs per library, alternating their order)
 
@@ -562,6 +562,27 @@ def default_map():
     return shapes + [s for s in sorted(drawn) if s not in shapes]
 
 
+def second_map():
+    """160 shapes drawn with another seed from other sizes than default_map's (N multiples of
+    384 among them, K up to 73728, M up to 16384), between 1 GFLOP and 1.5 TFLOP: a check that
+    the router's and kernels' standing against the reference holds off the shapes they were
+    tuned on."""
+    import random
+    rng = random.Random(777)
+    ms = [128, 256, 384, 512, 768, 1024, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 8192, 12288,
+          16384]
+    ns = [256, 384, 768, 1152, 1536, 2304, 3072, 3840, 4608, 5376, 6144, 7680, 9216, 10752, 12288,
+          13824, 18432, 24576]
+    ks = [256, 512, 1024, 1536, 2304, 3072, 4608, 6144, 9216, 12288, 18432, 24576, 36864, 49152,
+          73728]
+    drawn = set()
+    while len(drawn) < 160:
+        M, N, K = rng.choice(ms), rng.choice(ns), rng.choice(ks)
+        if 1e9 <= 2.0 * M * N * K <= 1.5e12:
+            drawn.add((M, N, K))
+    return sorted(drawn)
+
+
 def run_map(spec, repeat=1):
     """This library and the reference library on the same operands, shape by shape, by the
     reference's timing method (compare()); one JSON line per shape, then a summary line. With
@@ -571,7 +592,9 @@ def run_map(spec, repeat=1):
     ref = reference_library()
     if ref is None:
         raise SystemExit("--map needs the reference library (oracle/_ref/libmxfp6ref.so)")
-    if spec:
+    if spec == "second":
+        shapes = second_map()
+    elif spec:
         txt = open(spec).read() if os.path.exists(spec) else spec
         shapes = [tuple(int(v) for v in t.strip().split("x")) for t in txt.split(",") if t.strip()]
     else:
@@ -707,7 +730,8 @@ def main():
                     help="board power and clocks over SECONDS of back-to-back GEMMs instead")
     ap.add_argument("--map", nargs="?", const="", default=None, metavar="SHAPES",
                     help="this library against the reference library shape by shape instead "
-                         "(MxNxK,... or a file of them; default: 154 shapes)")
+                         "(MxNxK,... or a file of them; 'second': 160 other shapes; "
+                         "default: 154 shapes)")
     ap.add_argument("--repeat", type=int, default=1, metavar="R",
                     help="with --map: time each shape R more times per library, alternating "
                          "which runs first, and summarise by the ratio of the medians")
