@@ -32,10 +32,10 @@
 // current one is free for the copies of K-tile c + NB - 1. The B loads and scale loads are
 // ordinary loads whose waits the compiler places before the MFMAs that use them.
 // Prefetches past the workgroup's last K-tile are clamped to that K-tile (valid addresses, data
-// never used), so the K loop has no branch. A 128 x 256 workgroup with exactly two K-tiles
-// (K <= 384, or a split segment of two) takes a short path instead: both K-tiles' chunks, scales
-// and B operands (a second register set) are requested before the first MFMA, so K-tile 1 does
-// not wait out a memory latency for B loads issued during K-tile 0. MASK (ragged M or N) clamps the copy and load sources
+// never used), so the K loop has no branch. A 128 x 256 workgroup with two or three K-tiles
+// (K <= 576, or a split segment that short) takes a short path instead: every K-tile's chunk,
+// scales and B operands (a register set per K-tile) are requested before the first MFMA, so no
+// K-tile waits out a memory latency for B loads issued during the one before it. MASK (ragged M or N) clamps the copy and load sources
 // of the last tile row and column and masks the stores, as in the slab kernel.
 #pragma once
 
@@ -87,14 +87,14 @@ struct WideGeom {
     // In the prologue: after chunk 0's copies, those of chunks 1 .. NB - 2, the scale loads of
     // K-tile 0 and the B loads of its three slabs.
     static constexpr int PRO_WAIT = (NB - 2) * A_ISS + NGA + 1 + SUBS * 2 * NPW;
-    // Two K-tiles (wide_kernel's short path): everything is loaded up front, chunk 0, the scales
-    // and B operands of K-tile 0, chunk 1, the scales and B operands of K-tile 1; issued after
-    // chunk 1, and after chunk 0
-    static constexpr int TWO_CHUNK1_WAIT = NGA + 1 + SUBS * 2 * NPW;
-    static constexpr int TWO_PRO_WAIT = NGA + 1 + SUBS * 2 * NPW + A_ISS + TWO_CHUNK1_WAIT;
-    // the short path holds a second set of B operands: built for the 128 x 256 tile only (the
+    // Two or three K-tiles (wide_kernel's short path): everything is loaded up front, K-tile by
+    // K-tile its chunk, scales and B operands; the operations issued after chunk c's copies
+    static constexpr int short_wait(int nk, int c) {
+        return NGA + 1 + SUBS * 2 * NPW + (nk - 1 - c) * (A_ISS + NGA + 1 + SUBS * 2 * NPW);
+    }
+    // the short path holds a set of B operands per K-tile: built for the 128 x 256 tile only (the
     // others have no registers to spare)
-    static constexpr bool TWO_PATH = MB == 4 && NPW == 2;
+    static constexpr bool SHORT_PATH = MB == 4 && NPW == 2;
     static_assert(MB == 4 || MB == 8, "128 or 256 rows");
     static_assert(NPW >= 1 && NPW <= 4, "B scale group holds <= 4 blocks");
     // NB = 3: the prologue issues chunk 1 before the loop, and the count above then holds for
@@ -104,7 +104,8 @@ struct WideGeom {
     static_assert(cps(0) + cps(1) + cps(2) == A_ISS && cps(2) >= 1, "copies per K-tile");
     static_assert(copy_k(cps(0) - 1) < NMF, "copy positions");
     static_assert(read_k(MB - 1) < NMF, "read positions");
-    static_assert(CHUNK_WAIT <= 63 && PRO_WAIT <= 63 && TWO_PRO_WAIT <= 63, "vmcnt range");
+    static_assert(CHUNK_WAIT <= 63 && PRO_WAIT <= 63, "vmcnt range");
+    static_assert(!SHORT_PATH || short_wait(3, 0) <= 63, "vmcnt range (short path)");
 };
 
 // acc[mi][ni] += A(mi) * B(ni) with the scale bytes mi % 4 of sa and ni of sb (op_sel must be a
@@ -256,82 +257,80 @@ __global__ void __launch_bounds__(256, 1)
     v3i sc_a[NGA], sc_b;   // scale dwords of the current K-tile
     v3i sn_a[NGA], sn_b;   // and of the next one
 
-    if constexpr (G::TWO_PATH) {
-        if (nkt == 2) {
-            // Two K-tiles (K <= 384, or a split segment of two): both K-tiles' chunks, scales and
-            // B operands are requested before the first MFMA, so K-tile 1 does not wait for loads
-            // issued during K-tile 0; no K-tile follows, so nothing is clamped and K-tile 1 needs
-            // no barrier.
-            v8i RB1[SUBS][NPW];
-            v3i s1_a[NGA], s1_b;
+    if constexpr (G::SHORT_PATH) {
+        // Two or three K-tiles (K <= 576, or a split segment that short): every K-tile's chunk,
+        // scales and B operands (a register set per K-tile) are requested before the first MFMA,
+        // so no K-tile waits for loads issued during the one before it; nothing is clamped, and
+        // the last K-tile needs no barrier. Chunk c goes to LDS buffer c.
+        auto short_path = [&](auto nk) {
+            constexpr int NK = decltype(nk)::value;
+            v8i RBk[NK][SUBS][NPW];
+            v3i ska[NK][NGA], skb[NK];
 #pragma unroll
-            for (int i = 0; i < G::A_ISS; i++) a_copy(i, kt0, 0);
-            load_scales(sc_a, sc_b, kt0);
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
+            for (int c = 0; c < NK; c++) {
 #pragma unroll
-            for (int s = 0; s < SUBS; s++)
+                for (int i = 0; i < G::A_ISS; i++) a_copy(i, kt0 + c, c);
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+                load_scales(ska[c], skb[c], kt0 + c);
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int ni = 0; ni < NPW; ni++) {
-                    load_b(RB[s][ni], ni, kt0, s);
-                    asm volatile("" ::: "memory");
-                    __builtin_amdgcn_sched_barrier(0);
-                }
+                for (int s = 0; s < SUBS; s++)
 #pragma unroll
-            for (int i = 0; i < G::A_ISS; i++) a_copy(i, kt0 + 1, 1);
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
-            load_scales(s1_a, s1_b, kt0 + 1);
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int s = 0; s < SUBS; s++)
-#pragma unroll
-                for (int ni = 0; ni < NPW; ni++) {
-                    load_b(RB1[s][ni], ni, kt0 + 1, s);
-                    asm volatile("" ::: "memory");
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            wait_vmcnt<G::TWO_PRO_WAIT>();  // chunk 0 landed
+                    for (int ni = 0; ni < NPW; ni++) {
+                        load_b(RBk[c][s][ni], ni, kt0 + c, s);
+                        asm volatile("" ::: "memory");
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+            }
+            wait_vmcnt<G::short_wait(NK, 0)>();  // chunk 0 landed
             ring_barrier();
 #pragma unroll
             for (int mi = 0; mi < MB; mi++) read_a(RA[0][mi], 0, 0, mi);
-            // K-tile F (0 or 1) from LDS buffer F; slab s uses A set s (three sets)
-            auto two_ktile = [&](auto first) {
-                constexpr bool F0 = decltype(first)::value;
+            // K-tile C from LDS buffer C; slab s uses A set s (three sets)
+            auto step = [&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                constexpr bool MORE = C + 1 < NK;
 #pragma unroll
                 for (int s = 0; s < SUBS; s++) {
-                    if (F0 && s == SUBS - 1) {
-                        wait_vmcnt<G::TWO_CHUNK1_WAIT>();  // chunk 1 complete for every wave
+                    if (MORE && s == SUBS - 1) {
+                        // chunk C + 1 complete for every wave
+                        wait_vmcnt<G::short_wait(NK, MORE ? C + 1 : 0)>();
                         ring_barrier();
                     }
                     const int nxt = (s + 1) % SUBS;
-                    const int rbuf = s + 1 < SUBS ? (F0 ? 0 : 1) : 1;
+                    const int rbuf = s + 1 < SUBS ? C : C + 1;
                     const int rs = s + 1 < SUBS ? s + 1 : 0;
 #pragma unroll
                     for (int k = 0; k < NMF; k++) {
                         const int ni = k / MB, mi = k % MB;
                         const int g = mi / GA;
-                        const v3i& xa = F0 ? sc_a[g] : s1_a[g];
-                        const v3i& xb = F0 ? sc_b : s1_b;
-                        const int sa = s == 0 ? xa.x : s == 1 ? xa.y : xa.z;
-                        const int sb = s == 0 ? xb.x : s == 1 ? xb.y : xb.z;
-                        wide_mfma<MB, NPW>(acc, mi, ni, RA[s][mi], F0 ? RB[s][ni] : RB1[s][ni],
-                                           sa, sb);
+                        const int sa = s == 0 ? ska[C][g].x : s == 1 ? ska[C][g].y : ska[C][g].z;
+                        const int sb = s == 0 ? skb[C].x : s == 1 ? skb[C].y : skb[C].z;
+                        wide_mfma<MB, NPW>(acc, mi, ni, RA[s][mi], RBk[C][s][ni], sa, sb);
 #pragma unroll
                         for (int i = 0; i < MB; i++)
-                            if (k == G::read_k(i) && (F0 || s + 1 < SUBS))
+                            if (k == G::read_k(i) && (MORE || s + 1 < SUBS))
                                 read_a(RA[nxt][i], rbuf, rs, i);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             };
-            two_ktile(std::true_type{});
-            two_ktile(std::false_type{});
+            step(std::integral_constant<int, 0>{});
+            step(std::integral_constant<int, 1>{});
+            if constexpr (NK == 3) step(std::integral_constant<int, 2>{});
             store_tile<MB, NPW, OutT, SPLIT, MASK, STREAM>(acc, D, ws, M, N,
                                                         wg_m * MT + 4 * (lane >> 5),
                                                         wg_n * NT + wave * NPW * 32 + (lane & 31),
                                                         lane, wg_z);
+        };
+        if (nkt == 2) {
+            short_path(std::integral_constant<int, 2>{});
+            return;
+        }
+        if (nkt == 3) {
+            short_path(std::integral_constant<int, 3>{});
             return;
         }
     }
