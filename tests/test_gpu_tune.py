@@ -79,3 +79,26 @@ def test_tuned_plan_is_used_and_correct(orc, M, N, K):
 
     mx.tune_reset()
     assert mx.tuned_plan(ot, M, N, p.Kp) is None
+
+
+def test_loaded_plan_is_used(orc, tmp_path):
+    """A plan from a measured-plan file (mxfp6_gemm_tune_load) is what gemm() runs: bit-equal to
+    the same plan run explicitly, within the oracle bar on sampled rows."""
+    ot = mx.OUT_F16
+    M, N, K = 2048, 2048, 16384
+    p = mx.make_problem(M, N, K, seed=99)
+    routed = tuple(mx.choose_tile(M, N, p.Kp))
+    plan = ((128, 256) + routed[2:], 2, False)
+    f = tmp_path / "plans.txt"
+    f.write_text(f"{ot} {M} {N} {p.Kp} {plan[0][0]} {plan[0][1]} {plan[0][2]} {plan[0][3]} "
+                 f"{plan[1]} 0\n")
+    assert mx.tune_load(str(f)) == (1, 0)
+    assert mx.gemm_plan(ot, M, N, p.Kp, mx.plan_workspace_size(M, N, p.Kp, 2, 0)) == plan
+    dp = DevProblem(p, routed)
+    got = _gemm(dp, ot, mx.plan_workspace_size(M, N, p.Kp, 2, 0))
+    want = run_explicit(DevProblem(p, plan[0]), ot, splits=2, a_layout=0)
+    assert (got.view("u4") == want.view("u4")).all(), "gemm() did not run the loaded plan"
+    rows = np.r_[0:2, M // 2, M - 2:M]
+    R, ab = orc.gemm_f64(p.a_packed, p.a_row_bytes, p.a_scales, p.b_packed, p.b_row_bytes,
+                         p.b_scales, M, N, K, rows=rows)
+    checks.check(got[rows], R, ab, ot)
