@@ -32,10 +32,11 @@
 // current one is free for the copies of K-tile c + NB - 1. The B loads and scale loads are
 // ordinary loads whose waits the compiler places before the MFMAs that use them.
 // Prefetches past the workgroup's last K-tile are clamped to that K-tile (valid addresses, data
-// never used), so the K loop has no branch. A 128 x 256 workgroup with two or three K-tiles
-// (K <= 576, or a split segment that short) takes a short path instead: every K-tile's chunk,
-// scales and B operands (a register set per K-tile) are requested before the first MFMA, so no
-// K-tile waits out a memory latency for B loads issued during the one before it. MASK (ragged M or N) clamps the copy and load sources
+// never used), so the K loop has no branch. A 128 x 384 workgroup with a single K-tile, or a
+// 128 x 256 one with up to three (K <= 576, or a split segment that short), takes a short path
+// instead: every K-tile's chunk, scales and B operands (a register set per K-tile) are requested
+// before the first MFMA, so no K-tile waits out a memory latency for B loads issued during the
+// one before it, and no clamped prefetch is issued. MASK (ragged M or N) clamps the copy and load sources
 // of the last tile row and column and masks the stores, as in the slab kernel.
 #pragma once
 
@@ -87,14 +88,15 @@ struct WideGeom {
     // In the prologue: after chunk 0's copies, those of chunks 1 .. NB - 2, the scale loads of
     // K-tile 0 and the B loads of its three slabs.
     static constexpr int PRO_WAIT = (NB - 2) * A_ISS + NGA + 1 + SUBS * 2 * NPW;
-    // Two or three K-tiles (wide_kernel's short path): everything is loaded up front, K-tile by
+    // One to three K-tiles (wide_kernel's short path): everything is loaded up front, K-tile by
     // K-tile its chunk, scales and B operands; the operations issued after chunk c's copies
     static constexpr int short_wait(int nk, int c) {
         return NGA + 1 + SUBS * 2 * NPW + (nk - 1 - c) * (A_ISS + NGA + 1 + SUBS * 2 * NPW);
     }
-    // the short path holds a set of B operands per K-tile: built for the 128 x 256 tile only (the
-    // others have no registers to spare)
-    static constexpr bool SHORT_PATH = MB == 4 && NPW == 2;
+    // the short path holds a set of B operands per K-tile: up to three K-tiles on the 128 x 256
+    // tile, one on 128 x 384; none on 128 x 512 and 256 x 256, whose masked and repacked-A
+    // instantiations would then spill (the registers are allocated for the whole kernel)
+    static constexpr int SHORT_MAX = MB == 4 && NPW == 2 ? 3 : MB == 4 && NPW == 3 ? 1 : 0;
     static_assert(MB == 4 || MB == 8, "128 or 256 rows");
     static_assert(NPW >= 1 && NPW <= 4, "B scale group holds <= 4 blocks");
     // NB = 3: the prologue issues chunk 1 before the loop, and the count above then holds for
@@ -105,7 +107,7 @@ struct WideGeom {
     static_assert(copy_k(cps(0) - 1) < NMF, "copy positions");
     static_assert(read_k(MB - 1) < NMF, "read positions");
     static_assert(CHUNK_WAIT <= 63 && PRO_WAIT <= 63, "vmcnt range");
-    static_assert(!SHORT_PATH || short_wait(3, 0) <= 63, "vmcnt range (short path)");
+    static_assert(SHORT_MAX == 0 || short_wait(SHORT_MAX, 0) <= 63, "vmcnt range (short path)");
 };
 
 // acc[mi][ni] += A(mi) * B(ni) with the scale bytes mi % 4 of sa and ni of sb (op_sel must be a
@@ -257,11 +259,12 @@ __global__ void __launch_bounds__(256, 1)
     v3i sc_a[NGA], sc_b;   // scale dwords of the current K-tile
     v3i sn_a[NGA], sn_b;   // and of the next one
 
-    if constexpr (G::SHORT_PATH) {
-        // Two or three K-tiles (K <= 576, or a split segment that short): every K-tile's chunk,
-        // scales and B operands (a register set per K-tile) are requested before the first MFMA,
-        // so no K-tile waits for loads issued during the one before it; nothing is clamped, and
-        // the last K-tile needs no barrier. Chunk c goes to LDS buffer c.
+    if constexpr (G::SHORT_MAX > 0) {
+        // One K-tile, or on the 128 x 256 tile up to three (K <= 576, or a split segment that
+        // short): every K-tile's chunk, scales and B operands (a register set per K-tile) are
+        // requested before the first MFMA, so no K-tile waits for loads issued during the one
+        // before it; nothing is clamped, and the last K-tile needs no barrier. Chunk c goes to
+        // LDS buffer c.
         auto short_path = [&](auto nk) {
             constexpr int NK = decltype(nk)::value;
             v8i RBk[NK][SUBS][NPW];
@@ -288,7 +291,7 @@ __global__ void __launch_bounds__(256, 1)
             ring_barrier();
 #pragma unroll
             for (int mi = 0; mi < MB; mi++) read_a(RA[0][mi], 0, 0, mi);
-            // K-tile C from LDS buffer C; slab s uses A set s (three sets)
+            // K-tile C from LDS buffer C; slab s uses A set s (three sets) or (3 C + s) % 2 (two)
             auto step = [&](auto cc) {
                 constexpr int C = decltype(cc)::value;
                 constexpr bool MORE = C + 1 < NK;
@@ -299,7 +302,8 @@ __global__ void __launch_bounds__(256, 1)
                         wait_vmcnt<G::short_wait(NK, MORE ? C + 1 : 0)>();
                         ring_barrier();
                     }
-                    const int nxt = (s + 1) % SUBS;
+                    const int cur = NSET == 3 ? s : (3 * C + s) % 2;
+                    const int nxt = NSET == 3 ? (s + 1) % 3 : (3 * C + s + 1) % 2;
                     const int rbuf = s + 1 < SUBS ? C : C + 1;
                     const int rs = s + 1 < SUBS ? s + 1 : 0;
 #pragma unroll
@@ -308,7 +312,7 @@ __global__ void __launch_bounds__(256, 1)
                         const int g = mi / GA;
                         const int sa = s == 0 ? ska[C][g].x : s == 1 ? ska[C][g].y : ska[C][g].z;
                         const int sb = s == 0 ? skb[C].x : s == 1 ? skb[C].y : skb[C].z;
-                        wide_mfma<MB, NPW>(acc, mi, ni, RA[s][mi], RBk[C][s][ni], sa, sb);
+                        wide_mfma<MB, NPW>(acc, mi, ni, RA[cur][mi], RBk[C][s][ni], sa, sb);
 #pragma unroll
                         for (int i = 0; i < MB; i++)
                             if (k == G::read_k(i) && (MORE || s + 1 < SUBS))
@@ -318,20 +322,26 @@ __global__ void __launch_bounds__(256, 1)
                 }
             };
             step(std::integral_constant<int, 0>{});
-            step(std::integral_constant<int, 1>{});
+            if constexpr (NK >= 2) step(std::integral_constant<int, 1>{});
             if constexpr (NK == 3) step(std::integral_constant<int, 2>{});
             store_tile<MB, NPW, OutT, SPLIT, MASK, STREAM>(acc, D, ws, M, N,
                                                         wg_m * MT + 4 * (lane >> 5),
                                                         wg_n * NT + wave * NPW * 32 + (lane & 31),
                                                         lane, wg_z);
         };
-        if (nkt == 2) {
-            short_path(std::integral_constant<int, 2>{});
+        if (nkt == 1) {
+            short_path(std::integral_constant<int, 1>{});
             return;
         }
-        if (nkt == 3) {
-            short_path(std::integral_constant<int, 3>{});
-            return;
+        if constexpr (G::SHORT_MAX >= 3) {
+            if (nkt == 2) {
+                short_path(std::integral_constant<int, 2>{});
+                return;
+            }
+            if (nkt == 3) {
+                short_path(std::integral_constant<int, 3>{});
+                return;
+            }
         }
     }
 
