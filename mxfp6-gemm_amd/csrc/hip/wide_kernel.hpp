@@ -32,11 +32,13 @@
 // current one is free for the copies of K-tile c + NB - 1. The B loads and scale loads are
 // ordinary loads whose waits the compiler places before the MFMAs that use them.
 // Prefetches past the workgroup's last K-tile are clamped to that K-tile (valid addresses, data
-// never used), so the K loop has no branch. A 128 x 384 workgroup with a single K-tile, or a
-// 128 x 256 one with up to three (K <= 576, or a split segment that short), takes a short path
-// instead: every K-tile's chunk, scales and B operands (a register set per K-tile) are requested
-// before the first MFMA, so no K-tile waits out a memory latency for B loads issued during the
-// one before it, and no clamped prefetch is issued. MASK (ragged M or N) clamps the copy and load sources
+// never used), so the K loop has no branch. A workgroup with a single K-tile, or a 128 x 256 one
+// with up to three (K <= 576, or a split segment that short), takes a short path instead: every
+// K-tile's chunk, scales and B operands (a register set per K-tile) are requested before the
+// first MFMA, so no K-tile waits out a memory latency for B loads issued during the one before
+// it, and no clamped prefetch is issued (128 x 512 and 256 x 256 run single K-tiles in an
+// instantiation of their own, ONE, unmasked only: with the path in their main kernel the masked
+// and repacked-A instantiations would spill, and so would a masked ONE). MASK (ragged M or N) clamps the copy and load sources
 // of the last tile row and column and masks the stores, as in the slab kernel.
 #pragma once
 
@@ -107,7 +109,7 @@ struct WideGeom {
     static_assert(copy_k(cps(0) - 1) < NMF, "copy positions");
     static_assert(read_k(MB - 1) < NMF, "read positions");
     static_assert(CHUNK_WAIT <= 63 && PRO_WAIT <= 63, "vmcnt range");
-    static_assert(SHORT_MAX == 0 || short_wait(SHORT_MAX, 0) <= 63, "vmcnt range (short path)");
+    static_assert(short_wait(SHORT_MAX > 0 ? SHORT_MAX : 1, 0) <= 63, "vmcnt range (short path)");
 };
 
 // acc[mi][ni] += A(mi) * B(ni) with the scale bytes mi % 4 of sa and ni of sb (op_sel must be a
@@ -128,7 +130,7 @@ __device__ __forceinline__ void wide_mfma(v16f (&acc)[MB][NPW], int mi, int ni, 
 }
 
 template <int MB_, int NPW_, int NB_, int XG, typename OutT, bool SPLIT, bool ASH, bool MASK,
-          bool STREAM>
+          bool STREAM, bool ONE = false>
 __global__ void __launch_bounds__(256, 1)
     wide_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
@@ -259,7 +261,7 @@ __global__ void __launch_bounds__(256, 1)
     v3i sc_a[NGA], sc_b;   // scale dwords of the current K-tile
     v3i sn_a[NGA], sn_b;   // and of the next one
 
-    if constexpr (G::SHORT_MAX > 0) {
+    if constexpr (G::SHORT_MAX > 0 || ONE) {
         // One K-tile, or on the 128 x 256 tile up to three (K <= 576, or a split segment that
         // short): every K-tile's chunk, scales and B operands (a register set per K-tile) are
         // requested before the first MFMA, so no K-tile waits for loads issued during the one
@@ -329,6 +331,12 @@ __global__ void __launch_bounds__(256, 1)
                                                         wg_n * NT + wave * NPW * 32 + (lane & 31),
                                                         lane, wg_z);
         };
+        if constexpr (ONE) {
+            // the instantiation for single K-tiles of the tiles without the path in their main
+            // kernel: nothing of the main loop is compiled in (the code below is unreachable)
+            short_path(std::integral_constant<int, 1>{});
+            return;
+        }
         if (nkt == 1) {
             short_path(std::integral_constant<int, 1>{});
             return;
@@ -452,6 +460,16 @@ hipError_t wide_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipS
     using G = WideGeom<MB, NPW, NB>;
     const dim3 grid((unsigned)((d->M + G::MT - 1) / G::MT), (unsigned)((d->N + G::NT - 1) / G::NT),
                     (unsigned)d->splits);
+    if constexpr (G::SHORT_MAX == 0 && !MASK) {
+        // every K segment a single K-tile: the short-path instantiation (not for masked tiles,
+        // whose instantiation of it would spill)
+        if (d->Kp / 192 == d->splits)
+            return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK, STREAM, true>,
+                                 grid, dim3(G::THREADS), st, A,
+                                 static_cast<const uint8_t*>(d->Bsh), d->sA, d->sB,
+                                 SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr,
+                                 d->M, d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1);
+    }
     return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK, STREAM>, grid,
                          dim3(G::THREADS), st, A, static_cast<const uint8_t*>(d->Bsh), d->sA,
                          d->sB, SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr,

@@ -49,6 +49,20 @@ def test_wide_split_bitwise_equals_direct_split(WIDE, M, tn, S):
 
 
 @pytest.mark.parametrize("WIDE", WIDE_TILES)
+@pytest.mark.parametrize("S,K", [(1, 192), (3, 576), (6, 1152)])
+def test_wide_single_k_tile_segments(WIDE, S, K):
+    """Every K segment one K-tile (the short path, or for 128 x 512 and 256 x 256 their
+    single-K-tile instantiation): bit for bit the direct kernel, rows and repacked A."""
+    M, N = 512, WIDE[1] * 2
+    p = mx.make_problem(M, N, K, seed=S * 11 + K)
+    dp = g.DevProblem(p, WIDE)
+    for a_layout in (0, 1):
+        Dw = g.run_explicit(dp, mx.OUT_F32, splits=S, a_layout=a_layout)
+        Dd = g.run_direct(dp, mx.OUT_F32, splits=S)
+        assert np.array_equal(Dw.view(np.uint32), Dd.view(np.uint32)), a_layout
+
+
+@pytest.mark.parametrize("WIDE", WIDE_TILES)
 @pytest.mark.parametrize("M,N,K", [(300, 700, 960), (97, 1000, 2112), (129, 513, 384),
                                    (1, 33, 192)])
 def test_wide_masked_equals_slab_masked(WIDE, M, N, K):
