@@ -17,6 +17,7 @@ pytestmark = pytest.mark.gpu
     (2048, 102272, 1024, mx.OUT_F16),   # 256x256 wide tile, last tile column masked
     (1024, 102272, 2048, mx.OUT_BF16),
     (4096, 16384, 1024, mx.OUT_F32),
+    (8192, 12288, 192, mx.OUT_F32),     # a single K-tile: the 256x256 tile's single-K-tile kernel
 ])
 def test_routed_streaming_plan_equals_direct_kernel(M, N, K, out_type):
     p = mx.make_problem(M, N, K, seed=M + 11 * N + K)
