@@ -36,9 +36,10 @@
 // with up to three (K <= 576, or a split segment that short), takes a short path instead: every
 // K-tile's chunk, scales and B operands (a register set per K-tile) are requested before the
 // first MFMA, so no K-tile waits out a memory latency for B loads issued during the one before
-// it, and no clamped prefetch is issued (128 x 512 and 256 x 256 run single K-tiles in an
-// instantiation of their own, ONE, unmasked only: with the path in their main kernel the masked
-// and repacked-A instantiations would spill, and so would a masked ONE). MASK (ragged M or N) clamps the copy and load sources
+// it, and no clamped prefetch is issued (128 x 512 and 256 x 256 run segments of one or two
+// K-tiles in instantiations of their own, ONE = 1 or 2, unmasked only: with the path in their
+// main kernel the masked and repacked-A instantiations would spill, and so would a masked ONE).
+// MASK (ragged M or N) clamps the copy and load sources
 // of the last tile row and column and masks the stores, as in the slab kernel.
 #pragma once
 
@@ -130,7 +131,7 @@ __device__ __forceinline__ void wide_mfma(v16f (&acc)[MB][NPW], int mi, int ni, 
 }
 
 template <int MB_, int NPW_, int NB_, int XG, typename OutT, bool SPLIT, bool ASH, bool MASK,
-          bool STREAM, bool ONE = false>
+          bool STREAM, int ONE = 0>
 __global__ void __launch_bounds__(256, 1)
     wide_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
@@ -261,7 +262,7 @@ __global__ void __launch_bounds__(256, 1)
     v3i sc_a[NGA], sc_b;   // scale dwords of the current K-tile
     v3i sn_a[NGA], sn_b;   // and of the next one
 
-    if constexpr (G::SHORT_MAX > 0 || ONE) {
+    if constexpr (G::SHORT_MAX > 0 || ONE > 0) {
         // One K-tile, or on the 128 x 256 tile up to three (K <= 576, or a split segment that
         // short): every K-tile's chunk, scales and B operands (a register set per K-tile) are
         // requested before the first MFMA, so no K-tile waits for loads issued during the one
@@ -269,6 +270,7 @@ __global__ void __launch_bounds__(256, 1)
         // LDS buffer c.
         auto short_path = [&](auto nk) {
             constexpr int NK = decltype(nk)::value;
+            static_assert(G::short_wait(NK, 0) <= 63, "vmcnt range (short path)");
             v8i RBk[NK][SUBS][NPW];
             v3i ska[NK][NGA], skb[NK];
 #pragma unroll
@@ -331,10 +333,10 @@ __global__ void __launch_bounds__(256, 1)
                                                         wg_n * NT + wave * NPW * 32 + (lane & 31),
                                                         lane, wg_z);
         };
-        if constexpr (ONE) {
-            // the instantiation for single K-tiles of the tiles without the path in their main
-            // kernel: nothing of the main loop is compiled in (the code below is unreachable)
-            short_path(std::integral_constant<int, 1>{});
+        if constexpr (ONE > 0) {
+            // the instantiation for segments of ONE K-tiles of the tiles without the path in their
+            // main kernel: nothing of the main loop is compiled in (the code below is unreachable)
+            short_path(std::integral_constant<int, ONE>{});
             return;
         }
         if (nkt == 1) {
@@ -461,10 +463,16 @@ hipError_t wide_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipS
     const dim3 grid((unsigned)((d->M + G::MT - 1) / G::MT), (unsigned)((d->N + G::NT - 1) / G::NT),
                     (unsigned)d->splits);
     if constexpr (G::SHORT_MAX == 0 && !MASK) {
-        // every K segment a single K-tile: the short-path instantiation (not for masked tiles,
-        // whose instantiation of it would spill)
+        // every K segment one or two K-tiles: the short-path instantiations (not for masked
+        // tiles, whose instantiations of it would spill)
+        if (d->Kp / 192 == 2 * d->splits)
+            return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK, STREAM, 2>,
+                                 grid, dim3(G::THREADS), st, A,
+                                 static_cast<const uint8_t*>(d->Bsh), d->sA, d->sB,
+                                 SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr,
+                                 d->M, d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1);
         if (d->Kp / 192 == d->splits)
-            return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK, STREAM, true>,
+            return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK, STREAM, 1>,
                                  grid, dim3(G::THREADS), st, A,
                                  static_cast<const uint8_t*>(d->Bsh), d->sA, d->sB,
                                  SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr,

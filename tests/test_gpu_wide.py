@@ -49,10 +49,10 @@ def test_wide_split_bitwise_equals_direct_split(WIDE, M, tn, S):
 
 
 @pytest.mark.parametrize("WIDE", WIDE_TILES)
-@pytest.mark.parametrize("S,K", [(1, 192), (3, 576), (6, 1152)])
+@pytest.mark.parametrize("S,K", [(1, 192), (3, 576), (6, 1152), (1, 384), (3, 1152)])
 def test_wide_single_k_tile_segments(WIDE, S, K):
-    """Every K segment one K-tile (the short path, or for 128 x 512 and 256 x 256 their
-    single-K-tile instantiation): bit for bit the direct kernel, rows and repacked A."""
+    """Every K segment one or two K-tiles (the short path, or for 128 x 512 and 256 x 256 their
+    short-path instantiations): bit for bit the direct kernel, rows and repacked A."""
     M, N = 512, WIDE[1] * 2
     p = mx.make_problem(M, N, K, seed=S * 11 + K)
     dp = g.DevProblem(p, WIDE)
