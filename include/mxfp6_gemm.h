@@ -94,7 +94,10 @@ int mxfp6_gemm_async(int out_type, int M, int N, int Kp, const void* dA, const v
  * another tile of the routed scale grouping: the same bits). A shape whose split-K
  * partials (mxfp6_gemm_workspace_size) exceed the scratch is rejected with MXFP6_ERR_SCRATCH,
  * before any device work. Every call on a GPU shares that GPU's scratch: calls that overlap on one
- * GPU (concurrent streams or host threads) race; serialise them. No counterpart in the reference:
+ * GPU (concurrent streams or host threads) race; serialise them. The first call on a GPU looks the
+ * scratch's device address up (hipGetSymbolAddress, which may load the code object): make it
+ * outside stream capture, e.g. once eagerly at set-up; later calls may be captured into a HIP
+ * graph. No counterpart in the reference:
  * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). */
 int mxfp6_gemm_noalloc_async(int out_type, int M, int N, int Kp, const void* dA,
@@ -169,10 +172,13 @@ int mxfp6_gemm_tune_load(const char* path, int* loaded, int* skipped);
 int mxfp6_gemm_plan(int out_type, int M, int N, int Kp, size_t ws_bytes, int tile[4], int* splits,
                     int* a_repack);
 
-/* Whether gemm()'s plan for (out_type, M, N, Kp, A_row_bytes) writes D with nontemporal stores
+/* Whether the routed plan for (out_type, M, N, Kp, A_row_bytes) writes D with nontemporal stores
  * (unsplit plans whose operands fit in MI355X's 256 MiB last-level cache but whose operands and D
- * together do not). No counterpart in the reference (its epilogue stores are plain); D's values
- * are the same either way. */
+ * together do not). The answer is for the plan gemm() runs with the preferred workspace
+ * (mxfp6_gemm_preferred_workspace_size) and no measured plan registered for the shape; a measured
+ * plan or a shorter workspace can run another plan, whose stores are decided the same way from
+ * that plan. No counterpart in the reference (its epilogue stores are plain); D's values are the
+ * same either way. */
 int mxfp6_gemm_streams_output(int out_type, int M, int N, int Kp, int A_row_bytes);
 
 /* Workspace bytes of an explicit plan (0 when splits == 1 and a_repack == 0). */

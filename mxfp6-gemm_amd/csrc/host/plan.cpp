@@ -159,10 +159,15 @@ void visit_plans(int M, int N, int Kp, F&& f) {
                 for (int ci = 0; ci < kNCands + kNSkinny && S <= k_tiles; ci++) {
                     const TileChoice& tc = ci < kNCands ? kCands[ci] : kSkinny[ci - kNCands];
                     if (reg && (M % tc.MT != 0 || (N % tc.NT != 0) != (pass == 1))) continue;
-                    // a regular shape's scales may be tiled by the header's tile_scale, which
-                    // holds floor(dim / (32 * group)) whole groups: the grouping must divide the
-                    // shape (an N-masked 256x192 or 128x384, NPW 3, needs (N / 32) % 3 == 0)
-                    if (reg && ((M / 32) % tc.MPW != 0 || (N / 32) % tc.NPW != 0)) continue;
+                    // a dimension that is a whole number of 32-blocks may have its scales tiled
+                    // by the header's tile_scale, which holds floor(dim / (32 * group)) whole
+                    // groups, while a masked tile reads up to group ceil(dim / (32 * group)) - 1:
+                    // the grouping must divide dim / 32 (N = 4000, 125 blocks, excludes NPW 2
+                    // and 4; an N-masked 128x384, NPW 3, needs (N / 32) % 3 == 0). Ragged
+                    // dimensions cannot go through the header and take the C ABI's ceil layout.
+                    if ((M % 32 == 0 && (M / 32) % tc.MPW != 0) ||
+                        (N % 32 == 0 && (N / 32) % tc.NPW != 0))
+                        continue;
                     f(tc, S, rp != 0);
                 }
 }

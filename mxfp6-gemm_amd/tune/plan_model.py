@@ -1,5 +1,6 @@
 """The router's plan-time model (csrc/host/plan.cpp plan_time_us / best_plan) in Python, and its
-fit to measured plans (sweep_plans.py output), which scores the plans the model picks.
+fit to measured plans (plans_mi355x.jsonl: one JSON line per shape with every plan's measured
+time on one MI355X), which scores the plans the model picks.
 
   python mxfp6-gemm_amd/tune/plan_model.py [plans.jsonl ...]   # refit, print the constants and
                                                               # how close the picks come to the
@@ -81,8 +82,9 @@ def plan_time_us(c, tile, M, N, Kp, S, repack):
 def candidates(M, N, Kp):
     """The plans best_plan visits, in its order. Regular shapes (M % 32 == 0, N % 128 == 0) take
     the tiles whose MT divides M, the 32- and 64-row ones included (the last tile column masked
-    when NT does not divide N, visited after every dividing plan) whose scale grouping divides
-    the shape; ragged ones any tile, masked."""
+    when NT does not divide N, visited after every dividing plan); ragged ones any tile, masked.
+    On every shape the scale grouping divides each dimension that is a whole number of
+    32-blocks."""
     kt = Kp // K_TILE
     regular = M % 32 == 0 and N % 128 == 0
     cands = (SKINNY if M % 128 else TILES + SKINNY) if regular else TILES + SKINNY
@@ -95,8 +97,10 @@ def candidates(M, N, Kp):
                 for tile in cands:
                     if regular and (M % tile[0] or bool(N % tile[1]) != masked):
                         continue
-                    # the header's tile_scale holds whole scale groups only
-                    if regular and ((M // 32) % tile[2] or (N // 32) % tile[3]):
+                    # the header's tile_scale holds whole scale groups only: on a dimension
+                    # of whole 32-blocks the grouping must divide dim / 32
+                    if (M % 32 == 0 and (M // 32) % tile[2]) or \
+                            (N % 32 == 0 and (N // 32) % tile[3]):
                         continue
                     out.append((tile, S, rp))
     return out

@@ -73,8 +73,45 @@ def test_router_covers_every_multiple_of_128(mx):
     assert not bad and not badgroup and masked > 0, (bad[:5], badgroup[:5])
 
 
+def test_router_grouping_divides_every_multiple_of_32(mx):
+    """Every M and N multiple of 32 (N not a multiple of 128 included, where the last tile column
+    is masked): the routed grouping divides M/32 and N/32, so the header's recipe
+    tile_scale(preprocess_scale(.., dim, Kp), group, 3) holds every scale group the kernel reads,
+    and its size is the device layout's. A grouping that left a partial group (N = 4000 on
+    NPW 2: 62 whole groups from the header, 63 read by the masked kernel) would read past the
+    header-sized scale buffer."""
+    lib = mx.lib()
+    bad = []
+    for K in (1024, 8192, 105728):
+        Kp = _kpad(K)
+        for M in range(32, 8193, 32):
+            for N in range(32, 16385, 32):
+                t = mx.choose_tile(M, N, Kp)
+                if (M // 32) % t[2] or (N // 32) % t[3]:
+                    bad.append((M, N, K, tuple(t)))
+        # sizes: the header's floor count equals the kernel's ceil count for the routed grouping
+        for M, N in ((4096, 4000), (1024, 4064), (256, 2720), (96, 4000), (8192, 8320)):
+            t = mx.choose_tile(M, N, Kp)
+            for dim, g in ((M, t[2]), (N, t[3])):
+                hdr = lib.mxfp6_tile_scale_bytes(dim, Kp, g, 3)
+                if hdr == 0 or hdr != mx.tiled_scale_bytes(dim, Kp, g):
+                    bad.append((M, N, K, tuple(t), dim, g))
+    assert not bad, (len(bad), bad[:8])
+
+
+def test_router_grouping_planted_partial_group_is_caught(mx):
+    """The check above fails on a grouping with a partial group: N = 4000 (125 blocks) with
+    NPW 2 leaves one block over, and the header's buffer is one group short of the kernel's."""
+    Kp = _kpad(8192)
+    assert (4000 // 32) % 2 == 1
+    assert mx.lib().mxfp6_tile_scale_bytes(4000, Kp, 2, 3) == 0  # the C ABI refuses it
+    floor_groups, ceil_groups = 4000 // 32 // 2, -(-(4000 // 32) // 2)
+    assert ceil_groups == floor_groups + 1
+
+
 @pytest.mark.parametrize("M,N,K", [(512, 8320, 8192), (640, 13184, 1024), (128, 6016, 105728),
-                                   (8192, 8320, 8192), (2048, 1152, 16128)])
+                                   (8192, 8320, 8192), (2048, 1152, 16128), (4096, 4000, 8192),
+                                   (1024, 4064, 4096), (256, 2720, 8192)])
 def test_header_tile_scale_size_matches_kernel_layout(mx, M, N, K):
     """On shapes where an N-masked tile with three 32-column blocks per wave would have been
     chosen, the header-sized scale buffers (tile_scale_bytes, floor) equal the size of the layout

@@ -29,6 +29,13 @@ BINS = {"shared": os.path.join(HERE, "dropin_gemm"),
     (512, 8320, 8192, 1, "static", "preferred"),
     (2048, 8192, 4096, 1, "shared", "preferred"),  # a plan that repacks A into the workspace
     (2048, 8192, 4096, 2, "static", "ref"),        # the same plan on row-major A
+    # N a multiple of 32 but not of 128 (last tile column masked): N/32 = 125 and 85 are odd, so
+    # a grouping of two or four blocks would leave a partial scale group that the header's
+    # tile_scale drops and the masked kernel reads
+    (4096, 4000, 8192, 1, "shared", "ref"),
+    (4096, 4000, 8192, 2, "static", "ref"),
+    (256, 2720, 8192, 1, "shared", "ref"),
+    (256, 2720, 8192, 0, "static", "preferred"),
 ])
 def test_cpp_caller(M, N, K, out_type, link, ws):
     exe = BINS[link]

@@ -53,7 +53,7 @@ def test_routed_small_shapes(g, orc, out_type, M, N, K):
                                   (256, 192, 4, 3), (128, 512, 4, 4)])
 @pytest.mark.parametrize("out_type", [0, 1, 2])
 def test_forced_tiles(g, orc, tile, out_type):
-    M, N, K = 256, 768, 960  # K-tail: kpad(960) = 1152
+    M, N, K = 256, 1536, 960  # every tile divides 256 x 1536; K-tail: kpad(960) = 1152
     p = mx.make_problem(M, N, K, dist_a=mx.DIST_STUDENT_T3, dist_b=mx.DIST_STUDENT_T3, seed=11)
     D = g.run_forced(g.DevProblem(p, tile), out_type)
     R, ab = _oracle(orc, p)

@@ -63,6 +63,27 @@ def test_wide_single_k_tile_segments(WIDE, S, K):
 
 
 @pytest.mark.parametrize("WIDE", WIDE_TILES)
+@pytest.mark.parametrize("K", [192, 384, 576])
+def test_wide_short_path_lowp_outputs(WIDE, K):
+    """Unsplit K of one to three K-tiles (the short path, or the short-path instantiations of
+    128 x 512 and 256 x 256) with 16-bit outputs: FP32 equals the direct kernel bit for bit, and
+    FP16 / BF16 equal that FP32 rounded to nearest-even on the host, rows and repacked A."""
+    M, N = 512, WIDE[1] * 2
+    p = mx.make_problem(M, N, K, dist_a=mx.DIST_STUDENT_T3, dist_b=mx.DIST_STUDENT_T3,
+                        seed=K * 5 + WIDE[1])
+    dp = g.DevProblem(p, WIDE)
+    Dd = g.run_direct(dp, mx.OUT_F32)
+    for a_layout in (0, 1):
+        D32 = g.run_explicit(dp, mx.OUT_F32, a_layout=a_layout)
+        assert np.array_equal(D32.view(np.uint32), Dd.view(np.uint32)), a_layout
+        D16 = g.run_explicit(dp, mx.OUT_F16, a_layout=a_layout)
+        want16 = D32.astype(np.float16).astype(np.float32)
+        assert np.array_equal(D16.view(np.uint32), want16.view(np.uint32)), a_layout
+        Db16 = g.run_explicit(dp, mx.OUT_BF16, a_layout=a_layout)
+        assert np.array_equal(Db16.view(np.uint32), checks.round_bf16(D32).view(np.uint32)), a_layout
+
+
+@pytest.mark.parametrize("WIDE", WIDE_TILES)
 @pytest.mark.parametrize("M,N,K", [(300, 700, 960), (97, 1000, 2112), (129, 513, 384),
                                    (1, 33, 192)])
 def test_wide_masked_equals_slab_masked(WIDE, M, N, K):
