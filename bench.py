@@ -39,7 +39,10 @@ loop; `sclk_mhz` reports the clock the loop ran at). Besides the contract fields
   per_config    the five workloads, this library and the reference library each timed by that
                 same method on identical operands: TFLOPs, fraction of 10.1 PF, ratio, and for the
                 split-K workload the algorithmic HBM GB/s;
-  cpu_baseline  the reference CPU GEMM's arithmetic on this host (a bounded sample, scaled).
+  cpu_baseline  the reference CPU GEMM's arithmetic on this host's CPU share (OMP_NUM_THREADS
+                threads, else every CPU the process may use; the count is in `cores`): for the
+                headline a bounded sample of A rows scaled to the whole GEMM, and in each
+                per_config entry the same for that workload (the small one in full).
 The reference library and the oracle are baselines only: nothing here routes the measured GEMM
 through them.
 """
@@ -154,15 +157,27 @@ def frac_at(tflops, mhz):
     return round(tflops * 1e12 / (FLOP_PER_CLK * mhz * 1e6), 4) if mhz else None
 
 
+def host_threads():
+    """Threads for the CPU baseline: the process's CPU share. OMP_NUM_THREADS when set (a GPU box
+    gives one GPU's jobs 16 host threads and sets it so), else the CPUs this process may run on;
+    never more than the latter."""
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        want = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        want = 0
+    return max(1, min(avail, want) if want > 0 else avail)
+
+
 def cpu_baseline(p, target_cpu_s=12.0):
     """The reference CPU GEMM's arithmetic (tests/reference.hpp: dequantise both operands to FP32,
     then one sequential FP32 dot per output; the oracle's restatement, pinned bit-exact to the
     reference function) on the same operands, on this host's cores. B is dequantised once (timed);
     the dots are timed on a bounded sample of A rows and scaled by M / rows (their cost is exactly
-    linear in the number of rows)."""
+    linear in the number of rows); a workload whose dots fit the time target runs in full."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = host_threads()
     t0 = time.perf_counter()
     bf = oracle.dequant_f32(p.b_packed, p.b_row_bytes, p.b_scales, p.N, p.K)
     t_deq = time.perf_counter() - t0
@@ -178,11 +193,14 @@ def cpu_baseline(p, target_cpu_s=12.0):
                             nthreads=threads)
     t_rows = time.perf_counter() - t0
     full = t_deq + t_rows * p.M / nrows
+    whole = nrows == p.M
     return {"value": round(2.0 * p.M * p.N * p.K / full / 1e12, 6), "unit": "TFLOP/s",
-            "cores": threads, "kind": "port",
-            "sample": f"B dequantised once ({t_deq:.2f} s, 1 thread) + dots of {nrows} of {p.M} "
-                      f"A rows x {p.N} columns ({t_rows:.2f} s on {threads} threads), "
-                      f"scaled x{p.M / nrows:.1f}: {full:.1f} s per GEMM"}
+            "cores": threads, "host_cpus": os.cpu_count(), "kind": "port", "full": whole,
+            "sample": f"B dequantised once ({t_deq:.2f} s, 1 thread) + dots of "
+                      + (f"all {p.M} A rows x {p.N} columns ({t_rows:.3f} s on {threads} threads): "
+                         f"{full:.3f} s per GEMM" if whole else
+                         f"{nrows} of {p.M} A rows x {p.N} columns ({t_rows:.2f} s on {threads} "
+                         f"threads), scaled x{p.M / nrows:.1f}: {full:.1f} s per GEMM")}
 
 
 def copy_calibration(mib=256, reps=5):
@@ -439,6 +457,7 @@ def run(names, steps, warmup, with_cpu, with_ref, per_config):
     import torch
     ref = reference_library() if with_ref else None
     lines = []
+    cpu_done = {}
     for n in names:
         w, out = headline(n, steps, warmup, ref)
         if ref is not None:
@@ -453,6 +472,7 @@ def run(names, steps, warmup, with_cpu, with_ref, per_config):
         if with_cpu and n == names[0]:
             log(f"[bench] {n}: CPU baseline ...")
             out["cpu_baseline"] = cpu_baseline(w.p)
+            cpu_done[n] = out["cpu_baseline"]
         lines.append((w, out))
         del w
         torch.cuda.empty_cache()
@@ -461,6 +481,13 @@ def run(names, steps, warmup, with_cpu, with_ref, per_config):
         for n in sorted(CONFIGS):
             w = Workload(n, ref)
             pc[n] = compare(w, torch.cuda.current_stream())
+            if with_cpu:
+                # every workload beside the reference CPU path (the headline's own sample where
+                # it was just taken; the small workload runs in full)
+                if n not in cpu_done:
+                    log(f"[bench] {n}: CPU baseline ...")
+                    cpu_done[n] = cpu_baseline(w.p)
+                pc[n]["cpu_baseline"] = cpu_done[n]
             del w
             torch.cuda.empty_cache()
         lines[0][1]["per_config"] = pc
