@@ -12,6 +12,11 @@ drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX 
   python bench.py --prep      (device operand preparation: float -> MXFP6 device layouts, GB/s)
   python bench.py --power S   (board power and clocks over S seconds of back-to-back GEMMs of the
                                workload, this library then the reference library; amd-smi)
+  python bench.py --roof [S]  (the MFMA-only diagnostic kernel against the workload's GEMM: the
+                               cycles per MFMA and the board's power roof, each sustained S s)
+  python bench.py --ab PLANS [--config cN] [--repeat R]  (explicit plans MTxNTxMPWxNPW[:S[:r]]
+                               of a workload against each other and the routed plan, R rounds,
+                               order rotated)
   python bench.py --map [SHAPES|second] [--repeat R]  (this library against the reference library,
                                shape by shape: MxNxK,... or the default map of 154 shapes, FP16
                                out; R > 1: R more runs per library, alternating their order)
@@ -736,6 +741,164 @@ def run_power(name, seconds):
     return out
 
 
+def run_ab(name, plans, repeat):
+    """Explicit plans of one workload against each other (and the routed plan), on the same
+    operands, each timed by the reference's method (compare()'s best_of), `repeat` rounds with
+    the order rotating every round; prints one JSON line with every plan's series and median.
+    plans: "MTxNTxMPWxNPW[:S[:r]]" separated by commas (S K segments, r for a repacked A)."""
+    import torch
+    w = Workload(name)
+    M, N, Kp, p = w.M, w.N, w.p.Kp, w.p
+    stream = torch.cuda.current_stream()
+    dev = torch.device("cuda:0")
+    entries = [("routed", lambda: w.ours(stream))]
+    keep = []
+    for spec in plans.split(","):
+        parts = spec.strip().split(":")
+        tile = tuple(int(v) for v in parts[0].split("x"))
+        S = int(parts[1]) if len(parts) > 1 else 1
+        rp = len(parts) > 2 and parts[2] == "r"
+        _, sa, sb = p.layouts(tile)
+        dsa, dsb = torch.from_numpy(sa).to(dev), torch.from_numpy(sb).to(dev)
+        wsb = mx.plan_workspace_size(M, N, Kp, S, rp)
+        ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=dev)
+        keep.append((dsa, dsb, ws))
+
+        def fn(tile=tile, S=S, rp=rp, dsa=dsa, dsb=dsb, ws=ws, wsb=wsb):
+            rc = mx.gemm_explicit(w.ot, M, N, Kp, tile, S, w.dA.data_ptr(), w.dB.data_ptr(),
+                                  dsa.data_ptr(), dsb.data_ptr(), w.D.data_ptr(), p.a_row_bytes,
+                                  ws.data_ptr() if wsb else 0, wsb, stream=stream.cuda_stream,
+                                  a_layout=mx.A_REPACK if rp else mx.A_ROWS)
+            if rc != 0:
+                raise RuntimeError(f"plan {tile} S {S}: {mx.STATUS.get(rc, rc)}")
+        entries.append((spec.strip(), fn))
+    series = {k: [] for k, _ in entries}
+    for r in range(repeat):
+        order = entries[r % len(entries):] + entries[:r % len(entries)]
+        for k, fn in order:
+            series[k].append(round(best_of(fn, stream)[0] * 1e3, 2))
+    out = {"workload": workload_name(M, N, w.K, w.ot), "routed": {"tile": list(w.tile),
+           "splitk": w.S, "a_repacked": w.repack}, "repeat": repeat,
+           "method": "best mean of 4 x 20 launches after 8 warm-ups per run; plan order rotated "
+                     "every run", "us": series,
+           "median_us": {k: float(np.median(v)) for k, v in series.items()}}
+    return out
+
+
+def diag_library():
+    """libmxfp6diag.so (the MFMA-only diagnostic kernel), loaded with ctypes."""
+    import ctypes as C
+    path = os.path.join(ROOT, "mxfp6-gemm_amd", "lib", "libmxfp6diag.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"{path} missing: build with make -C mxfp6-gemm_amd")
+    lib = C.CDLL(path)
+    f = lib.mxfp6_diag_mfma_roof_async
+    f.restype = C.c_int
+    f.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int,
+                  C.c_void_p, C.c_void_p]
+    return lib
+
+
+def run_roof(name, steps, warmup, seconds):
+    """The MFMA-only diagnostic against the GEMM of one workload, in one process: the MFMA stream
+    of the workload's tile kernel (its grid, its K slabs, 16 accumulators per wave for the 256x256
+    tile) with every data path taken out, on the workload's real operand codes and scales. Both
+    are timed like the headline (warmup, then `steps` launches between events, the clock sampled
+    around them), and then each sustained for `seconds` with amd-smi sampling the board's power
+    and clock. The diagnostic's cycle count per MFMA (from each wave's s_memtime) shows the issue
+    rate of back-to-back MFMAs; its sustained rate is what the board's power limit leaves of the
+    dense MXFP6 peak: the practical roof of any tile kernel on this board."""
+    import torch
+    w = Workload(name)
+    if tuple(w.tile[:2]) not in ((256, 256), (128, 384)) or w.S != 1:
+        raise SystemExit(f"--roof: workload {name} is not an unsplit 256x256 or 128x384 route")
+    lib = diag_library()
+    shape = 0 if tuple(w.tile[:2]) == (256, 256) else 1
+    mb, npw = (8, 2) if shape == 0 else (4, 3)
+    wgs = -(-w.M // w.tile[0]) * -(-w.N // w.tile[1])
+    slabs = w.p.Kp // 64
+    cyc = torch.zeros(wgs * 4, dtype=torch.int64, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    op_blocks = w.dB.numel() // 1536
+    sc_dwords = w.dsb.numel() // 4
+
+    def roof():
+        if lib.mxfp6_diag_mfma_roof_async(shape, w.dB.data_ptr(), op_blocks, w.dsb.data_ptr(),
+                                          sc_dwords, cyc.data_ptr(), wgs, slabs, None,
+                                          stream.cuda_stream):
+            raise RuntimeError("mfma roof launch failed")
+
+    mfma_flops = float(wgs) * 4 * slabs * mb * npw * 2 * 32 * 32 * 64
+    out = {"metric": "MFMA-only roof vs GEMM, 1xMI355X", "workload": workload_name(w.M, w.N, w.K, w.ot),
+           "tile": list(w.tile), "roof_grid": wgs, "roof_slabs": slabs,
+           "roof_mfmas_per_wave": slabs * mb * npw, "steps": steps, "warmup": warmup,
+           "power_cap_w": power_cap_w()}
+    for label, fn, flops in (("mfma_only", roof, mfma_flops), ("gemm", lambda: w.ours(stream), w.flops)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        clock = ClockProbe()
+        clock.start(stream)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        sclk = clock.stop(stream)
+        ms = e0.elapsed_time(e1) / steps
+        tf = flops / ms / 1e9
+        r = {"us": round(ms * 1e3, 2), "tflops": round(tf, 1), "frac": round(tf / PEAK_TFLOPS, 4),
+             "sclk_mhz": sclk, "frac_at_sclk": frac_at(tf, sclk)}
+        if label == "mfma_only":
+            c = cyc.cpu().numpy().astype(np.float64)
+            r["cycles_per_mfma_mean"] = round(float(c.mean()) / (slabs * mb * npw), 2)
+            r["cycles_per_mfma_min"] = round(float(c.min()) / (slabs * mb * npw), 2)
+        out[label] = r
+        log(f"[bench] roof {label}: {r}")
+    if seconds > 0:
+        for label, fn, flops in (("mfma_only", roof, mfma_flops), ("gemm", lambda: w.ours(stream), w.flops)):
+            samples, done = [], threading.Event()
+
+            def sample():
+                while not done.is_set():
+                    v = smi_power_clock()
+                    if v is not None:
+                        samples.append(v)
+                    done.wait(0.25)
+            t0 = time.time()
+            while time.time() - t0 < 1.0:
+                for _ in range(20):
+                    fn()
+                torch.cuda.synchronize()
+            th = threading.Thread(target=sample)
+            th.start()
+            calls, t1 = 0, time.time()
+            while time.time() - t1 < seconds:
+                for _ in range(20):
+                    fn()
+                torch.cuda.synchronize()
+                calls += 20
+            el = time.time() - t1
+            done.set()
+            th.join()
+            pw = [v[0] for v in samples]
+            ck = [v[1] for v in samples if v[1] is not None]
+            tf = flops * calls / el / 1e12
+            out[label]["sustained"] = {
+                "seconds": round(el, 1), "calls": calls, "tflops": round(tf, 1),
+                "frac": round(tf / PEAK_TFLOPS, 4),
+                "socket_power_w_mean": round(sum(pw) / len(pw), 1) if pw else None,
+                "gfx_clock_mhz_mean": round(sum(ck) / len(ck), 1) if ck else None,
+                "samples": len(samples)}
+            log(f"[bench] roof {label} sustained: {out[label]['sustained']}")
+    out["gemm_over_roof"] = round(out["gemm"]["tflops"] / out["mfma_only"]["tflops"], 4)
+    if "sustained" in out["gemm"]:
+        out["gemm_over_roof_sustained"] = round(out["gemm"]["sustained"]["tflops"] /
+                                                out["mfma_only"]["sustained"]["tflops"], 4)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -755,6 +918,12 @@ def main():
                     help="time the device operand preparation (quantize + layouts) instead")
     ap.add_argument("--power", type=float, default=0.0, metavar="SECONDS",
                     help="board power and clocks over SECONDS of back-to-back GEMMs instead")
+    ap.add_argument("--roof", type=float, default=None, nargs="?", const=5.0, metavar="SECONDS",
+                    help="the MFMA-only diagnostic kernel against the workload's GEMM instead "
+                         "(timed like the headline, then each sustained for SECONDS, default 5)")
+    ap.add_argument("--ab", default=None, metavar="PLANS",
+                    help="explicit plans of the workload against each other and the routed plan "
+                         "instead (MTxNTxMPWxNPW[:S[:r]],...; with --repeat R rounds)")
     ap.add_argument("--map", nargs="?", const="", default=None, metavar="SHAPES",
                     help="this library against the reference library shape by shape instead "
                          "(MxNxK,... or a file of them; 'second': 160 other shapes; "
@@ -776,6 +945,12 @@ def main():
         return
     if a.power > 0:
         print(json.dumps(run_power(a.config, a.power)), flush=True)
+        return
+    if a.ab is not None:
+        print(json.dumps(run_ab(a.config, a.ab, max(a.repeat, 1))), flush=True)
+        return
+    if a.roof is not None:
+        print(json.dumps(run_roof(a.config, a.steps, a.warmup, a.roof)), flush=True)
         return
     if a.map is not None:
         run_map(a.map, a.repeat)

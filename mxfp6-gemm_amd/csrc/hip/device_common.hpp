@@ -37,6 +37,11 @@ __device__ __forceinline__ v16f mfma_fp6(v16f acc, v8i a, v8i b, int sa, int sb)
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc, 2, 2, SA, sa, SB, sb);
 }
 
+// The lane's index in its wave (mbcnt over a full mask), computed afresh rather than kept live.
+__device__ __forceinline__ int lane_id() {
+    return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
 template <typename OutT>
 __device__ __forceinline__ OutT cvt_out(float v);
 template <>

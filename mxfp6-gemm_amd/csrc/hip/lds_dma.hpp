@@ -6,6 +6,8 @@
 // before every read) nor a pending vector load (its loop-merge waits would do the same); the
 // kernels keep the vector-memory count themselves (s_waitcnt vmcnt).
 #pragma once
+#include <utility>
+
 #include "device_common.hpp"
 
 namespace mxfp6_dev {
@@ -24,6 +26,19 @@ __device__ __forceinline__ void dma16(uint32_t lds, const void* gbase, uint32_t 
                  : "memory");
 }
 
+// dma16 into LDS lds + OFF: M0 is set from the scalar base plus the constant in one SALU
+// instruction (a kernel's ring position is a compile-time constant).
+template <int OFF>
+__device__ __forceinline__ void dma16_at(uint32_t lds, const void* gbase, uint32_t voff) {
+    if constexpr (OFF == 0)
+        dma16(lds, gbase, voff);
+    else
+        asm volatile("s_add_u32 m0, %0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                     :
+                     : "s"(lds), "v"(voff), "s"(gbase), "n"(OFF)
+                     : "memory");
+}
+
 // Same with a per-lane 64-bit global address.
 __device__ __forceinline__ void dma16_flat(uint32_t lds, const void* gaddr) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
@@ -38,6 +53,26 @@ __device__ __forceinline__ void dma4_flat(uint32_t lds, const void* gaddr) {
                  :
                  : "s"(lds), "v"(gaddr)
                  : "memory");
+}
+
+// f(std::integral_constant<int, I>) for I = 0 .. N-1, in order (a loop whose index is a
+// compile-time constant in its body).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Buffer resource of a raw (untyped, unstrided) buffer at `base` with no effective bound: buffer
+// loads through it take a VGPR offset, an SGPR offset and an immediate, with no 64-bit address
+// arithmetic per load.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t raw_rsrc(const __attribute__((address_space(1))) uint8_t* base) {
+    // dword 3: 32-bit data format (required for untyped loads on gfx9), no swizzle, no index
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
 }
 
 template <int N>

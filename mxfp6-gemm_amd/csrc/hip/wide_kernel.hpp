@@ -67,7 +67,10 @@ struct WideGeom {
     static constexpr int CHUNK = MT * SUBS * SLAB_BYTES;         // one K-tile of A
     static constexpr int COPIES = CHUNK / 1024;                  // wave copies of 1 KiB
     static constexpr int A_ISS = (COPIES + NWAVES - 1) / NWAVES; // copies per wave per chunk
-    static constexpr int LDS = NB * CHUNK + 1024;                // + dummy sink
+    // LDS buffer stride: room for every wave's A_ISS copies, so the copies that a chunk does
+    // not need (128-row tiles: 18 real of 20) land in the buffer's own unread tail
+    static constexpr int CST = A_ISS * NWAVES * 1024;
+    static constexpr int LDS = NB * CST;
     // copies of slab s, and the MFMA after which copy j of a slab is issued
     static constexpr int cps(int s) { return A_ISS / SUBS + (s < A_ISS % SUBS ? 1 : 0); }
     static constexpr int CSTEP = cps(0) <= 2 ? NMF / 4 : NMF / cps(0);
@@ -184,43 +187,55 @@ __global__ void __launch_bounds__(256, 1)
         }
     }
     const uint32_t lds0 = lds_u32(lds);
-    const uint32_t lds_dummy = __builtin_amdgcn_readfirstlane(lds0 + NB * CHUNK);
-    // copy i of chunk kt (absolute K-tile, clamped to the segment) into LDS buffer buf
-    auto a_copy = [&](int i, int kt, int buf) {
-        const int j = i * G::NWAVES + wave;
-        const uint32_t dst = j < G::COPIES ? lds0 + buf * CHUNK + j * 1024 : lds_dummy;
+    // LDS destination of copy i in buffer 0 (scalar); buffer b adds b * CST in the copy itself
+    uint32_t a_dst[G::A_ISS];
+#pragma unroll
+    for (int i = 0; i < G::A_ISS; i++)
+        a_dst[i] = __builtin_amdgcn_readfirstlane(lds0 + (i * G::NWAVES + wave) * 1024);
+    // copy i of chunk kt (absolute K-tile, clamped to the segment) into LDS buffer BUF
+    auto a_copy = [&](int i, int kt, auto bufc) {
+        constexpr int BUF = decltype(bufc)::value;
         const uint8_t* src = a_tile + (size_t)kt * (ASH ? SUBS * OPBLK_BYTES : SUBS * SLAB_BYTES);
-        dma16(__builtin_amdgcn_readfirstlane(dst), src, a_voff[i]);
+        dma16_at<BUF * G::CST>(a_dst[i], src, a_voff[i]);
     };
 
     // ---- B operand and scale loads of this wave
     const int b_blk_last = (N + 31) / 32 - 1;
     const int sa_grp_last = ((M + 31) / 32 + GA - 1) / GA - 1;
     const int sb_grp_last = ((N + 31) / 32 + NPW - 1) / NPW - 1;
-    gbl_cptr b_col[NPW];
+    // The B operand and scale loads are buffer loads: a resource per B block column and per scale
+    // group (base address in SGPRs), the lane's part as a constant VGPR offset, the K-tile as a
+    // scalar offset and the slab as the instruction's immediate, so a load needs no address
+    // arithmetic of its own. The bases are hidden from the optimizer (opaque_gptr): the loads then
+    // keep their order relative to the asm copies and are not merged across them.
+    rsrc_t b_rs[NPW];
 #pragma unroll
     for (int ni = 0; ni < NPW; ni++) {
         int blk = wg_n * (NT / 32) + wave * NPW + ni;
         if (MASK) blk = min(blk, b_blk_last);
-        b_col[ni] = opaque_gptr(Bsh + (size_t)blk * k64n * OPBLK_BYTES);
+        b_rs[ni] = raw_rsrc(opaque_gptr(Bsh + (size_t)blk * k64n * OPBLK_BYTES));
     }
-    // lane's scale dwords of K-tile 0 (the dword of slab s at + 4 s), per A group and for B
-    gbl_cptr sa_lane[NGA];
+    // the lane's scale dwords of a K-tile (the dword of slab s at + 4 s), per A group and for B
+    rsrc_t sa_rs[NGA];
 #pragma unroll
     for (int g = 0; g < NGA; g++) {
         int ga = wg_m * NGA + g;
         if (MASK) ga = min(ga, sa_grp_last);
-        sa_lane[g] = opaque_gptr(sA + (size_t)ga * k_tiles * 64 * 12) + lane * 12;
+        sa_rs[g] = raw_rsrc(opaque_gptr(sA + (size_t)ga * k_tiles * 64 * 12));
     }
     int gb = wg_n * G::NWAVES + wave;
     if (MASK) gb = min(gb, sb_grp_last);
-    const gbl_cptr sb_lane = opaque_gptr(sB + (size_t)gb * k_tiles * 64 * 12) + lane * 12;
+    const rsrc_t sb_rs = raw_rsrc(opaque_gptr(sB + (size_t)gb * k_tiles * 64 * 12));
+    const int v_b0 = (int)opaque_v(16 * lane), v_b1 = (int)opaque_v(1024 + 8 * lane);
+    const int v_sc = (int)opaque_v(12 * lane);
 
     // slab s of K-tile kt, block ni, into v
     auto load_b = [&](v8i& v, int ni, int kt, int s) {
-        const gbl_cptr p = b_col[ni] + (size_t)(kt * SUBS + s) * OPBLK_BYTES;
-        const v4i y0 = *reinterpret_cast<__attribute__((address_space(1))) const v4i*>(p + 16 * lane);
-        const v2i y1 = *reinterpret_cast<__attribute__((address_space(1))) const v2i*>(p + 1024 + 8 * lane);
+        const int so = kt * (SUBS * OPBLK_BYTES);
+        const v4i y0 = __builtin_bit_cast(
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(b_rs[ni], v_b0 + s * OPBLK_BYTES, so, 0));
+        const v2i y1 = __builtin_bit_cast(
+            v2i, __builtin_amdgcn_raw_buffer_load_b64(b_rs[ni], v_b1 + s * OPBLK_BYTES, so, 0));
         const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
         v = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
     };
@@ -228,24 +243,43 @@ __global__ void __launch_bounds__(256, 1)
     auto load_scales = [&](v3i (&a)[NGA], v3i& b, int kt) {
 #pragma unroll
         for (int g = 0; g < NGA; g++)
-            a[g] = *reinterpret_cast<__attribute__((address_space(1))) const v3i_a4*>(sa_lane[g] + (size_t)kt * 768);
-        b = *reinterpret_cast<__attribute__((address_space(1))) const v3i_a4*>(sb_lane + (size_t)kt * 768);
+            a[g] = __builtin_bit_cast(v3i, __builtin_amdgcn_raw_buffer_load_b96(sa_rs[g], v_sc, kt * 768, 0));
+        b = __builtin_bit_cast(v3i, __builtin_amdgcn_raw_buffer_load_b96(sb_rs, v_sc, kt * 768, 0));
     };
 
-    // ---- A operand reads (LDS): slab s of the chunk in buffer buf, block mi
+    // ---- A operand reads (LDS): slab s of the chunk in buffer BUF, block mi. The addresses are
+    // per-buffer (repacked A: two per buffer) or per-(buffer, block) (row-major A) base VGPRs
+    // computed once, plus the slab's offset as the instructions' immediate: no address arithmetic
+    // per read (a ds_read2_b64 reaches 2040 bytes past its base, a row-major block's three slabs
+    // 96 + 16).
     const lds_cptr lds3 = (lds_cptr)lds;
     const uint32_t a_rd = ASH ? (uint32_t)(lane * 16)
                               : (uint32_t)((lane & 31) * SUBS * SLAB_BYTES + (lane >> 5) * 24);
-    auto read_a = [&](v8i& dst, int buf, int s, int mi) {
-        if (ASH) {
-            const uint32_t o = opaque_v(buf * CHUNK + (mi * SUBS + s) * OPBLK_BYTES + a_rd);
-            const v4i y0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(lds3 + o);
+    // (the masked instantiations hold clamp values besides: one base per buffer for row-major A,
+    // and the block's offset added per read, so that they stay within the register file)
+    constexpr bool PER_BLOCK = !ASH && !MASK;
+    constexpr int NBASE = ASH ? 2 : PER_BLOCK ? MB : 1;
+    uint32_t a_base[NB][NBASE];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < NBASE; i++)
+            a_base[b][i] = ASH ? opaque_v(b * G::CST + (i == 0 ? a_rd : 1024u + 8u * lane))
+                               : opaque_v(b * G::CST + i * 32 * SUBS * SLAB_BYTES + a_rd);
+    auto read_a = [&](v8i& dst, auto bufc, int s, int mi) {
+        constexpr int BUF = decltype(bufc)::value;
+        if constexpr (ASH) {
+            const int o = (mi * SUBS + s) * OPBLK_BYTES;
+            const v4i y0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(
+                lds3 + a_base[BUF][0] + o);
             const v2i y1 = *reinterpret_cast<const __attribute__((address_space(3))) v2i*>(
-                lds3 + o + 1024 - 8 * lane);
+                lds3 + a_base[BUF][1] + o);
             const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
             dst = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
         } else {
-            const uint32_t o = opaque_v(buf * CHUNK + mi * 32 * SUBS * SLAB_BYTES + s * SLAB_BYTES + a_rd);
+            const uint32_t o = PER_BLOCK ? a_base[BUF][PER_BLOCK ? mi : 0] + s * SLAB_BYTES
+                                         : opaque_v(a_base[BUF][0] + mi * 32 * SUBS * SLAB_BYTES +
+                                                    s * SLAB_BYTES);
             const v6i_a8 x = *reinterpret_cast<const __attribute__((address_space(3))) v6i_a8*>(lds3 + o);
             dst = __builtin_shufflevector(x, x, 0, 1, 2, 3, 4, 5, -1, -1);
         }
@@ -257,10 +291,9 @@ __global__ void __launch_bounds__(256, 1)
 #pragma unroll
         for (int j = 0; j < NPW; j++) acc[i][j] = v16f{};
 
-    v8i RB[SUBS][NPW];     // B operands, slot s = slab s of a K-tile
-    v8i RA[NSET][MB];      // A operands
-    v3i sc_a[NGA], sc_b;   // scale dwords of the current K-tile
-    v3i sn_a[NGA], sn_b;   // and of the next one
+    v8i RB[SUBS][NPW];        // B operands, slot s = slab s of a K-tile
+    v8i RA[NSET][MB];         // A operands
+    v3i sc_a[2][NGA], sc_b[2];  // scale dwords of K-tiles of even and of odd index
 
     if constexpr (G::SHORT_MAX > 0 || ONE > 0) {
         // One K-tile, or on the 128 x 256 tile up to three (K <= 576, or a split segment that
@@ -273,10 +306,10 @@ __global__ void __launch_bounds__(256, 1)
             static_assert(G::short_wait(NK, 0) <= 63, "vmcnt range (short path)");
             v8i RBk[NK][SUBS][NPW];
             v3i ska[NK][NGA], skb[NK];
+            static_for<NK>([&](auto cc) {
+                constexpr int c = decltype(cc)::value;
 #pragma unroll
-            for (int c = 0; c < NK; c++) {
-#pragma unroll
-                for (int i = 0; i < G::A_ISS; i++) a_copy(i, kt0 + c, c);
+                for (int i = 0; i < G::A_ISS; i++) a_copy(i, kt0 + c, cc);
                 asm volatile("" ::: "memory");
                 __builtin_amdgcn_sched_barrier(0);
                 load_scales(ska[c], skb[c], kt0 + c);
@@ -290,11 +323,11 @@ __global__ void __launch_bounds__(256, 1)
                         asm volatile("" ::: "memory");
                         __builtin_amdgcn_sched_barrier(0);
                     }
-            }
+            });
             wait_vmcnt<G::short_wait(NK, 0)>();  // chunk 0 landed
             ring_barrier();
 #pragma unroll
-            for (int mi = 0; mi < MB; mi++) read_a(RA[0][mi], 0, 0, mi);
+            for (int mi = 0; mi < MB; mi++) read_a(RA[0][mi], std::integral_constant<int, 0>{}, 0, mi);
             // K-tile C from LDS buffer C; slab s uses A set s (three sets) or (3 C + s) % 2 (two)
             auto step = [&](auto cc) {
                 constexpr int C = decltype(cc)::value;
@@ -308,7 +341,6 @@ __global__ void __launch_bounds__(256, 1)
                     }
                     const int cur = NSET == 3 ? s : (3 * C + s) % 2;
                     const int nxt = NSET == 3 ? (s + 1) % 3 : (3 * C + s + 1) % 2;
-                    const int rbuf = s + 1 < SUBS ? C : C + 1;
                     const int rs = s + 1 < SUBS ? s + 1 : 0;
 #pragma unroll
                     for (int k = 0; k < NMF; k++) {
@@ -319,8 +351,13 @@ __global__ void __launch_bounds__(256, 1)
                         wide_mfma<MB, NPW>(acc, mi, ni, RA[cur][mi], RBk[C][s][ni], sa, sb);
 #pragma unroll
                         for (int i = 0; i < MB; i++)
-                            if (k == G::read_k(i) && (MORE || s + 1 < SUBS))
-                                read_a(RA[nxt][i], rbuf, rs, i);
+                            if (k == G::read_k(i) && (MORE || s + 1 < SUBS)) {
+                                // slab s + 1 of chunk C, or slab 0 of chunk C + 1
+                                if (s + 1 < SUBS)
+                                    read_a(RA[nxt][i], cc, rs, i);
+                                else if constexpr (MORE)
+                                    read_a(RA[nxt][i], std::integral_constant<int, C + 1>{}, rs, i);
+                            }
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
@@ -328,10 +365,11 @@ __global__ void __launch_bounds__(256, 1)
             step(std::integral_constant<int, 0>{});
             if constexpr (NK >= 2) step(std::integral_constant<int, 1>{});
             if constexpr (NK == 3) step(std::integral_constant<int, 2>{});
+            const int le = lane_id();  // recomputed: no lane value stays live across the K loop
             store_tile<MB, NPW, OutT, SPLIT, MASK, STREAM>(acc, D, ws, M, N,
-                                                        wg_m * MT + 4 * (lane >> 5),
-                                                        wg_n * NT + wave * NPW * 32 + (lane & 31),
-                                                        lane, wg_z);
+                                                        wg_m * MT + 4 * (le >> 5),
+                                                        wg_n * NT + wave * NPW * 32 + (le & 31),
+                                                        le, wg_z);
         };
         if constexpr (ONE > 0) {
             // the instantiation for segments of ONE K-tiles of the tiles without the path in their
@@ -360,9 +398,10 @@ __global__ void __launch_bounds__(256, 1)
     // which places the B waits, then sees at least the count of loads in flight on entry to the
     // loop that it sees around it; the empty asm statements keep it from merging or reordering the
     // loads). PRO_WAIT counts the same operations after chunk 0 in either order.
+    using I0 = std::integral_constant<int, 0>;
 #pragma unroll
-    for (int i = 0; i < G::A_ISS; i++) a_copy(i, kt0, 0);
-    load_scales(sc_a, sc_b, kt0);
+    for (int i = 0; i < G::A_ISS; i++) a_copy(i, kt0, I0{});
+    load_scales(sc_a[0], sc_b[0], kt0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -374,10 +413,12 @@ __global__ void __launch_bounds__(256, 1)
             __builtin_amdgcn_sched_barrier(0);
         }
         if (s == 0) {
+            static_for<NB - 2>([&](auto cc) {
+                constexpr int C = decltype(cc)::value + 1;
 #pragma unroll
-            for (int c = 1; c < NB - 1; c++)
-#pragma unroll
-                for (int i = 0; i < G::A_ISS; i++) a_copy(i, min(kt0 + c, kt_last), c);
+                for (int i = 0; i < G::A_ISS; i++)
+                    a_copy(i, min(kt0 + C, kt_last), std::integral_constant<int, C>{});
+            });
             asm volatile("" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -385,15 +426,18 @@ __global__ void __launch_bounds__(256, 1)
     wait_vmcnt<G::PRO_WAIT>();  // chunk 0 landed
     ring_barrier();
 #pragma unroll
-    for (int mi = 0; mi < MB; mi++) read_a(RA[0][mi], 0, 0, mi);
+    for (int mi = 0; mi < MB; mi++) read_a(RA[0][mi], I0{}, 0, mi);
 
-    int buf = 0;  // LDS buffer of K-tile c's chunk
-    // K-tile c; P: its parity in the two-set A rotation (slab s uses set (3 P + s) % 2), 0 with
-    // three sets (slab s uses set s)
-    auto ktile = [&](int c, auto par) {
-        constexpr int P = decltype(par)::value;
-        const int nbuf = buf + 1 == NB ? 0 : buf + 1;            // chunk c + 1
-        const int cbuf = buf == 0 ? NB - 1 : buf - 1;            // chunk c + NB - 1 (c - 1's)
+    // K-tile c = T (mod 6) of the pass: chunk in LDS buffer BUF = T % NB, scales in set Q = T % 2
+    // (the next K-tile's go to the other set), and with two A register sets slab s uses set
+    // (3 Q + s) % 2 (with three, set s). Everything that rotates is a compile-time constant.
+    auto ktile = [&](int c, auto tt) {
+        constexpr int T = decltype(tt)::value;
+        constexpr int BUF = T % NB, NBUF = (T + 1) % NB, CBUF = (T + NB - 1) % NB;
+        constexpr int Q = T % 2;
+        using BufC = std::integral_constant<int, BUF>;
+        using NBufC = std::integral_constant<int, NBUF>;
+        using CBufC = std::integral_constant<int, CBUF>;
         const int kt_copy = min(kt0 + c + NB - 1, kt_last);
         const int kt_next = min(kt0 + c + 1, kt_last);
 #pragma unroll
@@ -405,10 +449,8 @@ __global__ void __launch_bounds__(256, 1)
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 ring_barrier();
             }
-            const int cur = NSET == 3 ? s : (3 * P + s) % 2;           // set of slab s
-            const int nxt = NSET == 3 ? (s + 1) % 3 : (3 * P + s + 1) % 2;  // of the next slab
-            // slab s + 1 of this K-tile, or slab 0 of the next, goes to RA[nxt]
-            const int rbuf = s + 1 < SUBS ? buf : nbuf;
+            const int cur = NSET == 3 ? s : (3 * Q + s) % 2;           // set of slab s
+            const int nxt = NSET == 3 ? (s + 1) % 3 : (3 * Q + s + 1) % 2;  // of the next slab
             const int rs = s + 1 < SUBS ? s + 1 : 0;
             int ci = 0;  // copies of this slab so far
             const int c0 = s == 0 ? 0 : s == 1 ? G::cps(0) : G::cps(0) + G::cps(1);
@@ -416,42 +458,46 @@ __global__ void __launch_bounds__(256, 1)
             for (int k = 0; k < NMF; k++) {
                 const int ni = k / MB, mi = k % MB;
                 const int g = mi / GA;
-                const int sa = s == 0 ? sc_a[g].x : s == 1 ? sc_a[g].y : sc_a[g].z;
-                const int sb = s == 0 ? sc_b.x : s == 1 ? sc_b.y : sc_b.z;
+                const int sa = s == 0 ? sc_a[Q][g].x : s == 1 ? sc_a[Q][g].y : sc_a[Q][g].z;
+                const int sb = s == 0 ? sc_b[Q].x : s == 1 ? sc_b[Q].y : sc_b[Q].z;
                 wide_mfma<MB, NPW>(acc, mi, ni, RA[cur][mi], RB[s][ni], sa, sb);
-                if (s == 0 && k == 0) load_scales(sn_a, sn_b, kt_next);
+                if (s == 0 && k == 0) load_scales(sc_a[1 - Q], sc_b[1 - Q], kt_next);
                 if (ci < G::cps(s) && k == G::copy_k(ci)) {
-                    a_copy(c0 + ci, kt_copy, cbuf);
+                    a_copy(c0 + ci, kt_copy, CBufC{});
                     ci++;
                 }
                 if (G::b_load_at(k)) load_b(RB[s][ni], ni, kt_next, s);
+                // slab s + 1 of this K-tile, or slab 0 of the next, goes to RA[nxt]
 #pragma unroll
                 for (int i = 0; i < MB; i++)
-                    if (k == G::read_k(i)) read_a(RA[nxt][i], rbuf, rs, i);
+                    if (k == G::read_k(i)) {
+                        if (s + 1 < SUBS)
+                            read_a(RA[nxt][i], BufC{}, rs, i);
+                        else
+                            read_a(RA[nxt][i], NBufC{}, rs, i);
+                    }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-#pragma unroll
-        for (int g = 0; g < NGA; g++) sc_a[g] = sn_a[g];
-        sc_b = sn_b;
-        buf = nbuf;
     };
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
+    // passes of six K-tiles (the buffer rotates with period NB = 3, the sets with period 2); a
+    // K loop of any length leaves after the K-tile that completes it
     int c = 0;
-    if constexpr (NSET == 2) {
-        for (; c + 1 < nkt; c += 2) {
-            ktile(c, P0{});
-            ktile(c + 1, P1{});
-        }
+    bool done = false;
+    while (!done) {
+        static_for<6>([&](auto tt) {
+            if (done) return;
+            ktile(c, tt);
+            done = ++c == nkt;
+        });
     }
-    for (; c < nkt; c++) ktile(c, P0{});
 
     // epilogue (the clamped prefetches of the last K-tiles are drained first); STREAM: D written
     // with nontemporal stores
     wait_vmcnt0();
-    store_tile<MB, NPW, OutT, SPLIT, MASK, STREAM>(acc, D, ws, M, N, wg_m * MT + 4 * (lane >> 5),
-                                                wg_n * NT + wave * NPW * 32 + (lane & 31), lane,
+    const int le = lane_id();  // recomputed: no lane value stays live across the K loop
+    store_tile<MB, NPW, OutT, SPLIT, MASK, STREAM>(acc, D, ws, M, N, wg_m * MT + 4 * (le >> 5),
+                                                wg_n * NT + wave * NPW * 32 + (le & 31), le,
                                                 wg_z);
 }
 
