@@ -14,7 +14,7 @@ drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX 
                                workload, this library then the reference library; amd-smi)
   python bench.py --roof [S]  (the MFMA-only diagnostic kernel against the workload's GEMM: the
                                cycles per MFMA and the board's power roof, each sustained S s)
-  python bench.py --ab PLANS [--config cN] [--repeat R]  (explicit plans MTxNTxMPWxNPW[:S[:r]]
+  python bench.py --ab PLANS [--config cN] [--repeat R]  (explicit plans MTxNTxMPWxNPW[:S[:r|p]]
                                of a workload against each other and the routed plan, R rounds,
                                order rotated)
   python bench.py --map [SHAPES|second] [--repeat R]  (this library against the reference library,
@@ -745,7 +745,9 @@ def run_ab(name, plans, repeat):
     """Explicit plans of one workload against each other (and the routed plan), on the same
     operands, each timed by the reference's method (compare()'s best_of), `repeat` rounds with
     the order rotating every round; prints one JSON line with every plan's series and median.
-    plans: "MTxNTxMPWxNPW[:S[:r]]" separated by commas (S K segments, r for a repacked A)."""
+    plans: "MTxNTxMPWxNPW[:S[:r|p]]" separated by commas (S K segments; r: A repacked by the plan,
+    the repack timed with it; p: A repacked once beforehand, the tile kernel alone on the
+    preshuffled copy)."""
     import torch
     w = Workload(name)
     M, N, Kp, p = w.M, w.N, w.p.Kp, w.p
@@ -753,22 +755,33 @@ def run_ab(name, plans, repeat):
     dev = torch.device("cuda:0")
     entries = [("routed", lambda: w.ours(stream))]
     keep = []
+    ash = None
     for spec in plans.split(","):
         parts = spec.strip().split(":")
         tile = tuple(int(v) for v in parts[0].split("x"))
         S = int(parts[1]) if len(parts) > 1 else 1
-        rp = len(parts) > 2 and parts[2] == "r"
+        lay = {"r": mx.A_REPACK, "p": mx.A_PRESHUFFLED}.get(parts[2] if len(parts) > 2 else "",
+                                                           mx.A_ROWS)
+        a_ptr = w.dA.data_ptr()
+        if lay == mx.A_PRESHUFFLED:
+            # A repacked once here, outside the timing: the tile kernel alone on preshuffled A
+            if ash is None:
+                ash = torch.empty(mx.preshuffled_bytes(M, Kp), dtype=torch.uint8, device=dev)
+                if mx.preshuffle_rows(w.dA.data_ptr(), p.a_row_bytes, M, Kp, ash.data_ptr(),
+                                      stream.cuda_stream):
+                    raise RuntimeError("repack failed")
+            a_ptr = ash.data_ptr()
         _, sa, sb = p.layouts(tile)
         dsa, dsb = torch.from_numpy(sa).to(dev), torch.from_numpy(sb).to(dev)
-        wsb = mx.plan_workspace_size(M, N, Kp, S, rp)
+        wsb = mx.plan_workspace_size(M, N, Kp, S, lay == mx.A_REPACK)
         ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=dev)
         keep.append((dsa, dsb, ws))
 
-        def fn(tile=tile, S=S, rp=rp, dsa=dsa, dsb=dsb, ws=ws, wsb=wsb):
-            rc = mx.gemm_explicit(w.ot, M, N, Kp, tile, S, w.dA.data_ptr(), w.dB.data_ptr(),
+        def fn(tile=tile, S=S, lay=lay, a_ptr=a_ptr, dsa=dsa, dsb=dsb, ws=ws, wsb=wsb):
+            rc = mx.gemm_explicit(w.ot, M, N, Kp, tile, S, a_ptr, w.dB.data_ptr(),
                                   dsa.data_ptr(), dsb.data_ptr(), w.D.data_ptr(), p.a_row_bytes,
                                   ws.data_ptr() if wsb else 0, wsb, stream=stream.cuda_stream,
-                                  a_layout=mx.A_REPACK if rp else mx.A_ROWS)
+                                  a_layout=lay)
             if rc != 0:
                 raise RuntimeError(f"plan {tile} S {S}: {mx.STATUS.get(rc, rc)}")
         entries.append((spec.strip(), fn))
@@ -923,7 +936,8 @@ def main():
                          "(timed like the headline, then each sustained for SECONDS, default 5)")
     ap.add_argument("--ab", default=None, metavar="PLANS",
                     help="explicit plans of the workload against each other and the routed plan "
-                         "instead (MTxNTxMPWxNPW[:S[:r]],...; with --repeat R rounds)")
+                         "instead (MTxNTxMPWxNPW[:S[:r|p]],...; r: repacked A, p: A preshuffled "
+                         "beforehand; with --repeat R rounds)")
     ap.add_argument("--map", nargs="?", const="", default=None, metavar="SHAPES",
                     help="this library against the reference library shape by shape instead "
                          "(MxNxK,... or a file of them; 'second': 160 other shapes; "
