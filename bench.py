@@ -14,7 +14,7 @@ drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX 
                                workload, this library then the reference library; amd-smi)
   python bench.py --roof [S]  (the MFMA-only diagnostic kernel against the workload's GEMM: the
                                cycles per MFMA and the board's power roof, each sustained S s)
-  python bench.py --ab PLANS [--config cN] [--repeat R]  (explicit plans MTxNTxMPWxNPW[:S[:r|p]]
+  python bench.py --ab PLANS [--config cN] [--repeat R]  (explicit plans MTxNTxMPWxNPW[:S[:r|p|s]]
                                of a workload against each other and the routed plan, R rounds,
                                order rotated)
   python bench.py --map [SHAPES|second] [--repeat R]  (this library against the reference library,
@@ -745,9 +745,9 @@ def run_ab(name, plans, repeat):
     """Explicit plans of one workload against each other (and the routed plan), on the same
     operands, each timed by the reference's method (compare()'s best_of), `repeat` rounds with
     the order rotating every round; prints one JSON line with every plan's series and median.
-    plans: "MTxNTxMPWxNPW[:S[:r|p]]" separated by commas (S K segments; r: A repacked by the plan,
-    the repack timed with it; p: A repacked once beforehand, the tile kernel alone on the
-    preshuffled copy)."""
+    plans: "MTxNTxMPWxNPW[:S[:r|p|s]]" separated by commas (S K segments; r: A repacked by the
+    plan, the repack timed with it; p: A repacked once beforehand, the tile kernel alone on the
+    preshuffled copy; s: row-major A staged in LDS in 12-byte units, swizzled, wide tiles)."""
     import torch
     w = Workload(name)
     M, N, Kp, p = w.M, w.N, w.p.Kp, w.p
@@ -760,8 +760,8 @@ def run_ab(name, plans, repeat):
         parts = spec.strip().split(":")
         tile = tuple(int(v) for v in parts[0].split("x"))
         S = int(parts[1]) if len(parts) > 1 else 1
-        lay = {"r": mx.A_REPACK, "p": mx.A_PRESHUFFLED}.get(parts[2] if len(parts) > 2 else "",
-                                                           mx.A_ROWS)
+        lay = {"r": mx.A_REPACK, "p": mx.A_PRESHUFFLED, "s": mx.A_ROWS_SWIZZLED}.get(
+            parts[2] if len(parts) > 2 else "", mx.A_ROWS)
         a_ptr = w.dA.data_ptr()
         if lay == mx.A_PRESHUFFLED:
             # A repacked once here, outside the timing: the tile kernel alone on preshuffled A
@@ -936,8 +936,9 @@ def main():
                          "(timed like the headline, then each sustained for SECONDS, default 5)")
     ap.add_argument("--ab", default=None, metavar="PLANS",
                     help="explicit plans of the workload against each other and the routed plan "
-                         "instead (MTxNTxMPWxNPW[:S[:r|p]],...; r: repacked A, p: A preshuffled "
-                         "beforehand; with --repeat R rounds)")
+                         "instead (MTxNTxMPWxNPW[:S[:r|p|s]],...; r: repacked A, p: A "
+                         "preshuffled beforehand, s: row-major A staged swizzled; with --repeat R "
+                         "rounds)")
     ap.add_argument("--map", nargs="?", const="", default=None, metavar="SHAPES",
                     help="this library against the reference library shape by shape instead "
                          "(MxNxK,... or a file of them; 'second': 160 other shapes; "

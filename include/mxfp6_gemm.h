@@ -115,7 +115,10 @@ int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4],
 /* Run an explicit plan: the pipelined kernel with tile {MT, NT, MPW, NPW} (masked when it does
  * not divide M x N), `splits` K segments and an A layout: 0 = row-major A (A_row_bytes per row); 1 = repack row-major A into the workspace in
  * the preshuffled operand layout first, then read that; 2 = dA already holds A in the preshuffled
- * layout (mxfp6_preshuffle_rows_async output; A_row_bytes is then only checked). Needs ws of
+ * layout (mxfp6_preshuffle_rows_async output; A_row_bytes is then only checked); 3 = row-major A
+ * as 0, staged in LDS in 12-byte units whose slots are swizzled per row (operand reads free of
+ * bank conflicts; the four wide tiles only, dividing M x N, else MXFP6_ERR_ARG; same output bits
+ * as 0; never routed: measured no faster). Needs ws of
  * mxfp6_plan_workspace_size(M, N, Kp, splits, a_layout == 1) bytes. For tuning, benchmarks and
  * callers that keep A preshuffled; the scales must be tiled with this tile's MPW/NPW. No
  * counterpart in the reference (it is the reference's gemm_force_tile, src/gemm.cpp:89-107, plus a

@@ -39,6 +39,22 @@ __device__ __forceinline__ void dma16_at(uint32_t lds, const void* gbase, uint32
                      : "memory");
 }
 
+// 12 bytes per lane global -> LDS: lane l's bytes go to LDS m0 + OFF + 16*l (the instruction keeps a
+// 16-byte LDS stride per lane; the last 4 bytes of each slot are not written).
+template <int OFF>
+__device__ __forceinline__ void dma12_at(uint32_t lds, const void* gbase, uint32_t voff) {
+    if constexpr (OFF == 0)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx3 %1, %2"
+                     :
+                     : "s"(lds), "v"(voff), "s"(gbase)
+                     : "memory");
+    else
+        asm volatile("s_add_u32 m0, %0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx3 %1, %2"
+                     :
+                     : "s"(lds), "v"(voff), "s"(gbase), "n"(OFF)
+                     : "memory");
+}
+
 // Same with a per-lane 64-bit global address.
 __device__ __forceinline__ void dma16_flat(uint32_t lds, const void* gaddr) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"

@@ -361,6 +361,7 @@ hipError_t slab_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipS
 template <int MT, int NT, int WM, int WN, int XG, int NS, typename KT, bool SPLIT>
 int slab_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     static_assert(SlabGeom<MT, NT, WM, WN, NS>::LDS <= 160 * 1024, "LDS budget");
+    if (d->a_layout == MXFP6_A_ROWS_SWIZZLED) return 2;  // a staging of the wide tiles only
     const bool mask = d->M % MT != 0 || d->N % NT != 0;
     const uint8_t* A = static_cast<const uint8_t*>(d->A);
     if (d->a_layout == MXFP6_A_REPACK) {
@@ -404,8 +405,11 @@ hipError_t wide_launch_st(const mxfp6_launch_desc* d, const uint8_t* A, hipStrea
 template <int MB, int NPW, int XG, typename KT, bool SPLIT>
 int wide_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
     using G = WideGeom<MB, NPW, WIDE_NB>;
-    static_assert(G::LDS <= 160 * 1024, "LDS budget");
+    static_assert(G::LDS <= 160 * 1024 && WideGeom<MB, NPW, WIDE_NB, true>::LDS <= 160 * 1024,
+                  "LDS budget");
     const bool mask = d->M % G::MT != 0 || d->N % G::NT != 0;
+    // the swizzled staging of row-major A: unmasked tiles, plain stores
+    if (d->a_layout == MXFP6_A_ROWS_SWIZZLED && (mask || d->out_stream)) return 2;
     const uint8_t* A = static_cast<const uint8_t*>(d->A);
     if (d->a_layout == MXFP6_A_REPACK) {
         if (repack_rows_launch(A, d->A_row_bytes, d->M, d->Kp / 64, static_cast<uint8_t*>(d->Ash),
@@ -414,7 +418,7 @@ int wide_launch_t(const mxfp6_launch_desc* d, hipStream_t st) {
         A = static_cast<const uint8_t*>(d->Ash);
     }
     hipError_t e;
-    if (d->a_layout == MXFP6_A_ROWS)
+    if (d->a_layout == MXFP6_A_ROWS || d->a_layout == MXFP6_A_ROWS_SWIZZLED)
         e = mask ? wide_launch_st<MB, NPW, XG, KT, SPLIT, false, true>(d, A, st)
                  : wide_launch_st<MB, NPW, XG, KT, SPLIT, false, false>(d, A, st);
     else

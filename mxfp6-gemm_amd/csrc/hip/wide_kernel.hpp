@@ -41,6 +41,12 @@
 // main kernel the masked and repacked-A instantiations would spill, and so would a masked ONE).
 // MASK (ragged M or N) clamps the copy and load sources
 // of the last tile row and column and masks the stores, as in the slab kernel.
+// SWZ (explicit plans only, never routed; row-major A, unmasked) stages a chunk row as twelve
+// 12-byte units in 16-byte LDS slots (global_load_lds_dwordx3), the slots of row r permuted by
+// XOR with (r / 4) % 4: a lane's 24-byte operand is then two 16-byte-aligned ds_read_b128 (four
+// bytes of each unused), and the 16 lanes one LDS cycle serves read 16 distinct slot positions,
+// so the operand reads are free of bank conflicts, for a third more copy instructions and a third
+// more LDS per chunk (48 instead of 36 KiB at 256 rows).
 #pragma once
 
 #include <type_traits>
@@ -56,16 +62,18 @@ namespace mxfp6_dev {
 // MFMA k; (s = 0, k = 0) the scale loads of the next K-tile; the slab's next A copy when k is a
 // copy position; the two loads of B block k / MB when MFMA k was its last use in the slab
 // (k % MB == MB - 1); the LDS read of an A block of the next slab when k is a read position.
-template <int MB_, int NPW_, int NB_>
+template <int MB_, int NPW_, int NB_, bool SWZ_ = false>
 struct WideGeom {
     static constexpr int MB = MB_, NPW = NPW_, NB = NB_;
+    static constexpr bool SWZ = SWZ_;                            // 12-byte units, swizzled rows
     static constexpr int MT = 32 * MB, NT = 4 * 32 * NPW, NWAVES = 4, THREADS = 256;
     static constexpr int GA = MB < 4 ? MB : 4;                   // A scale group (blocks)
     static constexpr int NGA = MB / GA;                          // A scale groups per tile
     static constexpr int NMF = MB * NPW;                         // MFMAs per wave per slab
     static constexpr int NSET = MB <= 4 ? 3 : 2;                 // A operand register sets
     static constexpr int CHUNK = MT * SUBS * SLAB_BYTES;         // one K-tile of A
-    static constexpr int COPIES = CHUNK / 1024;                  // wave copies of 1 KiB
+    // wave copies per chunk: of 1 KiB, or (SWZ) of 64 12-byte units, 12 per row
+    static constexpr int COPIES = SWZ ? MT * 12 / 64 : CHUNK / 1024;
     static constexpr int A_ISS = (COPIES + NWAVES - 1) / NWAVES; // copies per wave per chunk
     // LDS buffer stride: room for every wave's A_ISS copies, so the copies that a chunk does
     // not need (128-row tiles: 18 real of 20) land in the buffer's own unread tail
@@ -134,13 +142,14 @@ __device__ __forceinline__ void wide_mfma(v16f (&acc)[MB][NPW], int mi, int ni, 
 }
 
 template <int MB_, int NPW_, int NB_, int XG, typename OutT, bool SPLIT, bool ASH, bool MASK,
-          bool STREAM, int ONE = 0>
+          bool STREAM, int ONE = 0, bool SWZ = false>
 __global__ void __launch_bounds__(256, 1)
     wide_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
                 OutT* __restrict__ D, float* __restrict__ ws, int M, int N, int Kp,
                 int A_row_bytes, int S) {
-    using G = WideGeom<MB_, NPW_, NB_>;
+    using G = WideGeom<MB_, NPW_, NB_, SWZ>;
+    static_assert(!SWZ || (!ASH && !MASK && ONE == 0), "SWZ: row-major A, unmasked tiles");
     constexpr int MT = G::MT, NT = G::NT, MB = G::MB, NPW = G::NPW, NB = G::NB;
     constexpr int NGA = G::NGA, GA = G::GA, NSET = G::NSET, NMF = G::NMF;
     constexpr int CHUNK = G::CHUNK;
@@ -179,6 +188,12 @@ __global__ void __launch_bounds__(256, 1)
             const int rest = x - blk * (SUBS * OPBLK_BYTES);
             if (MASK) blk = min(blk, a_blk_last);
             a_voff[i] = (uint32_t)(blk * k64n * OPBLK_BYTES + rest);
+        } else if (SWZ) {
+            // LDS slot p = 64 j + l of the chunk holds unit u = v ^ ((r / 4) % 4) of row r = p / 12,
+            // v = p % 12 (bytes 12 u of the row's K-tile)
+            const int p = j * 64 + lane, row = p / 12;
+            const int u = (p - row * 12) ^ ((row >> 2) & 3);
+            a_voff[i] = (uint32_t)(row * A_row_bytes + 12 * u);
         } else {
             int row = x / (SUBS * SLAB_BYTES);
             const int col = x - row * (SUBS * SLAB_BYTES);
@@ -196,7 +211,10 @@ __global__ void __launch_bounds__(256, 1)
     auto a_copy = [&](int i, int kt, auto bufc) {
         constexpr int BUF = decltype(bufc)::value;
         const uint8_t* src = a_tile + (size_t)kt * (ASH ? SUBS * OPBLK_BYTES : SUBS * SLAB_BYTES);
-        dma16_at<BUF * G::CST>(a_dst[i], src, a_voff[i]);
+        if constexpr (SWZ)
+            dma12_at<BUF * G::CST>(a_dst[i], src, a_voff[i]);
+        else
+            dma16_at<BUF * G::CST>(a_dst[i], src, a_voff[i]);
     };
 
     // ---- B operand and scale loads of this wave
@@ -257,15 +275,20 @@ __global__ void __launch_bounds__(256, 1)
                               : (uint32_t)((lane & 31) * SUBS * SLAB_BYTES + (lane >> 5) * 24);
     // (the masked instantiations hold clamp values besides: one base per buffer for row-major A,
     // and the block's offset added per read, so that they stay within the register file)
-    constexpr bool PER_BLOCK = !ASH && !MASK;
-    constexpr int NBASE = ASH ? 2 : PER_BLOCK ? MB : 1;
+    // (SWZ: lane t reads units 4 s + 2 h and 4 s + 2 h + 1 of row t % 32 of the block, h = t / 32,
+    // in slots 4 s + ((2 h + e) ^ q) of the row, e = 0, 1, q = ((t % 32) / 4) % 4: two bases per
+    // buffer, the block's and slab's offsets as the reads' immediates)
+    constexpr bool PER_BLOCK = !ASH && !MASK && !SWZ;
+    constexpr int NBASE = ASH || SWZ ? 2 : PER_BLOCK ? MB : 1;
+    const uint32_t q4 = ((lane & 31) >> 2) & 3, h2 = (lane >> 5) * 2;
     uint32_t a_base[NB][NBASE];
 #pragma unroll
     for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int i = 0; i < NBASE; i++)
-            a_base[b][i] = ASH ? opaque_v(b * G::CST + (i == 0 ? a_rd : 1024u + 8u * lane))
-                               : opaque_v(b * G::CST + i * 32 * SUBS * SLAB_BYTES + a_rd);
+            a_base[b][i] = ASH   ? opaque_v(b * G::CST + (i == 0 ? a_rd : 1024u + 8u * lane))
+                           : SWZ ? opaque_v(b * G::CST + 192u * (lane & 31) + 16u * ((h2 + i) ^ q4))
+                                 : opaque_v(b * G::CST + i * 32 * SUBS * SLAB_BYTES + a_rd);
     auto read_a = [&](v8i& dst, auto bufc, int s, int mi) {
         constexpr int BUF = decltype(bufc)::value;
         if constexpr (ASH) {
@@ -276,6 +299,13 @@ __global__ void __launch_bounds__(256, 1)
                 lds3 + a_base[BUF][1] + o);
             const v4i y1w = __builtin_shufflevector(y1, y1, 0, 1, -1, -1);
             dst = __builtin_shufflevector(y0, y1w, 0, 1, 2, 3, 4, 5, -1, -1);
+        } else if constexpr (SWZ) {
+            const int o = mi * 32 * 192 + s * 64;
+            const v4i x0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(
+                lds3 + a_base[BUF][0] + o);
+            const v4i x1 = *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(
+                lds3 + a_base[BUF][1] + o);
+            dst = __builtin_shufflevector(x0, x1, 0, 1, 2, 4, 5, 6, -1, -1);
         } else {
             const uint32_t o = PER_BLOCK ? a_base[BUF][PER_BLOCK ? mi : 0] + s * SLAB_BYTES
                                          : opaque_v(a_base[BUF][0] + mi * 32 * SUBS * SLAB_BYTES +
@@ -508,6 +538,15 @@ hipError_t wide_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipS
     using G = WideGeom<MB, NPW, NB>;
     const dim3 grid((unsigned)((d->M + G::MT - 1) / G::MT), (unsigned)((d->N + G::NT - 1) / G::NT),
                     (unsigned)d->splits);
+    if constexpr (!ASH && !MASK && !STREAM) {
+        // row-major A staged swizzled (explicit plans): the main kernel for every segment length
+        if (d->a_layout == MXFP6_A_ROWS_SWIZZLED)
+            return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, false, false, false, 0, true>,
+                                 grid, dim3(G::THREADS), st, A,
+                                 static_cast<const uint8_t*>(d->Bsh), d->sA, d->sB,
+                                 SPLIT ? nullptr : static_cast<KT*>(d->D), SPLIT ? d->ws : nullptr,
+                                 d->M, d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1);
+    }
     if constexpr (G::SHORT_MAX == 0 && !MASK) {
         // every K segment one or two K-tiles: the short-path instantiations (not for masked
         // tiles, whose instantiations of it would spill)

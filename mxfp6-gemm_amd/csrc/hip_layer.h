@@ -12,7 +12,12 @@ extern "C" {
 #endif
 
 /* How the tile kernel finds A. */
-enum mxfp6_a_layout { MXFP6_A_ROWS = 0, MXFP6_A_REPACK = 1, MXFP6_A_PRESHUFFLED = 2 };
+enum mxfp6_a_layout {
+    MXFP6_A_ROWS = 0,
+    MXFP6_A_REPACK = 1,
+    MXFP6_A_PRESHUFFLED = 2,
+    MXFP6_A_ROWS_SWIZZLED = 3
+};
 
 /* Kernel families of the HIP layer. */
 enum mxfp6_kernel_id {
@@ -36,7 +41,9 @@ typedef struct mxfp6_launch_desc {
     float* ws;         /* splits * M * N floats when splits > 1 */
     int a_layout;      /* MXFP6_A_ROWS: A row-major (A_row_bytes per row);
                           MXFP6_A_REPACK: repack A into Ash first, the kernel reads Ash;
-                          MXFP6_A_PRESHUFFLED: A is already in the preshuffled operand layout */
+                          MXFP6_A_PRESHUFFLED: A is already in the preshuffled operand layout;
+                          MXFP6_A_ROWS_SWIZZLED: row-major A, staged in LDS in 12-byte units
+                          (wide tiles that divide M x N, plain stores; explicit plans only) */
     void* Ash;         /* MXFP6_A_REPACK: M * packed(Kp) bytes */
     int out_stream;    /* 1: the wide tile kernel writes D with nontemporal stores (unsplit plans
                           whose D would evict the operands from the last-level cache) */

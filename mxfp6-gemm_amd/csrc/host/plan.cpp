@@ -386,7 +386,7 @@ int run(int out_type, int M, int N, int Kp, const TileChoice& tc, int S, int a_l
     d.Ash = a_layout == MXFP6_A_REPACK
                 ? static_cast<uint8_t*>(ws) + (split_bytes(M, N, S) + 255) / 256 * 256
                 : nullptr;
-    d.out_stream = kernel == MXFP6_KERNEL_TILE &&
+    d.out_stream = kernel == MXFP6_KERNEL_TILE && a_layout != MXFP6_A_ROWS_SWIZZLED &&
                            streams_output(out_type, M, N, Kp, tc, S, a_layout == MXFP6_A_REPACK,
                                           A_row_bytes)
                        ? 1
@@ -744,7 +744,10 @@ extern "C" int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int
     const TileChoice tc = {tile[0], tile[1], tile[2], tile[3]};
     if (!mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW)) return MXFP6_ERR_TILE;
     if (splits < 1 || splits > Kp / K_TILE || a_layout < MXFP6_A_ROWS ||
-        a_layout > MXFP6_A_PRESHUFFLED)
+        a_layout > MXFP6_A_ROWS_SWIZZLED)
+        return MXFP6_ERR_ARG;
+    // the swizzled staging of row-major A exists for the wide tiles, unmasked
+    if (a_layout == MXFP6_A_ROWS_SWIZZLED && (!plan::is_wide(tc) || !plan::tile_divides(tile, M, N)))
         return MXFP6_ERR_ARG;
     const bool repack = a_layout == MXFP6_A_REPACK;
     if ((splits > 1 || repack) &&

@@ -196,7 +196,9 @@ def gemm_force_tile(out_type, M, N, Kp, tile, dA, dBsh, dsA, dsB, dD, A_row_byte
                                        A_row_bytes, 0, stream)
 
 
-A_ROWS, A_REPACK, A_PRESHUFFLED = 0, 1, 2
+# A layouts of an explicit plan (mxfp6_gemm_explicit): row-major, repacked by the plan, already
+# preshuffled, row-major staged in LDS in 12-byte units (wide tiles dividing M x N only)
+A_ROWS, A_REPACK, A_PRESHUFFLED, A_ROWS_SWIZZLED = 0, 1, 2, 3
 
 
 def gemm_explicit(out_type, M, N, Kp, tile, splits, dA, dBsh, dsA, dsB, dD, A_row_bytes, ws=0,

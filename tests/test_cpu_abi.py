@@ -63,6 +63,16 @@ def test_argument_checks_reject_before_launch(mx):
     assert mx.gemm_force_tile(0, 100, 128, 192, (128, 128, 2, 2), p, p, p, p, p, 144) == 4  # ragged
     assert mx.gemm_explicit(0, 100, 100, 192, (256, 128, 4, 2), 1, p, p, p, p, p, 144) == 4
     assert mx.gemm_explicit(0, 100, 100, 192, (128, 128, 2, 2), 2, p, p, p, p, p, 144) == 5  # no ws
+    # the swizzled staging of row-major A: wide tiles that divide M x N only, and no layout past it
+    sw = mx.A_ROWS_SWIZZLED
+    assert mx.gemm_explicit(0, 256, 256, 192, (128, 128, 2, 2), 1, p, p, p, p, p, 144,
+                            a_layout=sw) == 5                                        # slab tile
+    assert mx.gemm_explicit(0, 256, 384, 192, (256, 256, 4, 2), 1, p, p, p, p, p, 144,
+                            a_layout=sw) == 5                                        # masked N
+    assert mx.gemm_explicit(0, 200, 512, 192, (128, 512, 4, 4), 1, p, p, p, p, p, 144,
+                            a_layout=sw) == 5                                        # masked M
+    assert mx.gemm_explicit(0, 256, 256, 192, (256, 256, 4, 2), 1, p, p, p, p, p, 144,
+                            a_layout=sw + 1) == 5                                    # no layout 4
     assert mx.gemm_direct(0, 128, 128, 192, 5, 2, p, p, p, p, p, 144) == 5
     assert mx.gemm_direct(0, 128, 128, 192, 2, 2, p, p, p, p, p, 144, splits=2) == 5
     assert mx.gemm_direct(0, 96, 128, 192, 1, 1, p, p, p, p, p, 144) == 2   # M % 64

@@ -1,9 +1,9 @@
 """The wide tiles (four waves side by side, B streamed straight into registers, A staged in LDS one
-K-tile per row): 128 x 512, 128 x 256 and 256 x 256 (scale groups of 4 A blocks and 2 B blocks).
-Each is bit for bit equal to the direct kernel (same MFMAs, same K order) with row-major and
-repacked A, unsplit and split on both XCD maps; equal to the 256x256 slab kernel on ragged
-(masked) shapes (the same MFMA sequence per output block, whatever the scale grouping of the
-layouts); all output types against the FP64 oracle."""
+K-tile per row): 128 x 512, 128 x 384, 128 x 256 and 256 x 256. Each is bit for bit equal to the
+direct kernel (same MFMAs, same K order) with row-major A (staged as copied, and staged in
+swizzled 12-byte units: explicit layout 3) and repacked A, unsplit and split on both XCD maps;
+equal to the 256x256 slab kernel on ragged (masked) shapes (the same MFMA sequence per output
+block, whatever the scale grouping of the layouts); all output types against the FP64 oracle."""
 import numpy as np
 import pytest
 
@@ -19,7 +19,7 @@ WIDE_TILES = [(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4
 @pytest.mark.parametrize("WIDE", WIDE_TILES)
 @pytest.mark.parametrize("tm,tn,K", [(2, 2, 2112), (1, 1, 192), (1, 4, 4224), (3, 3, 3456),
                                      (2, 1, 384), (1, 2, 576)])
-@pytest.mark.parametrize("a_layout", [0, 1])
+@pytest.mark.parametrize("a_layout", [0, 1, 3])
 def test_wide_bitwise_equals_direct(WIDE, tm, tn, K, a_layout):
     """tm x tn tiles (M, N multiples of 256 and of the tile); the K-tile counts 11, 1, 22, 18, 2
     and 3: the 256 x 256 tile's K loop runs K-tiles in pairs, so odd counts take its
@@ -42,7 +42,7 @@ def test_wide_split_bitwise_equals_direct_split(WIDE, M, tn, S):
     K = 4224  # 22 K-tiles: uneven segments
     p = mx.make_problem(M, N, K, seed=S * 7 + M)
     dp = g.DevProblem(p, WIDE)
-    for a_layout in (0, 1):
+    for a_layout in (0, 1, 3):
         Dw = g.run_explicit(dp, mx.OUT_F32, splits=S, a_layout=a_layout)
         Dd = g.run_direct(dp, mx.OUT_F32, splits=S)
         assert np.array_equal(Dw.view(np.uint32), Dd.view(np.uint32)), a_layout
@@ -52,11 +52,12 @@ def test_wide_split_bitwise_equals_direct_split(WIDE, M, tn, S):
 @pytest.mark.parametrize("S,K", [(1, 192), (3, 576), (6, 1152), (1, 384), (3, 1152)])
 def test_wide_single_k_tile_segments(WIDE, S, K):
     """Every K segment one or two K-tiles (the short path, or for 128 x 512 and 256 x 256 their
-    short-path instantiations): bit for bit the direct kernel, rows and repacked A."""
+    short-path instantiations; the swizzled staging has no short path of its own and runs its main
+    loop): bit for bit the direct kernel, rows (both stagings) and repacked A."""
     M, N = 512, WIDE[1] * 2
     p = mx.make_problem(M, N, K, seed=S * 11 + K)
     dp = g.DevProblem(p, WIDE)
-    for a_layout in (0, 1):
+    for a_layout in (0, 1, 3):
         Dw = g.run_explicit(dp, mx.OUT_F32, splits=S, a_layout=a_layout)
         Dd = g.run_direct(dp, mx.OUT_F32, splits=S)
         assert np.array_equal(Dw.view(np.uint32), Dd.view(np.uint32)), a_layout
@@ -67,13 +68,14 @@ def test_wide_single_k_tile_segments(WIDE, S, K):
 def test_wide_short_path_lowp_outputs(WIDE, K):
     """Unsplit K of one to three K-tiles (the short path, or the short-path instantiations of
     128 x 512 and 256 x 256) with 16-bit outputs: FP32 equals the direct kernel bit for bit, and
-    FP16 / BF16 equal that FP32 rounded to nearest-even on the host, rows and repacked A."""
+    FP16 / BF16 equal that FP32 rounded to nearest-even on the host, rows (both stagings) and
+    repacked A."""
     M, N = 512, WIDE[1] * 2
     p = mx.make_problem(M, N, K, dist_a=mx.DIST_STUDENT_T3, dist_b=mx.DIST_STUDENT_T3,
                         seed=K * 5 + WIDE[1])
     dp = g.DevProblem(p, WIDE)
     Dd = g.run_direct(dp, mx.OUT_F32)
-    for a_layout in (0, 1):
+    for a_layout in (0, 1, 3):
         D32 = g.run_explicit(dp, mx.OUT_F32, a_layout=a_layout)
         assert np.array_equal(D32.view(np.uint32), Dd.view(np.uint32)), a_layout
         D16 = g.run_explicit(dp, mx.OUT_F16, a_layout=a_layout)
