@@ -82,6 +82,21 @@ def check(D, R, absdot, out_type):
 HALF_ULP = {0: (0.0, 0.0), 1: (2.0 ** -11, 2.0 ** -24), 2: (2.0 ** -8, 2.0 ** -133)}
 
 
+def spread_scales(p, span=12, seed=0):
+    """Lower every E8M0 block scale of both operands of problem p by its own random exponent in
+    [0, span] (kept >= 1), in place, and drop p's cached layouts. The products summed along K then
+    span about 2^(2 span) in magnitude while none grows (no FP16 overflow), so FP32 sums round and
+    their bits depend on the order of the additions: the operands of the bit-for-bit comparisons
+    between two computations. (With the generator's own scales, which follow each block's maximum,
+    the FP32 sums of the scaled products stay exact whatever the order.)"""
+    rng = np.random.default_rng(seed)
+    for sc in (p.a_scales, p.b_scales):
+        off = rng.integers(-span, 1, size=sc.shape)
+        sc[...] = np.clip(sc.astype(np.int32) + off, 1, 254).astype(np.uint8)
+    p.tiles.clear()
+    return p
+
+
 def _gemv64(X32, v64, chunk=1024):
     """X (float32 [R][K]) @ v (float64 [K]) in float64, a block of rows at a time."""
     out = np.empty(X32.shape[0], dtype=np.float64)

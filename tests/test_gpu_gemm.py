@@ -12,6 +12,13 @@ import mxfp6_amd as mx
 
 pytestmark = pytest.mark.gpu
 
+# Operands of the bit-for-bit comparisons between two computations: Student-t(3) codes with every
+# block scale lowered by a random exponent in [0, 12] (checks.spread_scales), so that FP32 sums of
+# the scaled products round and a different K order changes bits
+# (with the generator's own scales the partial sums stay exact;
+# test_bitwise_operands_see_the_k_order).
+T3 = {"dist_a": mx.DIST_STUDENT_T3, "dist_b": mx.DIST_STUDENT_T3}
+
 
 @pytest.fixture(scope="module")
 def g():
@@ -54,10 +61,34 @@ def test_routed_small_shapes(g, orc, out_type, M, N, K):
 @pytest.mark.parametrize("out_type", [0, 1, 2])
 def test_forced_tiles(g, orc, tile, out_type):
     M, N, K = 256, 1536, 960  # every tile divides 256 x 1536; K-tail: kpad(960) = 1152
-    p = mx.make_problem(M, N, K, dist_a=mx.DIST_STUDENT_T3, dist_b=mx.DIST_STUDENT_T3, seed=11)
+    p = mx.make_problem(M, N, K, **T3, seed=11)
     D = g.run_forced(g.DevProblem(p, tile), out_type)
     R, ab = _oracle(orc, p)
     checks.check(D, R, ab, out_type)
+
+
+def test_bitwise_operands_see_the_k_order(g):
+    """The bit-for-bit tests compare two computations of the same sums; they catch a kernel that
+    adds the right terms in another order only if the operands make FP32 rounding depend on the
+    order. The direct kernel, unsplit against split in three (the same products, summed per
+    segment and then across segments), shows that the spread scales do: at least 10% of the
+    outputs differ in their bits. With the generator's own scales (N(0,1) and Student-t(3) codes)
+    no output differs: every partial sum is exact."""
+    M, N, K = 256, 256, 4224
+    diff = {}
+    for name, dist, spread in (("spread", mx.DIST_STUDENT_T3, True),
+                               ("t3", mx.DIST_STUDENT_T3, False),
+                               ("normal", mx.DIST_NORMAL, False)):
+        p = mx.make_problem(M, N, K, dist_a=dist, dist_b=dist, seed=97)
+        if spread:
+            checks.spread_scales(p, seed=97)
+        dp = g.DevProblem(p, (128, 128, 2, 2))
+        D1 = g.run_direct(dp, mx.OUT_F32)
+        D3 = g.run_direct(dp, mx.OUT_F32, splits=3)
+        assert np.all(np.isfinite(D1)) and np.all(np.isfinite(D3))
+        diff[name] = int(np.count_nonzero(D1.view(np.uint32) != D3.view(np.uint32)))
+    assert diff["spread"] >= M * N // 10, diff
+    assert diff["t3"] == 0 and diff["normal"] == 0, diff
 
 
 @pytest.mark.parametrize("tile", [(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3),
@@ -67,7 +98,7 @@ def test_pipelined_kernel_bitwise_equals_direct(g, tile):
     """Both kernels add the same MFMA results in the same K order, so FP32 outputs are equal
     bit for bit (covers every wave block, slab and stage of the pipelined kernel)."""
     M, N, K = 512, 768, 2112  # 11 K-tiles: odd count, both ring stages, peeled tail
-    p = mx.make_problem(M, N, K, seed=71)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=71), seed=71)
     dp = g.DevProblem(p, tile)
     Dt = g.run_forced(dp, mx.OUT_F32)
     Dd = g.run_direct(dp, mx.OUT_F32)
@@ -76,7 +107,7 @@ def test_pipelined_kernel_bitwise_equals_direct(g, tile):
 
 def test_pipelined_split_bitwise_equals_direct_split(g):
     M, N, K = 512, 512, 3072
-    p = mx.make_problem(M, N, K, seed=81)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=81), seed=81)
     t = mx.choose_tile(M, N, p.Kp)
     S = mx.splitk_segments(M, N, p.Kp)
     assert S > 1
@@ -94,7 +125,7 @@ def test_segment_per_xcd_split_bitwise_equals_direct_split(g, tile, S, a_layout)
     (the workgroup -> (tile, segment) map differs from the grid's); every partial must still land
     in its segment's slot, so the result equals the direct kernel's split bit for bit."""
     M, N, K = 512, 768, 4224  # 22 K-tiles: uneven segments for S = 3 and 8
-    p = mx.make_problem(M, N, K, seed=83)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=83), seed=83)
     dp = g.DevProblem(p, tile)
     Dr = g.run_explicit(dp, mx.OUT_F32, splits=S, a_layout=a_layout)
     Dd = g.run_direct(dp, mx.OUT_F32, splits=S)
@@ -123,7 +154,7 @@ def test_skinny_tiles_bitwise_equal_direct(g, tile):
     """Every skinny tile, row-major and repacked A, unsplit and split: the same MFMAs in the same
     K order as the direct kernel, so FP32 outputs are equal bit for bit."""
     M, N, K = 192, 512, 2112  # 11 K-tiles: odd count, ring wrap, peeled tail
-    p = mx.make_problem(M, N, K, seed=91)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=91), seed=91)
     dp = g.DevProblem(p, tile)
     Dd = g.run_direct(dp, mx.OUT_F32)
     for a_layout in (0, 1):
@@ -142,7 +173,7 @@ def test_skinny_tiles_bitwise_equal_direct(g, tile):
 def test_repacked_a_bitwise_equals_direct(g, tile):
     """The kernel reading the repacked A multiplies the same operands in the same order."""
     M, N, K = 512, 768, 2112
-    p = mx.make_problem(M, N, K, seed=72)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=72), seed=72)
     dp = g.DevProblem(p, tile)
     Dr = g.run_explicit(dp, mx.OUT_F32, a_layout=1)
     Dd = g.run_direct(dp, mx.OUT_F32)
@@ -151,7 +182,7 @@ def test_repacked_a_bitwise_equals_direct(g, tile):
 
 def test_repacked_a_split_bitwise_equals_direct_split(g):
     M, N, K = 512, 512, 3072
-    p = mx.make_problem(M, N, K, seed=82)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=82), seed=82)
     dp = g.DevProblem(p, (128, 128, 2, 2))
     Dr = g.run_explicit(dp, mx.OUT_F32, splits=3, a_layout=1)
     Dd = g.run_direct(dp, mx.OUT_F32, splits=3)
@@ -178,7 +209,7 @@ def test_preshuffled_a_input(g):
     """A handed over already preshuffled (layout 2) gives the repack path's bits."""
     import torch
     M, N, K = 256, 512, 1536
-    p = mx.make_problem(M, N, K, seed=24)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=24), seed=24)
     dp = g.DevProblem(p, (256, 256, 4, 4))
     ash = torch.empty(M * p.Kp // 4 * 3, dtype=torch.uint8, device="cuda")
     assert mx.preshuffle_rows(dp.a.data_ptr(), p.a_row_bytes, M, p.Kp, ash.data_ptr()) == 0
@@ -194,7 +225,7 @@ def test_routed_repack_and_fallback(g, orc):
     M, N, K = g.routed_shape([(M, N, K) for K in (8192, 16384) for M in (384, 512, 640, 768, 1024)
                               for N in (4096, 5120, 5504, 6144, 6784, 8192)],
                              lambda t, S, rp: rp)
-    p = mx.make_problem(M, N, K, seed=23)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=23), seed=23)
     assert mx.repacks_a(M, N, p.Kp)
     dp = g.DevProblem(p, mx.choose_tile(M, N, p.Kp))
     rows = np.r_[0:8, 380:388, M - 8:M]
@@ -263,8 +294,8 @@ def test_split_k_uneven_segments_large_k(g, orc):
 
 def test_compact_and_padded_a_agree(g):
     M, N, K = 256, 256, 928
-    pc = mx.make_problem(M, N, K, seed=41, compact=True)
-    pp = mx.make_problem(M, N, K, seed=41, compact=False)
+    pc = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=41, compact=True), seed=41)
+    pp = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=41, compact=False), seed=41)
     assert np.array_equal(pc.a_codes_view(), pp.a_codes_view())
     t = mx.choose_tile(M, N, pc.Kp)
     Dc = g.run_routed(g.DevProblem(pc, t), mx.OUT_F32)
@@ -280,7 +311,7 @@ def test_row_stride_alignments(g, pad):
     import dataclasses
     import torch
     M, N, K = 256, 2048, 992  # Kp 1152; the repack is forced through the explicit plan
-    pp = mx.make_problem(M, N, K, seed=43, compact=False)
+    pp = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=43, compact=False), seed=43)
     rb = pp.a_row_bytes + pad
     a = np.zeros(M * rb, dtype=np.uint8)
     a.reshape(M, rb)[:, :pp.a_row_bytes] = pp.a_packed[:M * pp.a_row_bytes].reshape(M, -1)

@@ -7,6 +7,7 @@ stores and the same MFMA sequence), masked and unmasked, FP16, BF16 and FP32.
 import pytest
 import torch
 
+import checks
 import mxfp6_amd as mx
 from gpu_util import DevProblem, run_direct, run_routed, say
 
@@ -20,7 +21,8 @@ pytestmark = pytest.mark.gpu
     (8192, 12288, 192, mx.OUT_F32),     # a single K-tile: the 256x256 tile's single-K-tile kernel
 ])
 def test_routed_streaming_plan_equals_direct_kernel(M, N, K, out_type):
-    p = mx.make_problem(M, N, K, seed=M + 11 * N + K)
+    # block scales spread so that FP32 bits depend on the K order (compared bit for bit)
+    p = checks.spread_scales(mx.make_problem(M, N, K, seed=M + 11 * N + K), seed=K)
     tile = mx.choose_tile(M, N, p.Kp)
     assert mx.splitk_segments(M, N, p.Kp) == 1
     assert mx.streams_output(out_type, M, N, p.Kp, p.a_row_bytes), "plan does not stream D"

@@ -11,6 +11,13 @@ import checks
 import mxfp6_amd as mx
 import gpu_util as g
 
+# Operands of the bit-for-bit comparisons between two computations: Student-t(3) codes with every
+# block scale lowered by a random exponent in [0, 12] (checks.spread_scales), so that FP32 sums of
+# the scaled products round and a different K order changes bits
+# (with the generator's own scales the partial sums stay exact; test_gpu_gemm.py
+# test_bitwise_operands_see_the_k_order).
+T3 = {"dist_a": mx.DIST_STUDENT_T3, "dist_b": mx.DIST_STUDENT_T3}
+
 pytestmark = pytest.mark.gpu
 
 WIDE_TILES = [(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4, 2)]
@@ -25,7 +32,8 @@ def test_wide_bitwise_equals_direct(WIDE, tm, tn, K, a_layout):
     and 3: the 256 x 256 tile's K loop runs K-tiles in pairs, so odd counts take its
     single-K-tile tail; with 2 and 3 K-tiles most prefetches are clamped to the last K-tile."""
     M, N = 256 * tm, WIDE[1] * tn
-    p = mx.make_problem(M, N, K, seed=M + N + K + a_layout)
+    seed = M + N + K + a_layout
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=seed), seed=seed)
     dp = g.DevProblem(p, WIDE)
     Dw = g.run_explicit(dp, mx.OUT_F32, a_layout=a_layout)
     Dd = g.run_direct(dp, mx.OUT_F32)
@@ -40,7 +48,7 @@ def test_wide_split_bitwise_equals_direct_split(WIDE, M, tn, S):
     every partial lands in its segment's slot either way."""
     N = WIDE[1] * tn
     K = 4224  # 22 K-tiles: uneven segments
-    p = mx.make_problem(M, N, K, seed=S * 7 + M)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=S * 7 + M), seed=S * 7 + M)
     dp = g.DevProblem(p, WIDE)
     for a_layout in (0, 1, 3):
         Dw = g.run_explicit(dp, mx.OUT_F32, splits=S, a_layout=a_layout)
@@ -55,7 +63,7 @@ def test_wide_single_k_tile_segments(WIDE, S, K):
     short-path instantiations; the swizzled staging has no short path of its own and runs its main
     loop): bit for bit the direct kernel, rows (both stagings) and repacked A."""
     M, N = 512, WIDE[1] * 2
-    p = mx.make_problem(M, N, K, seed=S * 11 + K)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=S * 11 + K), seed=S * 11 + K)
     dp = g.DevProblem(p, WIDE)
     for a_layout in (0, 1, 3):
         Dw = g.run_explicit(dp, mx.OUT_F32, splits=S, a_layout=a_layout)
@@ -91,7 +99,7 @@ def test_wide_short_path_lowp_outputs(WIDE, K):
 def test_wide_masked_equals_slab_masked(WIDE, M, N, K):
     """Ragged shapes run the wide tile masked; its FP32 output equals the masked 256x256 slab
     kernel's (same scale grouping, same K order) bit for bit, and both meet the oracle bar."""
-    p = mx.make_problem(M, N, K, seed=M * 7 + N)
+    p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=M * 7 + N), seed=M * 7 + N)
     dw = g.DevProblem(p, WIDE)
     ds = g.DevProblem(p, (256, 256, 4, 4))
     for a_layout, S in ((0, 1), (1, 1), (0, 3)):
@@ -110,7 +118,7 @@ def test_wide_masked_equals_slab_masked(WIDE, M, N, K):
 def test_wide_output_types_against_oracle(WIDE, out_type):
     import oracle
     M, N, K = 256, 1024, 960  # K-tail: kpad(960) = 1152
-    p = mx.make_problem(M, N, K, dist_a=mx.DIST_STUDENT_T3, dist_b=mx.DIST_STUDENT_T3, seed=13)
+    p = mx.make_problem(M, N, K, **T3, seed=13)
     dp = g.DevProblem(p, WIDE)
     R, ab = oracle.problem_f64(p)
     for a_layout in (0, 1):
