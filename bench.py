@@ -17,6 +17,8 @@ drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX 
   python bench.py --ab PLANS [--config cN] [--repeat R]  (explicit plans MTxNTxMPWxNPW[:S[:r|p|s]]
                                of a workload against each other and the routed plan, R rounds,
                                order rotated)
+  python bench.py --e2e [--all]  (float A to D on the device: quantise to row-major A + the routed
+                                  gemm, against quantise to preshuffled A + the same plan)
   python bench.py --map [SHAPES|second] [--repeat R]  (this library against the reference library,
                                shape by shape: MxNxK,... or the default map of 154 shapes, FP16
                                out; R > 1: R more runs per library, alternating their order)
@@ -798,6 +800,72 @@ def run_ab(name, plans, repeat):
     return out
 
 
+def run_e2e(names):
+    """Float A to D on the device, two ways, for each workload: quantise A into row-major rows
+    (mxfp6_prepare_a_async) and run the routed gemm() on them (with its preferred workspace, so
+    that it repacks where the router does), against quantising A straight into the preshuffled
+    layout (mxfp6_prepare_a_preshuffled_async) and running the router's tile and split on it as
+    an explicit plan (A layout 2). B is prepared once beforehand (a weight); each path is timed
+    by the reference's method (best_of), both calls per step. FP32 A from N(0, sigma) of the
+    workload, B from N(0, 1): the timing does not depend on the values."""
+    import torch
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    out = {}
+    for name in names:
+        M, N, K, ot, (_, sa_), _, _ = CONFIGS[name]
+        Kp = mx.kpad(K)
+        tile = mx.choose_tile(M, N, Kp)
+        S = mx.splitk_segments(M, N, Kp)
+        g = torch.Generator(device=dev)
+        g.manual_seed(SEED ^ int(name[1:]))
+        A = torch.randn(M, K, device=dev, generator=g) * sa_
+        B = torch.randn(K, N, device=dev, generator=g)
+        rb = Kp // 4 * 3
+        bsh = torch.empty(mx.preshuffled_bytes(N, K), dtype=torch.uint8, device=dev)
+        tsb = torch.empty(mx.tiled_scale_bytes(N, K, tile[3]), dtype=torch.uint8, device=dev)
+        if mx.prepare_b_dev(B.data_ptr(), K, N, tile[3], bsh.data_ptr(), tsb.data_ptr(), sp):
+            raise RuntimeError("prepare_b failed")
+        del B
+        rows = torch.empty(M * rb, dtype=torch.uint8, device=dev)
+        ash = torch.empty(mx.preshuffled_bytes(M, K), dtype=torch.uint8, device=dev)
+        tsa = torch.empty(mx.tiled_scale_bytes(M, K, tile[2]), dtype=torch.uint8, device=dev)
+        D = torch.empty(M * N * mx.OUT_BYTES[ot], dtype=torch.uint8, device=dev)
+        wsr = mx.preferred_workspace_size(M, N, Kp)
+        wse = mx.plan_workspace_size(M, N, Kp, S, False)
+        ws = torch.empty(max(wsr, wse, 4), dtype=torch.uint8, device=dev)
+
+        def via_rows():
+            if mx.prepare_a_dev(A.data_ptr(), M, K, tile[2], rows.data_ptr(), rb,
+                                tsa.data_ptr(), sp):
+                raise RuntimeError("prepare_a failed")
+            if mx.gemm(ot, M, N, Kp, rows.data_ptr(), bsh.data_ptr(), tsa.data_ptr(),
+                       tsb.data_ptr(), D.data_ptr(), rb, ws.data_ptr(), wsr, stream=sp):
+                raise RuntimeError("gemm failed")
+
+        def via_preshuffled():
+            if mx.prepare_a_preshuffled_dev(A.data_ptr(), M, K, tile[2], ash.data_ptr(),
+                                            tsa.data_ptr(), sp):
+                raise RuntimeError("prepare_a_preshuffled failed")
+            if mx.gemm_explicit(ot, M, N, Kp, tile, S, ash.data_ptr(), bsh.data_ptr(),
+                                tsa.data_ptr(), tsb.data_ptr(), D.data_ptr(), rb,
+                                ws.data_ptr() if wse else 0, wse, stream=sp, a_layout=mx.A_PRESHUFFLED):
+                raise RuntimeError("explicit gemm failed")
+
+        t_rows = best_of(via_rows, stream)[0] * 1e3
+        t_pre = best_of(via_preshuffled, stream)[0] * 1e3
+        out[name] = {"workload": workload_name(M, N, K, ot), "tile": list(tile), "splitk": S,
+                     "routed_repacks_a": bool(mx.repacks_a(M, N, Kp)),
+                     "rows_then_gemm_us": round(t_rows, 1),
+                     "preshuffled_then_explicit_us": round(t_pre, 1),
+                     "ratio": round(t_rows / t_pre, 3)}
+        log(f"[bench] e2e {name}: {out[name]}")
+        del A, rows, ash, tsa, tsb, bsh, D, ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def diag_library():
     """libmxfp6diag.so (the MFMA-only diagnostic kernel), loaded with ctypes."""
     import ctypes as C
@@ -939,6 +1007,10 @@ def main():
                          "instead (MTxNTxMPWxNPW[:S[:r|p|s]],...; r: repacked A, p: A "
                          "preshuffled beforehand, s: row-major A staged swizzled; with --repeat R "
                          "rounds)")
+    ap.add_argument("--e2e", action="store_true",
+                    help="float A to D on the device instead: quantise to row-major A + the routed "
+                         "gemm against quantise to preshuffled A + the same plan (the workload, or "
+                         "with --all the four large ones)")
     ap.add_argument("--map", nargs="?", const="", default=None, metavar="SHAPES",
                     help="this library against the reference library shape by shape instead "
                          "(MxNxK,... or a file of them; 'second': 160 other shapes; "
@@ -960,6 +1032,9 @@ def main():
         return
     if a.power > 0:
         print(json.dumps(run_power(a.config, a.power)), flush=True)
+        return
+    if a.e2e:
+        print(json.dumps(run_e2e(["c2", "c3", "c4", "c5"] if a.all else [a.config])), flush=True)
         return
     if a.ab is not None:
         print(json.dumps(run_ab(a.config, a.ab, max(a.repeat, 1))), flush=True)

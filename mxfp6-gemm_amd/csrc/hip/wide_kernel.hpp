@@ -19,13 +19,15 @@
 //      per row, the K-tile's 144 contiguous bytes of the row-major operand (or, for A repacked
 //      into the preshuffled layout, the K-tile's three 1536-byte tiles of each 32-row block),
 //      MT x 144 bytes, copied with direct-to-LDS 16-byte loads (global_load_lds_dwordx4). A row's
-//      144 bytes take 2-3 cache lines where a 64-wide slab copy of 48 bytes takes 1-2 per slab, so
-//      row-major A costs about half the L2 requests of a per-slab copy. Chunks go through a ring
-//      of NB LDS buffers: chunk c + NB - 1 is copied during K-tile c (the wave's copies spread over
-//      the K-tile's three slabs; a chunk of 128 rows is 18 wave copies, two dummies keep the count
-//      per wave uniform), and a wave reads each slab's A operand blocks during the previous slab
-//      into a register set: three sets (one per slab of a K-tile) for MB 4, two alternating sets
-//      for MB 8 (the K loop then runs K-tiles in pairs).
+//      144 bytes at a 16-byte offset span two 128-byte cache lines where a 64-wide slab copy of 48
+//      bytes takes 1-2 per slab, so row-major A costs about half the L2 requests of a per-slab
+//      copy. Chunks go through a ring of NB LDS buffers: chunk c + NB - 1 is copied during K-tile
+//      c (the wave's copies spread over the K-tile's three slabs; a chunk of 128 rows is 18 wave
+//      copies, two dummies keep the count per wave uniform), and a wave reads each slab's A
+//      operand blocks during the previous slab into a register set: three sets (one per slab of a
+//      K-tile) for MB 4, two alternating sets for MB 8. The K loop runs passes of six K-tiles, so
+//      the chunk buffer (period 3), the A set and the scale set (period 2) of every step are
+//      compile-time constants.
 // One workgroup barrier per K-tile, at the start of its last slab: before it, each wave waits for
 // its own copies of the next chunk (vmcnt, exact: the issue order is static) and for its LDS reads
 // (lgkmcnt(0)); after it the next chunk is complete for every wave and the chunk read before the

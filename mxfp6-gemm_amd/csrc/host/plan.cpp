@@ -30,10 +30,10 @@ namespace plan {
 //   128x256, each wave 128x64             -> MPW 4, NPW 2   (8)
 //   256x256, each wave 256x64             -> MPW 4, NPW 2   (16; A scales in two groups of 4)
 // and the skinny tiles (waves 1x4), the only ones for M not a multiple of 128 (M a multiple of
-// 32), and on small grids faster than the big ones for any M (C1, 256x256x1024: 32x128 6.3 us
-// against 8.2 us on 128x128):
+// 32), and on small grids faster than the big ones for any M (C1, 256x256x1024: 32x128 6.2 us
+// against 7.2 us on 128x128 and 8.2 us on the 128x256 wide tile):
 //   64x256 (MPW 2, NPW 2), 32x256 (1, 2), 64x128 (2, 1), 32x128 (1, 1; two per CU)
-// Ragged shapes (M not a multiple of 32 or N not a multiple of 128) take any of the ten tiles,
+// Ragged shapes (M not a multiple of 32 or N not a multiple of 128) take any of the eleven tiles,
 // the last tile row and column masked (wg counts the partial tiles).
 // A plan is (tile, K segments S from SPLIT_CHOICES, A repacked or not); the router takes the plan
 // with the least predicted time. The time model (microseconds, MI355X) follows the kernel's

@@ -29,8 +29,9 @@ WIDE_TILES = [(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4
 @pytest.mark.parametrize("a_layout", [0, 1, 3])
 def test_wide_bitwise_equals_direct(WIDE, tm, tn, K, a_layout):
     """tm x tn tiles (M, N multiples of 256 and of the tile); the K-tile counts 11, 1, 22, 18, 2
-    and 3: the 256 x 256 tile's K loop runs K-tiles in pairs, so odd counts take its
-    single-K-tile tail; with 2 and 3 K-tiles most prefetches are clamped to the last K-tile."""
+    and 3: the K loop runs passes of six K-tiles and leaves after any of them (11 and 22 end
+    mid-pass, 18 on a pass boundary); with 2 and 3 K-tiles most prefetches are clamped to the last
+    K-tile."""
     M, N = 256 * tm, WIDE[1] * tn
     seed = M + N + K + a_layout
     p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=seed), seed=seed)
