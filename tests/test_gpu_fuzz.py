@@ -8,7 +8,9 @@ for (so the plans it picks are exercised: big and skinny tiles, N-masked and rag
 split-K on either XCD map, repacked A) and again with no
 workspace (the documented fallback to the unsplit, unrepacked plan), and is checked against the
 FP64 oracle at this build's bar (tests/checks.py) on every row of a small M, or on 48 spread rows.
-Outputs and workspaces carry guard regions that must survive the call.
+Outputs and workspaces carry guard regions that must survive the call. The same shapes run again
+on operands whose FP32 sums depend on the order of the additions (FP32 out, tests/checks.py
+spread_scales), where the two workspaces that run the same split must also agree bit for bit.
 """
 import numpy as np
 import pytest
@@ -81,3 +83,23 @@ def test_routed_random_shape(M, N, K, out_type):
     for with_ws in ("preferred", "split", False):
         D = _run(dp, out_type, with_ws)
         checks.check(D if rows is None else D[rows], R, ab, out_type)
+
+
+@pytest.mark.parametrize("M,N,K,_", _shapes())
+def test_routed_random_shape_order_sensitive(M, N, K, _):
+    """The same shapes on operands whose FP32 sums depend on the order of the additions (block
+    scales lowered by random exponents, checks.spread_scales), FP32 out: each run within the FP32
+    bar of the FP64 oracle, and the plan's whole workspace and the split-only one (the same K
+    segments, A repacked or read row-major) bit for bit equal."""
+    seed = M * 131 + N * 17 + K + 1
+    p = checks.spread_scales(mx.make_problem(M, N, K, seed=seed), seed=seed)
+    dp = DevProblem(p, mx.choose_tile(M, N, p.Kp))
+    rows = None if M <= 48 else np.unique(np.r_[0:4, M - 4:M,
+                                                 np.linspace(0, M - 1, 40).astype(int)])
+    R, ab = oracle.problem_f64(p, rows=rows)
+    out = {}
+    for with_ws in ("preferred", "split", False):
+        D = _run(dp, mx.OUT_F32, with_ws)
+        checks.check(D if rows is None else D[rows], R, ab, mx.OUT_F32)
+        out[with_ws] = D
+    assert np.array_equal(out["preferred"].view(np.uint32), out["split"].view(np.uint32))
