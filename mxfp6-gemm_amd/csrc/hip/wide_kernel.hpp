@@ -38,9 +38,13 @@
 // with up to three (K <= 576, or a split segment that short), takes a short path instead: every
 // K-tile's chunk, scales and B operands (a register set per K-tile) are requested before the
 // first MFMA, so no K-tile waits out a memory latency for B loads issued during the one before
-// it, and no clamped prefetch is issued (128 x 512 and 256 x 256 run segments of one or two
-// K-tiles in instantiations of their own, ONE = 1 or 2, unmasked only: with the path in their
-// main kernel the masked and repacked-A instantiations would spill, and so would a masked ONE).
+// it, and no clamped prefetch is issued (128 x 512 runs segments of one or two K-tiles and
+// 256 x 256 of one to three in instantiations of their own, ONE = 1, 2 or 3, unmasked only: with
+// the path in their main kernel the masked and repacked-A instantiations would spill, and so
+// would a masked ONE; three K-tiles of 128 x 512 would issue more loads up front than vmcnt
+// counts). With every CU requesting its first K-tiles at once, the main loop's one-K-tile lead
+// leaves each of the first K-tiles waiting on a loaded memory system; up front, the latencies
+// overlap (256 x 256, three K-tiles: 8192 x 4096 x 512 42.1 us in the main loop).
 // MASK (ragged M or N) clamps the copy and load sources
 // of the last tile row and column and masks the stores, as in the slab kernel.
 // SWZ (explicit plans only, never routed; row-major A, unmasked) stages a chunk row as twelve
@@ -550,8 +554,17 @@ hipError_t wide_kernel_launch(const mxfp6_launch_desc* d, const uint8_t* A, hipS
                                  d->M, d->N, d->Kp, d->A_row_bytes, SPLIT ? d->splits : 1);
     }
     if constexpr (G::SHORT_MAX == 0 && !MASK) {
-        // every K segment one or two K-tiles: the short-path instantiations (not for masked
-        // tiles, whose instantiations of it would spill)
+        // every K segment one to three K-tiles: the short-path instantiations (not for masked
+        // tiles, whose instantiations of it would spill; three K-tiles on 256 x 256 only, where
+        // the loads issued up front still fit the vmcnt range)
+        if constexpr (G::short_wait(3, 0) <= 63)
+            if (d->Kp / 192 == 3 * d->splits)
+                return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK, STREAM, 3>,
+                                     grid, dim3(G::THREADS), st, A,
+                                     static_cast<const uint8_t*>(d->Bsh), d->sA, d->sB,
+                                     SPLIT ? nullptr : static_cast<KT*>(d->D),
+                                     SPLIT ? d->ws : nullptr, d->M, d->N, d->Kp, d->A_row_bytes,
+                                     SPLIT ? d->splits : 1);
         if (d->Kp / 192 == 2 * d->splits)
             return launch_kernel(wide_kernel<MB, NPW, NB, XG, KT, SPLIT, ASH, MASK, STREAM, 2>,
                                  grid, dim3(G::THREADS), st, A,

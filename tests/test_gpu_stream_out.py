@@ -19,6 +19,7 @@ pytestmark = pytest.mark.gpu
     (1024, 102272, 2048, mx.OUT_BF16),
     (4096, 16384, 1024, mx.OUT_F32),
     (8192, 12288, 192, mx.OUT_F32),     # a single K-tile: the 256x256 tile's single-K-tile kernel
+    (8192, 12288, 576, mx.OUT_F32),     # three K-tiles: its three-K-tile kernel
 ])
 def test_routed_streaming_plan_equals_direct_kernel(M, N, K, out_type):
     # block scales spread so that FP32 bits depend on the K order (compared bit for bit)

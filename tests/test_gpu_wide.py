@@ -58,11 +58,13 @@ def test_wide_split_bitwise_equals_direct_split(WIDE, M, tn, S):
 
 
 @pytest.mark.parametrize("WIDE", WIDE_TILES)
-@pytest.mark.parametrize("S,K", [(1, 192), (3, 576), (6, 1152), (1, 384), (3, 1152)])
+@pytest.mark.parametrize("S,K", [(1, 192), (3, 576), (6, 1152), (1, 384), (3, 1152), (2, 1152),
+                                 (3, 1728)])
 def test_wide_single_k_tile_segments(WIDE, S, K):
-    """Every K segment one or two K-tiles (the short path, or for 128 x 512 and 256 x 256 their
-    short-path instantiations; the swizzled staging has no short path of its own and runs its main
-    loop): bit for bit the direct kernel, rows (both stagings) and repacked A."""
+    """Every K segment one, two or three K-tiles (the short path, or for 128 x 512 and 256 x 256
+    their short-path instantiations, three K-tiles on 256 x 256 only; the swizzled staging has no
+    short path of its own and runs its main loop): bit for bit the direct kernel, rows (both
+    stagings) and repacked A."""
     M, N = 512, WIDE[1] * 2
     p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=S * 11 + K), seed=S * 11 + K)
     dp = g.DevProblem(p, WIDE)
@@ -76,7 +78,7 @@ def test_wide_single_k_tile_segments(WIDE, S, K):
 @pytest.mark.parametrize("K", [192, 384, 576])
 def test_wide_short_path_lowp_outputs(WIDE, K):
     """Unsplit K of one to three K-tiles (the short path, or the short-path instantiations of
-    128 x 512 and 256 x 256) with 16-bit outputs: FP32 equals the direct kernel bit for bit, and
+    128 x 512 (one or two) and 256 x 256 (one to three)) with 16-bit outputs: FP32 equals the direct kernel bit for bit, and
     FP16 / BF16 equal that FP32 rounded to nearest-even on the host, rows (both stagings) and
     repacked A."""
     M, N = 512, WIDE[1] * 2
