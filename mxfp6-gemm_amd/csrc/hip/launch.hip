@@ -10,6 +10,7 @@
 #include "reduce_kernel.hpp"
 #include "repack_kernel.hpp"
 #include "slab_run.hpp"
+#include "tiny_kernel.hpp"
 
 using namespace mxfp6_dev;
 
@@ -56,6 +57,8 @@ int launch_typed(const mxfp6_launch_desc* d, hipStream_t st) {
         case MXFP6_KERNEL_DIRECT:
             return launch_direct<OutT>(d, st);
         case MXFP6_KERNEL_TILE: {
+            // the 32 x 32 tile: K split over the workgroup's waves, reduced in LDS (no workspace)
+            if (d->MT == 32 && d->NT == 32) return tiny_launch<OutT>(d, st);
             if (d->splits <= 1) return slab_run<OutT, false>(d, st);
             const int rc = slab_run<float, true>(d, st);
             return rc != 0 ? rc : launch_reduce<OutT>(d, st);

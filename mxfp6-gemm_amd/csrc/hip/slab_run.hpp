@@ -11,7 +11,8 @@ namespace mxfp6_dev {
 // (MT, NT, MPW, NPW) -> wave grid: the scale grouping fixes how many 32-blocks one wave holds,
 // so it also selects between the 4-wave and 8-wave instantiation of a tile.
 inline bool tile_supported(int MT, int NT, int mpw, int npw) {
-    return (MT == 32 && NT == 128 && mpw == 1 && npw == 1) ||
+    return (MT == 32 && NT == 32 && mpw == 1 && npw == 1) ||  // tiny_kernel.hpp (launch.hip)
+           (MT == 32 && NT == 128 && mpw == 1 && npw == 1) ||
            (MT == 32 && NT == 256 && mpw == 1 && npw == 2) ||
            (MT == 64 && NT == 128 && mpw == 2 && npw == 1) ||
            (MT == 64 && NT == 256 && mpw == 2 && npw == 2) ||

@@ -172,9 +172,38 @@ void visit_plans(int M, int N, int Kp, F&& f) {
                 }
 }
 
+// The 32 x 32 tile (tiny_kernel.hpp): K split over a workgroup's four waves, every operand loaded
+// before the first MFMA, the segments summed in LDS. Routed by a measured rule ahead of the model,
+// which has no term for it: at most one 32 x 32 block per CU and 3 to 12 K-tiles, in the fewest
+// segments of at most four K-tiles (fewer segments measured faster: 256 x 256 x 1024 5.1, 5.6 and
+// 6.1 us in 2, 3 and 4). Against the routed pipelined plans on 16 shapes of that range: 6-28%
+// faster (256 x 256 x 1024 6.09 -> 5.13 us, 256 x 256 x 768 5.17 -> 3.94, 512 x 256 x 1536 7.81 ->
+// 5.64, 256 x 1024 x 2048 9.01 -> 6.92); slower below 3 K-tiles (2-3%), on part of the shapes
+// with 13-16 (up to 4%), and on grids of two blocks per CU (1024 x 512 x 1024 6.38 -> 6.70).
+// The 32 x 32 tile splits K over its four waves: at most 4 segments of at most 4 K-tiles, on
+// row-major A (tiny_kernel.hpp).
+bool tiny_plan_ok(const TileChoice& tc, int Kp, int S, int a_layout) {
+    if (tc.MT != 32 || tc.NT != 32) return true;
+    const int kt = Kp / K_TILE;
+    return a_layout == MXFP6_A_ROWS && S >= 1 && S <= 4 && (kt + S - 1) / S <= 4;
+}
+
+const TileChoice kTiny = {32, 32, 1, 1};
+
+bool is_tiny(const TileChoice& tc) {
+    return tc.MT == kTiny.MT && tc.NT == kTiny.NT && tc.MPW == kTiny.MPW && tc.NPW == kTiny.NPW;
+}
+
+bool tiny_routed(int M, int N, int Kp, int cus) {
+    const long blocks = (long)((M + 31) / 32) * ((N + 31) / 32);
+    const int kt = Kp / K_TILE;
+    return blocks <= cus && kt >= 3 && kt <= 12;
+}
+
 Plan best_plan(int M, int N, int Kp, int cus) {
     Plan best = {{128, 128, 2, 2}, 1, false};
     if (!shape_ok(M, N, Kp)) return best;
+    if (tiny_routed(M, N, Kp, cus)) return {kTiny, (Kp / K_TILE + 3) / 4, false};
     double best_t = -1.0;
     visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
         const double t = plan_time_us(tc, M, N, Kp, S, rp, cus);
@@ -191,6 +220,9 @@ Plan best_plan(int M, int N, int Kp, int cus) {
 // with gemm_workspace_size's workspace, 1 with none). For a given S every tile of a grouping gives
 // the same output bits (each K segment's MFMAs in the same K order, the same reduction).
 Plan best_fitting_plan(int M, int N, int Kp, int cus, const TileChoice& grouping, int S_fixed) {
+    // the 32 x 32 tile itself where it can run the split (its plans never repack)
+    if (is_tiny(grouping) && tiny_plan_ok(grouping, Kp, S_fixed, MXFP6_A_ROWS))
+        return {grouping, S_fixed, false};
     Plan best = {grouping, S_fixed, false};
     double best_t = -1.0;
     visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
@@ -478,7 +510,11 @@ int tune(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh, c
         Plan plan;
     };
     std::vector<Ranked> ranked;
+    // the routed plan is always measured (the 32 x 32 tile is not among the model's plans)
+    if (plan_fits(M, N, Kp, routed.S, routed.repack, ws_bytes)) ranked.push_back({-1.0, routed});
     visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
+        if (tc.MT == routed.tc.MT && tc.NT == routed.tc.NT && S == routed.S && rp == routed.repack)
+            return;
         if (tc.MPW != routed.tc.MPW || tc.NPW != routed.tc.NPW) return;
         if (kernel_for(tc) != MXFP6_KERNEL_TILE) return;
         if (!plan_fits(M, N, Kp, S, rp, ws_bytes)) return;
@@ -729,6 +765,7 @@ extern "C" int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const i
     if (!plan::tile_divides(tile, M, N)) return MXFP6_ERR_TILE;
     const TileChoice tc = {tile[0], tile[1], tile[2], tile[3]};
     if (!mxfp6_hip_has_tile(tc.MT, tc.NT, tc.MPW, tc.NPW)) return MXFP6_ERR_TILE;
+    if (!plan::tiny_plan_ok(tc, Kp, 1, MXFP6_A_ROWS)) return MXFP6_ERR_TILE;
     return plan::run(out_type, M, N, Kp, tc, 1, MXFP6_A_ROWS, MXFP6_KERNEL_TILE, dA, dBsh, dsA,
                      dsB, dD, A_row_bytes, nullptr, stream);
 }
@@ -749,6 +786,7 @@ extern "C" int mxfp6_gemm_explicit(int out_type, int M, int N, int Kp, const int
     // the swizzled staging of row-major A exists for the wide tiles, unmasked
     if (a_layout == MXFP6_A_ROWS_SWIZZLED && (!plan::is_wide(tc) || !plan::tile_divides(tile, M, N)))
         return MXFP6_ERR_ARG;
+    if (!plan::tiny_plan_ok(tc, Kp, splits, a_layout)) return MXFP6_ERR_ARG;
     const bool repack = a_layout == MXFP6_A_REPACK;
     if ((splits > 1 || repack) &&
         (ws == nullptr || ws_bytes < plan::plan_bytes(M, N, Kp, splits, repack)))

@@ -21,6 +21,9 @@ SPLIT_CHOICES = (1, 2, 3, 4, 6, 8, 12, 16)
 # the routed tiles (256x192 is implemented but not routed: plan.cpp kCands)
 TILES = [(256, 256, 4, 4), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2), (128, 512, 4, 4),
          (128, 256, 4, 2), (256, 256, 4, 2)]
+# the 32 x 32 tile (tiny_kernel.hpp): routed by a measured rule ahead of the model (plan.cpp
+# tiny_routed): at most one 32 x 32 block per CU and 3 to 12 K-tiles, in ceil(K-tiles / 4) segments
+TINY = (32, 32, 1, 1)
 # the tiles whose B goes straight to registers (wide_kernel.hpp)
 WIDE = {(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4, 2)}
 SKINNY = [(64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)]
@@ -117,8 +120,16 @@ def _pick(times):
         bi = later[0]
 
 
+def tiny_routed(M, N, Kp):
+    kt = Kp // K_TILE
+    return -(-M // 32) * -(-N // 32) <= CUS and 3 <= kt <= 12
+
+
 def best_plan(c, M, N, Kp):
-    """(tile, S, repack) with the least predicted time, as plan.cpp best_plan."""
+    """(tile, S, repack) with the least predicted time, as plan.cpp best_plan (the 32 x 32 tile's
+    rule first)."""
+    if tiny_routed(M, N, Kp):
+        return (TINY, -(-(Kp // K_TILE) // 4), False)
     cands = candidates(M, N, Kp)
     if not cands:
         return ((128, 128, 2, 2), 1, False)
@@ -217,12 +228,15 @@ def evaluate(c, recs):
 def main():
     paths = sys.argv[1:] or [os.path.join(HERE, "plans_mi355x.jsonl")]
     recs = load([p for p in paths if p != "--no-fit"] or [os.path.join(HERE, "plans_mi355x.jsonl")])
-    # the constants are fitted on the shapes with M % 128 == 0 (every tile measured on them)
-    fit_recs = [r for r in recs if r["shape"][0] % 128 == 0]
+    # the constants are fitted on the shapes with M % 128 == 0 (every tile measured on them) that
+    # the model routes (not those of the 32 x 32 tile's rule)
+    def modelled(r):
+        M, N, K = r["shape"]
+        return M % 128 == 0 and not tiny_routed(M, N, (K + K_TILE - 1) // K_TILE * K_TILE)
+    fit_recs = [r for r in recs if modelled(r)]
     if "--no-fit" in sys.argv:
         c = CONSTANTS
     else:
-        fit_recs = [r for r in recs if r["shape"][0] % 128 == 0]
         c, l = fit(fit_recs, CONSTANTS)
         print("fitted constants (objective %.3f over %d shapes):" % (l, len(fit_recs)))
         for n in NAMES:

@@ -73,6 +73,13 @@ def test_argument_checks_reject_before_launch(mx):
                             a_layout=sw) == 5                                        # masked M
     assert mx.gemm_explicit(0, 256, 256, 192, (256, 256, 4, 2), 1, p, p, p, p, p, 144,
                             a_layout=sw + 1) == 5                                    # no layout 4
+    # the 32 x 32 tile: at most 4 segments of at most 4 K-tiles, row-major A
+    assert mx.gemm_explicit(0, 256, 256, 1152, (32, 32, 1, 1), 1, p, p, p, p, p, 864) == 5  # 6 > 4
+    assert mx.gemm_explicit(0, 256, 256, 3456, (32, 32, 1, 1), 4, p, p, p, p, p, 2592,
+                            ws=p, ws_bytes=1 << 30) == 5                             # 18 K-tiles
+    assert mx.gemm_explicit(0, 256, 256, 576, (32, 32, 1, 1), 1, p, p, p, p, p, 432,
+                            a_layout=mx.A_REPACK, ws=p, ws_bytes=1 << 30) == 5       # repack
+    assert mx.gemm_force_tile(0, 256, 256, 1152, (32, 32, 1, 1), p, p, p, p, p, 864) == 4
     assert mx.gemm_direct(0, 128, 128, 192, 5, 2, p, p, p, p, p, 144) == 5
     assert mx.gemm_direct(0, 128, 128, 192, 2, 2, p, p, p, p, p, 144, splits=2) == 5
     assert mx.gemm_direct(0, 96, 128, 192, 1, 1, p, p, p, p, p, 144) == 2   # M % 64

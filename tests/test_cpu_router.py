@@ -19,6 +19,8 @@ with open(os.path.join(GOLD, "ref_routing.json")) as f:
 IMPLEMENTED = {(128, 128, 2, 2), (128, 256, 2, 4), (128, 384, 4, 3), (256, 256, 4, 4),
                (256, 192, 4, 3), (128, 512, 4, 4), (128, 256, 4, 2), (256, 256, 4, 2)}
 SKINNY = {(64, 256, 2, 2), (32, 256, 1, 2), (64, 128, 2, 1), (32, 128, 1, 1)}
+# the 32 x 32 tile (K split over a workgroup's waves): routed by its own rule, not the model
+TINY = {(32, 32, 1, 1)}
 
 
 def _kpad(K):
@@ -65,7 +67,7 @@ def test_router_covers_every_multiple_of_128(mx):
             for K in (512, 16128, 105728):
                 Kp = _kpad(K)
                 t = mx.choose_tile(M, N, Kp)
-                if M % t[0] or tuple(t) not in IMPLEMENTED | SKINNY:
+                if M % t[0] or tuple(t) not in IMPLEMENTED | SKINNY | TINY:
                     bad.append((M, N, K, t))
                 if (M // 32) % t[2] or (N // 32) % t[3]:
                     badgroup.append((M, N, K, t))
@@ -148,7 +150,7 @@ def test_router_degenerate_shapes_do_not_trap(mx):
         Kp = _kpad(K)
         t = mx.choose_tile(M, N, Kp)
         if M > 0 and N > 0 and Kp > 0:
-            assert tuple(t) in IMPLEMENTED | SKINNY
+            assert tuple(t) in IMPLEMENTED | SKINNY | TINY
             if M % 32 == 0 and N % 128 == 0:
                 assert M % t[0] == 0 and N % t[1] == 0
         else:
@@ -162,7 +164,7 @@ def test_router_benchmark_shapes(mx):
     # 2048x6144x16128, where the 128x384 tile measured 116.7 us on the sweep's box (5% faster)
     # and tied with the pick on another.
     want = {
-        (256, 256, 1024): ((32, 128, 1, 1), 1),
+        (256, 256, 1024): ((32, 32, 1, 1), 2),         # 5.4 us, the best of 123 plans
         (8192, 8192, 8192): ((256, 256, 4, 2), 1),     # 307.4 us vs 319.7 on 256x256 (4, 4), repack
         (2048, 6144, 16128): ((256, 256, 4, 2), 1),    # 123.7 us vs 127.0 on 128x512
         (2048, 1024, 105728): ((256, 256, 4, 2), 8),   # 154.4 us vs 164.9 on 128x512
@@ -186,7 +188,7 @@ def test_router_small_k_plans(mx):
     (down to the 32- and 64-row tiles) and no extra launch for the repack; the router's model
     reproduces the measured winners."""
     want = {  # (M, N, K): (tile, S, repack) measured fastest
-        (256, 256, 1024): ((32, 128, 1, 1), 1, False),     # 6.2 us vs 6.5 for the next plan
+        (256, 256, 1024): ((32, 32, 1, 1), 2, False),      # 5.4 us vs 6.2 on 32x128 (1, 1)
         (1024, 1024, 1024): ((32, 128, 1, 1), 1, False),   # 6.7 us vs 7.1
         (2048, 1024, 1024): ((64, 128, 2, 1), 1, False),   # 7.8 us vs 8.2
         (2048, 256, 2048): ((32, 128, 1, 1), 1, False),    # 8.9 us vs 9.8 (no split)
@@ -199,6 +201,25 @@ def test_router_small_k_plans(mx):
         got = (tuple(mx.choose_tile(M, N, Kp)), mx.splitk_segments(M, N, Kp),
                mx.repacks_a(M, N, Kp))
         assert got == (tile, S, rp), (M, N, K, got)
+
+
+def test_router_tiny_rule(mx):
+    """The 32 x 32 tile exactly on grids of at most one 32 x 32 block per CU (256 on MI355X) with 3
+    to 12 K-tiles, in ceil(K-tiles / 4) segments of at most four K-tiles; its workspace is the
+    split's (the reference's S * M * N * 4 bytes, which its LDS reduction leaves untouched)."""
+    for M in (1, 32, 96, 128, 256, 300, 512, 1024, 2048):
+        for N in (32, 100, 256, 512, 1024, 4096):
+            for K in (192, 384, 576, 768, 1024, 2048, 2304, 2500, 3072):
+                Kp = _kpad(K)
+                kt = Kp // 192
+                blocks = -(-M // 32) * -(-N // 32)
+                t = tuple(mx.choose_tile(M, N, Kp))
+                S = mx.splitk_segments(M, N, Kp)
+                want = blocks <= 256 and 3 <= kt <= 12
+                assert (t == (32, 32, 1, 1)) == want, (M, N, K, t)
+                if want:
+                    assert S == -(-kt // 4) and -(-kt // S) <= 4, (M, N, K, S)
+                    assert mx.workspace_size(M, N, Kp) == (S * M * N * 4 if S > 1 else 0)
 
 
 def test_router_equals_the_tuning_model(mx):
@@ -243,7 +264,7 @@ def test_router_skinny_m(mx):
     """M a multiple of 32 but not of 128 routes to the 32- or 64-row tiles (one wave row, four
     wave columns); the tile's rows divide M, the split keeps >= 1 K-tile per segment, and the
     workspace is the plan's."""
-    skinny = {(32, 128, 1, 1), (32, 256, 1, 2), (64, 128, 2, 1), (64, 256, 2, 2)}
+    skinny = {(32, 128, 1, 1), (32, 256, 1, 2), (64, 128, 2, 1), (64, 256, 2, 2)} | TINY
     for M in (32, 64, 96, 160, 224, 480, 1056):
         for N in (128, 256, 384, 4096, 8192):
             for K in (192, 1024, 8192, 105728):
@@ -275,7 +296,7 @@ def test_router_ragged_shapes(mx):
                 t = tuple(mx.choose_tile(M, N, Kp))
                 S = mx.splitk_segments(M, N, Kp)
                 rp = mx.repacks_a(M, N, Kp)
-                assert t in IMPLEMENTED | SKINNY, (M, N, K, t)
+                assert t in IMPLEMENTED | SKINNY | TINY, (M, N, K, t)
                 assert 1 <= S <= min(16, Kp // 192)
                 tile, S2, rp2 = plan_model.best_plan(c, M, N, Kp)
                 assert (tile, S2, rp2) == (t, S, bool(rp)), (M, N, K)
