@@ -107,7 +107,8 @@ int mxfp6_gemm_noalloc_async(int out_type, int M, int N, int Kp, const void* dA,
 /* gemm_force_tile: run the tile {MT, NT, MPW, NPW} given by the caller instead of the router's
  * choice, unsplit. Test-only in the reference (src/gemm.cpp:85-107, not in its header); the
  * scales must be tiled with this tile's MPW/NPW. Rejects tiles the library does not implement
- * and tiles that do not divide M x N (mxfp6_gemm_explicit runs those masked). */
+ * and tiles that do not divide M x N (mxfp6_gemm_explicit runs those masked), and the 32 x 32
+ * tile past four K-tiles (its unsplit limit). */
 int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4], const void* dA,
                           const void* dBsh, const uint8_t* dsA, const uint8_t* dsB, void* dD,
                           int A_row_bytes, int B_row_bytes, void* stream);
@@ -118,7 +119,9 @@ int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4],
  * layout (mxfp6_preshuffle_rows_async output; A_row_bytes is then only checked); 3 = row-major A
  * as 0, staged in LDS in 12-byte units whose slots are swizzled per row (operand reads free of
  * bank conflicts; the four wide tiles only, dividing M x N, else MXFP6_ERR_ARG; same output bits
- * as 0; never routed: measured no faster). Needs ws of
+ * as 0; never routed: measured no faster). The tile {32, 32, 1, 1} splits K over a workgroup's
+ * waves (small grids): row-major A, at most 4 segments of at most 4 K-tiles, else MXFP6_ERR_ARG;
+ * the same bits as the other split plans of that grouping. Needs ws of
  * mxfp6_plan_workspace_size(M, N, Kp, splits, a_layout == 1) bytes. For tuning, benchmarks and
  * callers that keep A preshuffled; the scales must be tiled with this tile's MPW/NPW. No
  * counterpart in the reference (it is the reference's gemm_force_tile, src/gemm.cpp:89-107, plus a
@@ -134,9 +137,9 @@ int mxfp6_gemm_repacks_a(int M, int N, int Kp);
 
 /* Measured plan selection. No counterpart in the reference (its router is a fixed rule).
  *
- * mxfp6_gemm_tune times up to `candidates` of the router's best-predicted plans for (out_type, M,
- * N, Kp) -- those with choose_tile's scale grouping (the operands' scales are tiled for it) whose
- * workspace fits ws_bytes -- on the caller's operands (D is overwritten), and keeps the fastest for
+ * mxfp6_gemm_tune times up to `candidates` plans for (out_type, M, N, Kp) -- the routed plan
+ * first, then the router's best-predicted ones with choose_tile's scale grouping (the operands'
+ * scales are tiled for it), each whose workspace fits ws_bytes -- on the caller's operands (D is overwritten), and keeps the fastest for
  * the process: later gemm() calls of the shape and output type run it whenever their workspace
  * holds it (else the router's plan). It waits for `stream`, so it must not be called during graph
  * capture. The chosen plan is returned in tile, *splits and *a_repack (each may be NULL). A
