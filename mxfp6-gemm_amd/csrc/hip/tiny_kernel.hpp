@@ -3,20 +3,22 @@
 // TINY_MAX_KT K-tiles per segment) as one MFMA accumulation from zero in K order, with every
 // A, B and scale load of its segment issued before its first MFMA (the operands of up to 12
 // slabs held in registers: one memory latency per call instead of one per K slab); the S
-// partial blocks then meet in LDS and wave 0 sums them in segment order from zero,
-// ((0 + P0) + P1) + ..., as the split-K reduce does (reduce_kernel.hpp), and stores D. The output
+// partial blocks then meet in LDS and the four waves sum them, a quarter of the block each, in
+// segment order from zero, ((0 + P0) + P1) + ..., as the split-K reduce does (reduce_kernel.hpp),
+// and store D. The output
 // therefore has the bits of any S-segment split plan with a 1 x 1 scale grouping, with no
 // workspace and no second launch.
 // For grids of a few dozen blocks and short K (the latency floor: 256 x 256 x 1024 runs on 64 of
 // the 256 CUs), where a pipelined tile spends its time on per-slab copy issue and barriers.
-// A is row-major (a lane reads its row's 24 bytes of a slab as three 8-byte loads), B
+// A is row-major (a lane reads its row's 24 bytes of a slab as a 16- and an 8-byte load at
+// 8-byte alignment, as the direct kernel's compiled loads do), B
 // preshuffled, scales tiled with groups of one 32-block. MASK: the last block row / column
-// clamps its A row and masks its stores (the layouts hold whole 32-blocks).
+// clamps its A row and masks its stores (the layouts hold whole 32-blocks). The conversion to
+// FP16 / BF16 is cvt_out's round to nearest-even, the split-K reduce's.
 #pragma once
 
 #include "../hip_layer.h"
 #include "device_common.hpp"
-#include "epilogue.hpp"
 #include "lds_dma.hpp"
 
 namespace mxfp6_dev {
@@ -59,13 +61,10 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
             for (int s = 0; s < SUBS; s++) {
                 const int ka = kt * (SUBS * SLAB_BYTES);
-                const v2i x0 = __builtin_bit_cast(
-                    v2i, __builtin_amdgcn_raw_buffer_load_b64(a_rs, v_a + s * SLAB_BYTES, ka, 0));
-                const v2i x1 = __builtin_bit_cast(
-                    v2i, __builtin_amdgcn_raw_buffer_load_b64(a_rs, v_a + s * SLAB_BYTES + 8, ka, 0));
+                const v4i x01 = __builtin_bit_cast(
+                    v4i, __builtin_amdgcn_raw_buffer_load_b128(a_rs, v_a + s * SLAB_BYTES, ka, 0));
                 const v2i x2 = __builtin_bit_cast(
                     v2i, __builtin_amdgcn_raw_buffer_load_b64(a_rs, v_a + s * SLAB_BYTES + 16, ka, 0));
-                const v4i x01 = __builtin_shufflevector(x0, x1, 0, 1, 2, 3);
                 const v4i x2w = __builtin_shufflevector(x2, x2, 0, 1, -1, -1);
                 RA[c][s] = __builtin_shufflevector(x01, x2w, 0, 1, 2, 3, 4, 5, -1, -1);
                 const int kb = kt * (SUBS * OPBLK_BYTES);
@@ -90,16 +89,18 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int e = 0; e < 16; e++) part[wave][e][lane] = acc[e];
     __syncthreads();
-    if (wave != 0) return;
-    v16f r[1][1];
+    // the sums and stores split over the four waves: wave w takes elements 4 w .. 4 w + 3 of each
+    // lane (rows 8 w + 4 (l / 32) + r, r < 4, column l % 32 of the block); one wave storing all
+    // sixteen took 2.1 us of a 4.2 us workgroup at 256 x 256 x 1024, four take about a quarter
+    const int col = nb * 32 + (lane & 31);
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
+    for (int r = 0; r < 4; r++) {
+        const int e = 4 * wave + r;
         float x = 0.f;
         for (int w = 0; w < S; w++) x += part[w][e][lane];
-        r[0][0][e] = x;
+        const int row = mb * 32 + 8 * wave + 4 * (lane >> 5) + r;
+        if (!MASK || (row < M && col < N)) D[(size_t)row * N + col] = cvt_out<OutT>(x);
     }
-    store_tile<1, 1, OutT, false, MASK>(r, D, nullptr, M, N, mb * 32 + 4 * (lane >> 5),
-                                        nb * 32 + (lane & 31), lane, 0);
 }
 
 // One launch: grid ceil(M/32) x ceil(N/32), 256 threads; d->splits segments (1 to 4, each at

@@ -173,13 +173,15 @@ void visit_plans(int M, int N, int Kp, F&& f) {
 }
 
 // The 32 x 32 tile (tiny_kernel.hpp): K split over a workgroup's four waves, every operand loaded
-// before the first MFMA, the segments summed in LDS. Routed by a measured rule ahead of the model,
-// which has no term for it: at most one 32 x 32 block per CU and 3 to 12 K-tiles, in the fewest
-// segments of at most four K-tiles (fewer segments measured faster: 256 x 256 x 1024 5.1, 5.6 and
-// 6.1 us in 2, 3 and 4). Against the routed pipelined plans on 16 shapes of that range: 6-28%
-// faster (256 x 256 x 1024 6.09 -> 5.13 us, 256 x 256 x 768 5.17 -> 3.94, 512 x 256 x 1536 7.81 ->
-// 5.64, 256 x 1024 x 2048 9.01 -> 6.92); slower below 3 K-tiles (2-3%), on part of the shapes
-// with 13-16 (up to 4%), and on grids of two blocks per CU (1024 x 512 x 1024 6.38 -> 6.70).
+// before the first MFMA, the segments summed and stored by all four waves. Routed by a measured
+// rule ahead of the model, which has no term for it: grids that fit the chip in one round (two
+// workgroups per CU: 176 VGPRs a lane leave room for two waves per SIMD) and 2 to 16 K-tiles, in
+// the fewest segments of at most four K-tiles. Against the routed pipelined plans on 26 shapes of
+// that range: 3-36% faster (256 x 256 x 1024 6.09 -> 3.88 us, 256 x 256 x 384 4.17 -> 3.73,
+// 256 x 256 x 3072 8.22 -> 6.30, 1024 x 512 x 1024 6.34 -> 5.42, 1024 x 512 x 3072 12.59 ->
+// 10.12); slower with one K-tile (3.69 -> 3.77) and on grids of three blocks per CU, which take a
+// second round (1536 x 512 x 1024 6.41 -> 7.29). Fewer segments measured within 3% of the best
+// segment count (256 x 256 x 1024 3.88, 3.99 and 4.09 us in 2, 3 and 4).
 // The 32 x 32 tile splits K over its four waves: at most 4 segments of at most 4 K-tiles, on
 // row-major A (tiny_kernel.hpp).
 bool tiny_plan_ok(const TileChoice& tc, int Kp, int S, int a_layout) {
@@ -197,7 +199,7 @@ bool is_tiny(const TileChoice& tc) {
 bool tiny_routed(int M, int N, int Kp, int cus) {
     const long blocks = (long)((M + 31) / 32) * ((N + 31) / 32);
     const int kt = Kp / K_TILE;
-    return blocks <= cus && kt >= 3 && kt <= 12;
+    return blocks <= 2L * cus && kt >= 2 && kt <= 16;
 }
 
 Plan best_plan(int M, int N, int Kp, int cus) {

@@ -22,7 +22,7 @@ SPLIT_CHOICES = (1, 2, 3, 4, 6, 8, 12, 16)
 TILES = [(256, 256, 4, 4), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2), (128, 512, 4, 4),
          (128, 256, 4, 2), (256, 256, 4, 2)]
 # the 32 x 32 tile (tiny_kernel.hpp): routed by a measured rule ahead of the model (plan.cpp
-# tiny_routed): at most one 32 x 32 block per CU and 3 to 12 K-tiles, in ceil(K-tiles / 4) segments
+# tiny_routed): at most two 32 x 32 blocks per CU and 2 to 16 K-tiles, in ceil(K-tiles / 4) segments
 TINY = (32, 32, 1, 1)
 # the tiles whose B goes straight to registers (wide_kernel.hpp)
 WIDE = {(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4, 2)}
@@ -122,7 +122,7 @@ def _pick(times):
 
 def tiny_routed(M, N, Kp):
     kt = Kp // K_TILE
-    return -(-M // 32) * -(-N // 32) <= CUS and 3 <= kt <= 12
+    return -(-M // 32) * -(-N // 32) <= 2 * CUS and 2 <= kt <= 16
 
 
 def best_plan(c, M, N, Kp):

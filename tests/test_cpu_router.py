@@ -188,10 +188,10 @@ def test_router_small_k_plans(mx):
     (down to the 32- and 64-row tiles) and no extra launch for the repack; the router's model
     reproduces the measured winners."""
     want = {  # (M, N, K): (tile, S, repack) measured fastest
-        (256, 256, 1024): ((32, 32, 1, 1), 2, False),      # 5.4 us vs 6.2 on 32x128 (1, 1)
+        (256, 256, 1024): ((32, 32, 1, 1), 2, False),      # 3.9 us vs 6.2 on 32x128 (1, 1)
         (1024, 1024, 1024): ((32, 128, 1, 1), 1, False),   # 6.7 us vs 7.1
         (2048, 1024, 1024): ((64, 128, 2, 1), 1, False),   # 7.8 us vs 8.2
-        (2048, 256, 2048): ((32, 128, 1, 1), 1, False),    # 8.9 us vs 9.8 (no split)
+        (2048, 256, 2048): ((32, 32, 1, 1), 3, False),     # 7.9 us vs 8.9 on 32x128 (1, 1)
         (2048, 4096, 1024): ((128, 256, 4, 2), 1, False),  # 12.0 us vs 14.4 on 128x256 (2, 4)
         (4096, 2048, 2048): ((128, 256, 4, 2), 1, False),  # 18.9 us vs 20.1 on 128x256 (2, 4)
         (3072, 3072, 3072): ((128, 384, 4, 3), 1, False),  # 25.2 us vs 27.6 on 256x256
@@ -204,18 +204,18 @@ def test_router_small_k_plans(mx):
 
 
 def test_router_tiny_rule(mx):
-    """The 32 x 32 tile exactly on grids of at most one 32 x 32 block per CU (256 on MI355X) with 3
-    to 12 K-tiles, in ceil(K-tiles / 4) segments of at most four K-tiles; its workspace is the
+    """The 32 x 32 tile exactly on grids of at most two 32 x 32 blocks per CU (512 on MI355X) with 2
+    to 16 K-tiles, in ceil(K-tiles / 4) segments of at most four K-tiles; its workspace is the
     split's (the reference's S * M * N * 4 bytes, which its LDS reduction leaves untouched)."""
     for M in (1, 32, 96, 128, 256, 300, 512, 1024, 2048):
         for N in (32, 100, 256, 512, 1024, 4096):
-            for K in (192, 384, 576, 768, 1024, 2048, 2304, 2500, 3072):
+            for K in (192, 384, 576, 768, 1024, 2048, 2304, 2500, 3072, 3264):
                 Kp = _kpad(K)
                 kt = Kp // 192
                 blocks = -(-M // 32) * -(-N // 32)
                 t = tuple(mx.choose_tile(M, N, Kp))
                 S = mx.splitk_segments(M, N, Kp)
-                want = blocks <= 256 and 3 <= kt <= 12
+                want = blocks <= 512 and 2 <= kt <= 16
                 assert (t == (32, 32, 1, 1)) == want, (M, N, K, t)
                 if want:
                     assert S == -(-kt // 4) and -(-kt // S) <= 4, (M, N, K, S)

@@ -45,7 +45,8 @@ def test_small_config_fp32(g, orc):
 @pytest.mark.parametrize("out_type", [0, 1, 2])
 @pytest.mark.parametrize("M,N,K", [(128, 128, 192), (256, 384, 768), (384, 256, 960),
                                    (512, 768, 1152),
-                                   # routed to many short K segments (16, 5, 12 of 1-3 K-tiles)
+                                   # 128x128x4224 and 256x256x4096 routed to many short K
+                                   # segments (16 and 12 of 1-2 K-tiles on the 32x128 tile)
                                    (128, 128, 4224), (512, 512, 2048), (256, 256, 4096)])
 def test_routed_small_shapes(g, orc, out_type, M, N, K):
     p = mx.make_problem(M, N, K, seed=M * 3 + N * 7 + K)
@@ -106,11 +107,12 @@ def test_pipelined_kernel_bitwise_equals_direct(g, tile):
 
 
 def test_pipelined_split_bitwise_equals_direct_split(g):
-    M, N, K = 512, 512, 3072
+    # a shape routed to a split on a pipelined tile (not the 32 x 32 one, tested in test_gpu_tiny)
+    M, N, K = g.routed_shape([(512, 512, 4224), (768, 768, 3072), (1024, 512, 4224)],
+                             lambda t, S, rp: S > 1 and t != (32, 32, 1, 1))
     p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=81), seed=81)
     t = mx.choose_tile(M, N, p.Kp)
     S = mx.splitk_segments(M, N, p.Kp)
-    assert S > 1
     dp = g.DevProblem(p, t)
     Dr = g.run_routed(dp, mx.OUT_F32)
     Dd = g.run_direct(dp, mx.OUT_F32, splits=S)
@@ -142,7 +144,7 @@ SKINNY = [(32, 128, 1, 1), (32, 256, 1, 2), (64, 128, 2, 1), (64, 256, 2, 2)]
                                    (160, 256, 2048), (224, 512, 4096), (32, 4096, 8192)])
 def test_routed_skinny_m(g, orc, out_type, M, N, K):
     """M not a multiple of 128 routes to the 32- and 64-row tiles (the 32 x 32 one among them on
-    grids of at most one 32 x 32 block per CU with 3 to 12 K-tiles); the routed output meets the
+    grids of at most two 32 x 32 blocks per CU with 2 to 16 K-tiles); the routed output meets the
     oracle's bar."""
     p = mx.make_problem(M, N, K, seed=M * 5 + N + K)
     t = mx.choose_tile(M, N, p.Kp)
@@ -309,8 +311,9 @@ def test_compact_and_padded_a_agree(g):
 @pytest.mark.parametrize("pad", [4, 8, 16])
 def test_row_stride_alignments(g, pad):
     """A rows at a stride of packed(Kp) + pad bytes (4-, 8- and 16-byte aligned rows): the
-    row-major path, the repack path (its 4/8/16-byte load variants) and the device preshuffle
-    all give the bits of the padded-row problem."""
+    row-major paths (the routed plan, the plan without a workspace, a pipelined tile), the repack
+    path (its 4/8/16-byte load variants) and the device preshuffle all give the bits of the
+    padded-row problem."""
     import dataclasses
     import torch
     M, N, K = 256, 2048, 992  # Kp 1152; the repack is forced through the explicit plan
@@ -320,14 +323,21 @@ def test_row_stride_alignments(g, pad):
     a.reshape(M, rb)[:, :pp.a_row_bytes] = pp.a_packed[:M * pp.a_row_bytes].reshape(M, -1)
     ps = dataclasses.replace(pp, a_packed=a, a_row_bytes=rb)
     t = mx.choose_tile(M, N, pp.Kp)
-    ref = g.run_routed(g.DevProblem(pp, t), mx.OUT_F32)
-    dps = g.DevProblem(ps, t)
-    for got in (g.run_routed(dps, mx.OUT_F32), g.run_routed(dps, mx.OUT_F32, with_ws=False),
-                g.run_explicit(dps, mx.OUT_F32, a_layout=1)):
-        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    dpp, dps = g.DevProblem(pp, t), g.DevProblem(ps, t)
+    # with a workspace the routed plan; without one (a split plan then runs unsplit) another
+    for with_ws in (True, False):
+        ref = g.run_routed(dpp, mx.OUT_F32, with_ws=with_ws)
+        got = g.run_routed(dps, mx.OUT_F32, with_ws=with_ws)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), with_ws
+    # a pipelined tile, row-major and repacked (the 32 x 32 tile reads row-major A only)
+    tp = (128, 128, 2, 2)
+    ref_p = g.run_explicit(g.DevProblem(pp, tp), mx.OUT_F32)
+    dps_p = g.DevProblem(ps, tp)
+    for a_layout in (0, 1):
+        got = g.run_explicit(dps_p, mx.OUT_F32, a_layout=a_layout)
+        assert np.array_equal(got.view(np.uint32), ref_p.view(np.uint32)), a_layout
     ash_p = torch.empty(M * pp.Kp // 4 * 3, dtype=torch.uint8, device="cuda")
     ash_s = torch.empty_like(ash_p)
-    dpp = g.DevProblem(pp, t)
     assert mx.preshuffle_rows(dpp.a.data_ptr(), pp.a_row_bytes, M, pp.Kp, ash_p.data_ptr()) == 0
     assert mx.preshuffle_rows(dps.a.data_ptr(), rb, M, pp.Kp, ash_s.data_ptr()) == 0
     torch.cuda.synchronize()
