@@ -120,7 +120,7 @@ int mxfp6_gemm_force_tile(int out_type, int M, int N, int Kp, const int tile[4],
  * as 0, staged in LDS in 12-byte units whose slots are swizzled per row (operand reads free of
  * bank conflicts; the four wide tiles only, dividing M x N, else MXFP6_ERR_ARG; same output bits
  * as 0; never routed: measured no faster). The tile {32, 32, 1, 1} splits K over a workgroup's
- * waves (small grids): row-major A, at most 4 segments of at most 4 K-tiles, else MXFP6_ERR_ARG;
+ * waves (small grids): row-major A, at most 16 segments of at most 4 K-tiles, else MXFP6_ERR_ARG;
  * the same bits as the other split plans of that grouping. Needs ws of
  * mxfp6_plan_workspace_size(M, N, Kp, splits, a_layout == 1) bytes. For tuning, benchmarks and
  * callers that keep A preshuffled; the scales must be tiled with this tile's MPW/NPW. No

@@ -1,15 +1,17 @@
 // Tiny-shape kernel of libmxfp6gemm (tile {32, 32, 1, 1}): one workgroup per 32 x 32 block of D,
-// its four waves splitting K. Wave w computes K segment w of S (split_segment, S <= 4, at most
-// TINY_MAX_KT K-tiles per segment) as one MFMA accumulation from zero in K order, with every
-// A, B and scale load of its segment issued before its first MFMA (the operands of up to 12
-// slabs held in registers: one memory latency per call instead of one per K slab); the S
-// partial blocks then meet in LDS and the four waves sum them, a quarter of the block each, in
-// segment order from zero, ((0 + P0) + P1) + ..., as the split-K reduce does (reduce_kernel.hpp),
-// and store D. The output
+// its four waves splitting K. The K-tiles form S segments (split_segment, S <= TINY_MAX_SEG, at
+// most TINY_MAX_KT K-tiles each); wave w computes segments w, w + 4, w + 8, ... in turn, each as one
+// MFMA accumulation from zero in K order with every A, B and scale load of the segment issued
+// before its first MFMA (the operands of up to 12 slabs held in registers: one memory latency per
+// segment instead of one per K slab), and leaves each segment's partial block in LDS. The four
+// waves then sum the S partials, a quarter of the block each, in segment order from zero,
+// ((0 + P0) + P1) + ..., as the split-K reduce does (reduce_kernel.hpp), and store D. The output
 // therefore has the bits of any S-segment split plan with a 1 x 1 scale grouping, with no
 // workspace and no second launch.
-// For grids of a few dozen blocks and short K (the latency floor: 256 x 256 x 1024 runs on 64 of
-// the 256 CUs), where a pipelined tile spends its time on per-slab copy issue and barriers.
+// For grids of at most a few hundred blocks (the latency floor: 256 x 256 x 1024 runs on 64 of
+// the 256 CUs), where a pipelined tile spends its time on per-slab copy issue and barriers. Two
+// instantiations: MULTI = false for S <= 4 (one segment per wave, 16 KiB of LDS; 1.5-3% faster
+// than the loop, whose registers it does not need) and MULTI = true for S = 5-16.
 // A is row-major (a lane reads its row's 24 bytes of a slab as a 16- and an 8-byte load at
 // 8-byte alignment, as the direct kernel's compiled loads do), B
 // preshuffled, scales tiled with groups of one 32-block. MASK: the last block row / column
@@ -23,33 +25,15 @@
 
 namespace mxfp6_dev {
 
-constexpr int TINY_MAX_KT = 4;  // K-tiles per segment (operands of 12 slabs in registers)
+constexpr int TINY_MAX_KT = 4;    // K-tiles per segment (operands of 12 slabs in registers)
+constexpr int TINY_MAX_SEG = 16;  // segments per workgroup (their partials: 64 KiB of LDS)
 
-template <typename OutT, bool MASK>
-__global__ void __launch_bounds__(256)
-    tiny_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
-                const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
-                OutT* __restrict__ D, int M, int N, int Kp, int A_row_bytes, int S) {
+// One K segment (K-tiles kt0 .. kt0 + nkt - 1, nkt <= TINY_MAX_KT) of the 32 x 32 block: every
+// load issued, then the MFMAs in K order from zero.
+__device__ __forceinline__ v16f tiny_segment(rsrc_t a_rs, rsrc_t b_rs, rsrc_t sa_rs, rsrc_t sb_rs,
+                                             int v_a, int v_b0, int v_b1, int v_sc, int kt0,
+                                             int nkt) {
     constexpr int MAXKT = TINY_MAX_KT;
-    __shared__ float part[4][16][64];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int mb = blockIdx.x, nb = blockIdx.y;
-    const int k64n = Kp / 64, k_tiles = Kp / 192;
-    int kt0 = 0, nkt = 0;
-    if (wave < S) split_segment(k_tiles, S, wave, kt0, nkt);
-
-    // A: the lane's row (the last valid one past M) and K half; B: block nb; scales: group mb / nb
-    int row = mb * 32 + (lane & 31);
-    if (MASK) row = min(row, M - 1);
-    const rsrc_t a_rs = raw_rsrc(opaque_gptr(A));
-    const int v_a = (int)opaque_v((uint32_t)(row * A_row_bytes + (lane >> 5) * 24));
-    const rsrc_t b_rs = raw_rsrc(opaque_gptr(Bsh + (size_t)nb * k64n * OPBLK_BYTES));
-    const rsrc_t sa_rs = raw_rsrc(opaque_gptr(sA + (size_t)mb * k_tiles * 64 * 12));
-    const rsrc_t sb_rs = raw_rsrc(opaque_gptr(sB + (size_t)nb * k_tiles * 64 * 12));
-    const int v_b0 = (int)opaque_v(16 * lane), v_b1 = (int)opaque_v(1024 + 8 * lane);
-    const int v_sc = (int)opaque_v(12 * lane);
-
     v8i RA[MAXKT][SUBS], RB[MAXKT][SUBS];
     v3i SA[MAXKT], SB[MAXKT];
 #pragma unroll
@@ -86,8 +70,50 @@ __global__ void __launch_bounds__(256)
             acc = mfma_fp6<0, 0>(acc, RA[c][2], RB[c][2], SA[c].z, SB[c].z);
         }
     }
+    return acc;
+}
+
+template <typename OutT, bool MASK, bool MULTI>
+__global__ void __launch_bounds__(256)
+    tiny_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
+                const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
+                OutT* __restrict__ D, int M, int N, int Kp, int A_row_bytes, int S) {
+    __shared__ float part[MULTI ? TINY_MAX_SEG : 4][16][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int mb = blockIdx.x, nb = blockIdx.y;
+    const int k64n = Kp / 64, k_tiles = Kp / 192;
+
+    // A: the block row's 32 rows from a 64-bit base (32-bit offsets then stay within the block
+    // whatever M), the lane's row (the last valid one past M) and K half; B: block nb; scales:
+    // group mb / nb
+    int a_row = lane & 31;
+    if (MASK) a_row = min(a_row, M - 1 - mb * 32);
+    const rsrc_t a_rs = raw_rsrc(opaque_gptr(A + (size_t)mb * 32 * A_row_bytes));
+    const int v_a = (int)opaque_v((uint32_t)(a_row * A_row_bytes + (lane >> 5) * 24));
+    const rsrc_t b_rs = raw_rsrc(opaque_gptr(Bsh + (size_t)nb * k64n * OPBLK_BYTES));
+    const rsrc_t sa_rs = raw_rsrc(opaque_gptr(sA + (size_t)mb * k_tiles * 64 * 12));
+    const rsrc_t sb_rs = raw_rsrc(opaque_gptr(sB + (size_t)nb * k_tiles * 64 * 12));
+    const int v_b0 = (int)opaque_v(16 * lane), v_b1 = (int)opaque_v(1024 + 8 * lane);
+    const int v_sc = (int)opaque_v(12 * lane);
+
+    if constexpr (MULTI) {
+        // wave w: segments w, w + 4, ... in turn, each partial to its own LDS block
+        for (int seg = wave; seg < S; seg += 4) {
+            int kt0, nkt;
+            split_segment(k_tiles, S, seg, kt0, nkt);
+            const v16f acc = tiny_segment(a_rs, b_rs, sa_rs, sb_rs, v_a, v_b0, v_b1, v_sc, kt0, nkt);
 #pragma unroll
-    for (int e = 0; e < 16; e++) part[wave][e][lane] = acc[e];
+            for (int e = 0; e < 16; e++) part[seg][e][lane] = acc[e];
+        }
+    } else {
+        // wave w: segment w (waves past S write a zero block that is never read)
+        int kt0 = 0, nkt = 0;
+        if (wave < S) split_segment(k_tiles, S, wave, kt0, nkt);
+        const v16f acc = tiny_segment(a_rs, b_rs, sa_rs, sb_rs, v_a, v_b0, v_b1, v_sc, kt0, nkt);
+#pragma unroll
+        for (int e = 0; e < 16; e++) part[wave][e][lane] = acc[e];
+    }
     __syncthreads();
     // the sums and stores split over the four waves: wave w takes elements 4 w .. 4 w + 3 of each
     // lane (rows 8 w + 4 (l / 32) + r, r < 4, column l % 32 of the block); one wave storing all
@@ -103,12 +129,13 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// One launch: grid ceil(M/32) x ceil(N/32), 256 threads; d->splits segments (1 to 4, each at
-// most TINY_MAX_KT K-tiles: the host plan guarantees it); row-major A only. Returns 0, or 2.
+// One launch: grid ceil(M/32) x ceil(N/32), 256 threads; d->splits segments (1 to TINY_MAX_SEG,
+// each at most TINY_MAX_KT K-tiles: the host plan guarantees it); row-major A only. Returns 0,
+// or 2.
 template <typename OutT>
 int tiny_launch(const mxfp6_launch_desc* d, hipStream_t st) {
     const int kt = d->Kp / 192;
-    if (d->a_layout != MXFP6_A_ROWS || d->splits < 1 || d->splits > 4 ||
+    if (d->a_layout != MXFP6_A_ROWS || d->splits < 1 || d->splits > TINY_MAX_SEG ||
         (kt + d->splits - 1) / d->splits > TINY_MAX_KT)
         return 2;
     const dim3 grid((unsigned)((d->M + 31) / 32), (unsigned)((d->N + 31) / 32));
@@ -116,11 +143,11 @@ int tiny_launch(const mxfp6_launch_desc* d, hipStream_t st) {
     const uint8_t* A = static_cast<const uint8_t*>(d->A);
     const uint8_t* B = static_cast<const uint8_t*>(d->Bsh);
     OutT* D = static_cast<OutT*>(d->D);
-    const hipError_t e =
-        mask ? launch_kernel(tiny_kernel<OutT, true>, grid, dim3(256), st, A, B, d->sA, d->sB, D,
-                             d->M, d->N, d->Kp, d->A_row_bytes, d->splits)
-             : launch_kernel(tiny_kernel<OutT, false>, grid, dim3(256), st, A, B, d->sA, d->sB, D,
-                             d->M, d->N, d->Kp, d->A_row_bytes, d->splits);
+    const bool multi = d->splits > 4;
+    auto k = multi ? (mask ? tiny_kernel<OutT, true, true> : tiny_kernel<OutT, false, true>)
+                   : (mask ? tiny_kernel<OutT, true, false> : tiny_kernel<OutT, false, false>);
+    const hipError_t e = launch_kernel(k, grid, dim3(256), st, A, B, d->sA, d->sB, D, d->M, d->N,
+                                       d->Kp, d->A_row_bytes, d->splits);
     return e == hipSuccess ? 0 : 2;
 }
 

@@ -175,19 +175,24 @@ void visit_plans(int M, int N, int Kp, F&& f) {
 // The 32 x 32 tile (tiny_kernel.hpp): K split over a workgroup's four waves, every operand loaded
 // before the first MFMA, the segments summed and stored by all four waves. Routed by a measured
 // rule ahead of the model, which has no term for it: grids that fit the chip in one round (two
-// workgroups per CU: 176 VGPRs a lane leave room for two waves per SIMD) and 2 to 16 K-tiles, in
-// the fewest segments of at most four K-tiles. Against the routed pipelined plans on 26 shapes of
-// that range: 3-36% faster (256 x 256 x 1024 6.09 -> 3.88 us, 256 x 256 x 384 4.17 -> 3.73,
-// 256 x 256 x 3072 8.22 -> 6.30, 1024 x 512 x 1024 6.34 -> 5.42, 1024 x 512 x 3072 12.59 ->
-// 10.12); slower with one K-tile (3.69 -> 3.77) and on grids of three blocks per CU, which take a
-// second round (1536 x 512 x 1024 6.41 -> 7.29). Fewer segments measured within 3% of the best
-// segment count (256 x 256 x 1024 3.88, 3.99 and 4.09 us in 2, 3 and 4).
-// The 32 x 32 tile splits K over its four waves: at most 4 segments of at most 4 K-tiles, on
+// workgroups per CU: 176-192 VGPRs a lane leave room for two waves per SIMD) and 2 to 28 K-tiles;
+// up to 16 K-tiles in the fewest segments of at most four K-tiles (one per wave), past that in 8
+// (two per wave in turn). Against the routed pipelined plans on 26 shapes of 2-16 K-tiles: 3-36%
+// faster (256 x 256 x 1024 6.09 -> 3.88 us, 256 x 256 x 384 4.17 -> 3.73, 256 x 256 x 3072 8.22 ->
+// 6.30, 1024 x 512 x 1024 6.34 -> 5.42, 1024 x 512 x 3072 12.59 -> 10.12); slower with one K-tile
+// (3.69 -> 3.77) and on grids of three blocks per CU, which take a second round (1536 x 512 x 1024
+// 6.41 -> 7.29). Fewer segments measured within 3% of the best count (256 x 256 x 1024 3.88, 3.99
+// and 4.09 us in 2, 3 and 4). On 17 shapes of 17-32 K-tiles, 8 segments: up to 28 K-tiles 3-46%
+// faster on 11 of 12 (512 x 512 x 3264 9.88 -> 5.34 us, 512 x 512 x 4096 11.09 -> 7.63, 32 x 4096 x
+// 4096 8.91 -> 7.50, 64 x 2048 x 5376 9.58 -> 7.62; 96 x 4096 x 4096 4% slower), 6 better than 6
+// segments on all six measured; at 32 K-tiles slower on three of five (128 x 128 x 6144 7.09 ->
+// 9.57: a wave's segments in turn each wait a full memory latency).
+// The 32 x 32 tile splits K over its four waves: at most 16 segments of at most 4 K-tiles, on
 // row-major A (tiny_kernel.hpp).
 bool tiny_plan_ok(const TileChoice& tc, int Kp, int S, int a_layout) {
     if (tc.MT != 32 || tc.NT != 32) return true;
     const int kt = Kp / K_TILE;
-    return a_layout == MXFP6_A_ROWS && S >= 1 && S <= 4 && (kt + S - 1) / S <= 4;
+    return a_layout == MXFP6_A_ROWS && S >= 1 && S <= 16 && (kt + S - 1) / S <= 4;
 }
 
 const TileChoice kTiny = {32, 32, 1, 1};
@@ -199,13 +204,18 @@ bool is_tiny(const TileChoice& tc) {
 bool tiny_routed(int M, int N, int Kp, int cus) {
     const long blocks = (long)((M + 31) / 32) * ((N + 31) / 32);
     const int kt = Kp / K_TILE;
-    return blocks <= 2L * cus && kt >= 2 && kt <= 16;
+    return blocks <= 2L * cus && kt >= 2 && kt <= 28;
+}
+
+int tiny_segments(int Kp) {
+    const int kt = Kp / K_TILE;
+    return kt <= 16 ? (kt + 3) / 4 : 8;
 }
 
 Plan best_plan(int M, int N, int Kp, int cus) {
     Plan best = {{128, 128, 2, 2}, 1, false};
     if (!shape_ok(M, N, Kp)) return best;
-    if (tiny_routed(M, N, Kp, cus)) return {kTiny, (Kp / K_TILE + 3) / 4, false};
+    if (tiny_routed(M, N, Kp, cus)) return {kTiny, tiny_segments(Kp), false};
     double best_t = -1.0;
     visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
         const double t = plan_time_us(tc, M, N, Kp, S, rp, cus);

@@ -22,7 +22,8 @@ SPLIT_CHOICES = (1, 2, 3, 4, 6, 8, 12, 16)
 TILES = [(256, 256, 4, 4), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2), (128, 512, 4, 4),
          (128, 256, 4, 2), (256, 256, 4, 2)]
 # the 32 x 32 tile (tiny_kernel.hpp): routed by a measured rule ahead of the model (plan.cpp
-# tiny_routed): at most two 32 x 32 blocks per CU and 2 to 16 K-tiles, in ceil(K-tiles / 4) segments
+# tiny_routed): at most two 32 x 32 blocks per CU and 2 to 28 K-tiles, in ceil(K-tiles / 4) segments
+# up to 16 K-tiles and 8 past that (tiny_segments)
 TINY = (32, 32, 1, 1)
 # the tiles whose B goes straight to registers (wide_kernel.hpp)
 WIDE = {(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4, 2)}
@@ -122,14 +123,19 @@ def _pick(times):
 
 def tiny_routed(M, N, Kp):
     kt = Kp // K_TILE
-    return -(-M // 32) * -(-N // 32) <= 2 * CUS and 2 <= kt <= 16
+    return -(-M // 32) * -(-N // 32) <= 2 * CUS and 2 <= kt <= 28
+
+
+def tiny_segments(Kp):
+    kt = Kp // K_TILE
+    return -(-kt // 4) if kt <= 16 else 8
 
 
 def best_plan(c, M, N, Kp):
     """(tile, S, repack) with the least predicted time, as plan.cpp best_plan (the 32 x 32 tile's
     rule first)."""
     if tiny_routed(M, N, Kp):
-        return (TINY, -(-(Kp // K_TILE) // 4), False)
+        return (TINY, tiny_segments(Kp), False)
     cands = candidates(M, N, Kp)
     if not cands:
         return ((128, 128, 2, 2), 1, False)

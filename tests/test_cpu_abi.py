@@ -73,10 +73,14 @@ def test_argument_checks_reject_before_launch(mx):
                             a_layout=sw) == 5                                        # masked M
     assert mx.gemm_explicit(0, 256, 256, 192, (256, 256, 4, 2), 1, p, p, p, p, p, 144,
                             a_layout=sw + 1) == 5                                    # no layout 4
-    # the 32 x 32 tile: at most 4 segments of at most 4 K-tiles, row-major A
+    # the 32 x 32 tile: at most 16 segments of at most 4 K-tiles, row-major A
     assert mx.gemm_explicit(0, 256, 256, 1152, (32, 32, 1, 1), 1, p, p, p, p, p, 864) == 5  # 6 > 4
     assert mx.gemm_explicit(0, 256, 256, 3456, (32, 32, 1, 1), 4, p, p, p, p, p, 2592,
-                            ws=p, ws_bytes=1 << 30) == 5                             # 18 K-tiles
+                            ws=p, ws_bytes=1 << 30) == 5                             # 18 in 4
+    assert mx.gemm_explicit(0, 256, 256, 12480, (32, 32, 1, 1), 16, p, p, p, p, p, 9360,
+                            ws=p, ws_bytes=1 << 30) == 5                             # 65 in 16
+    assert mx.gemm_explicit(0, 256, 256, 13056, (32, 32, 1, 1), 17, p, p, p, p, p, 9792,
+                            ws=p, ws_bytes=1 << 30) == 5                             # 17 segments
     assert mx.gemm_explicit(0, 256, 256, 576, (32, 32, 1, 1), 1, p, p, p, p, p, 432,
                             a_layout=mx.A_REPACK, ws=p, ws_bytes=1 << 30) == 5       # repack
     assert mx.gemm_force_tile(0, 256, 256, 1152, (32, 32, 1, 1), p, p, p, p, p, 864) == 4

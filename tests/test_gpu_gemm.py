@@ -45,8 +45,8 @@ def test_small_config_fp32(g, orc):
 @pytest.mark.parametrize("out_type", [0, 1, 2])
 @pytest.mark.parametrize("M,N,K", [(128, 128, 192), (256, 384, 768), (384, 256, 960),
                                    (512, 768, 1152),
-                                   # 128x128x4224 and 256x256x4096 routed to many short K
-                                   # segments (16 and 12 of 1-2 K-tiles on the 32x128 tile)
+                                   # 128x128x4224 and 256x256x4096: 22 K-tiles in 8
+                                   # segments of the 32x32 tile, two per wave in turn
                                    (128, 128, 4224), (512, 512, 2048), (256, 256, 4096)])
 def test_routed_small_shapes(g, orc, out_type, M, N, K):
     p = mx.make_problem(M, N, K, seed=M * 3 + N * 7 + K)
