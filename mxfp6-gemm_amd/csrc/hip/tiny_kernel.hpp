@@ -9,9 +9,11 @@
 // therefore has the bits of any S-segment split plan with a 1 x 1 scale grouping, with no
 // workspace and no second launch.
 // For grids of at most a few hundred blocks (the latency floor: 256 x 256 x 1024 runs on 64 of
-// the 256 CUs), where a pipelined tile spends its time on per-slab copy issue and barriers. Two
-// instantiations: MULTI = false for S <= 4 (one segment per wave, 16 KiB of LDS; 1.5-3% faster
-// than the loop, whose registers it does not need) and MULTI = true for S = 5-16.
+// the 256 CUs), where a pipelined tile spends its time on per-slab copy issue and barriers. Three
+// instantiations: MULTI = false for S <= 4 (four waves, one segment each, 16 KiB of LDS; 1.5-3%
+// faster than the loop, whose registers it does not need) and MULTI = true for S = 5-16, with NW = 8
+// waves where the grid leaves one workgroup per CU (twice the loads in flight at the occupancy of
+// two waves per SIMD) and NW = 4 where two workgroups share a CU.
 // A is row-major (a lane reads its row's 24 bytes of a slab as a 16- and an 8-byte load at
 // 8-byte alignment, as the direct kernel's compiled loads do), B
 // preshuffled, scales tiled with groups of one 32-block. MASK: the last block row / column
@@ -73,11 +75,12 @@ __device__ __forceinline__ v16f tiny_segment(rsrc_t a_rs, rsrc_t b_rs, rsrc_t sa
     return acc;
 }
 
-template <typename OutT, bool MASK, bool MULTI>
-__global__ void __launch_bounds__(256)
+template <typename OutT, bool MASK, bool MULTI, int NW>
+__global__ void __launch_bounds__(NW * 64)
     tiny_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bsh,
                 const uint8_t* __restrict__ sA, const uint8_t* __restrict__ sB,
                 OutT* __restrict__ D, int M, int N, int Kp, int A_row_bytes, int S) {
+    static_assert(NW == 4 || (MULTI && NW == 8), "four waves, or eight looping over segments");
     __shared__ float part[MULTI ? TINY_MAX_SEG : 4][16][64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -98,8 +101,8 @@ __global__ void __launch_bounds__(256)
     const int v_sc = (int)opaque_v(12 * lane);
 
     if constexpr (MULTI) {
-        // wave w: segments w, w + 4, ... in turn, each partial to its own LDS block
-        for (int seg = wave; seg < S; seg += 4) {
+        // wave w: segments w, w + NW, ... in turn, each partial to its own LDS block
+        for (int seg = wave; seg < S; seg += NW) {
             int kt0, nkt;
             split_segment(k_tiles, S, seg, kt0, nkt);
             const v16f acc = tiny_segment(a_rs, b_rs, sa_rs, sb_rs, v_a, v_b0, v_b1, v_sc, kt0, nkt);
@@ -115,23 +118,25 @@ __global__ void __launch_bounds__(256)
         for (int e = 0; e < 16; e++) part[wave][e][lane] = acc[e];
     }
     __syncthreads();
-    // the sums and stores split over the four waves: wave w takes elements 4 w .. 4 w + 3 of each
-    // lane (rows 8 w + 4 (l / 32) + r, r < 4, column l % 32 of the block); one wave storing all
-    // sixteen took 2.1 us of a 4.2 us workgroup at 256 x 256 x 1024, four take about a quarter
+    // the sums and stores split over the waves: wave w takes elements EPW w .. EPW w + EPW - 1 of
+    // each lane (element e: row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32 of the block); one
+    // wave storing all sixteen took 2.1 us of a 4.2 us workgroup at 256 x 256 x 1024, four take
+    // about a quarter
+    constexpr int EPW = 16 / NW;
     const int col = nb * 32 + (lane & 31);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int e = 4 * wave + r;
+    for (int r = 0; r < EPW; r++) {
+        const int e = EPW * wave + r;
         float x = 0.f;
         for (int w = 0; w < S; w++) x += part[w][e][lane];
-        const int row = mb * 32 + 8 * wave + 4 * (lane >> 5) + r;
+        const int row = mb * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
         if (!MASK || (row < M && col < N)) D[(size_t)row * N + col] = cvt_out<OutT>(x);
     }
 }
 
-// One launch: grid ceil(M/32) x ceil(N/32), 256 threads; d->splits segments (1 to TINY_MAX_SEG,
-// each at most TINY_MAX_KT K-tiles: the host plan guarantees it); row-major A only. Returns 0,
-// or 2.
+// One launch: grid ceil(M/32) x ceil(N/32), 256 or 512 threads; d->splits segments (1 to
+// TINY_MAX_SEG, each at most TINY_MAX_KT K-tiles: the host plan guarantees it); row-major A only.
+// Returns 0, or 2.
 template <typename OutT>
 int tiny_launch(const mxfp6_launch_desc* d, hipStream_t st) {
     const int kt = d->Kp / 192;
@@ -144,10 +149,13 @@ int tiny_launch(const mxfp6_launch_desc* d, hipStream_t st) {
     const uint8_t* B = static_cast<const uint8_t*>(d->Bsh);
     OutT* D = static_cast<OutT*>(d->D);
     const bool multi = d->splits > 4;
-    auto k = multi ? (mask ? tiny_kernel<OutT, true, true> : tiny_kernel<OutT, false, true>)
-                   : (mask ? tiny_kernel<OutT, true, false> : tiny_kernel<OutT, false, false>);
-    const hipError_t e = launch_kernel(k, grid, dim3(256), st, A, B, d->sA, d->sB, D, d->M, d->N,
-                                       d->Kp, d->A_row_bytes, d->splits);
+    const int cus = mxfp6_hip_device_cus();
+    const bool eight = multi && (long)grid.x * grid.y <= (cus > 0 ? cus : 256);
+    auto k = eight   ? (mask ? tiny_kernel<OutT, true, true, 8> : tiny_kernel<OutT, false, true, 8>)
+             : multi ? (mask ? tiny_kernel<OutT, true, true, 4> : tiny_kernel<OutT, false, true, 4>)
+                     : (mask ? tiny_kernel<OutT, true, false, 4> : tiny_kernel<OutT, false, false, 4>);
+    const hipError_t e = launch_kernel(k, grid, dim3(eight ? 512 : 256), st, A, B, d->sA, d->sB, D,
+                                       d->M, d->N, d->Kp, d->A_row_bytes, d->splits);
     return e == hipSuccess ? 0 : 2;
 }
 

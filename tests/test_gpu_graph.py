@@ -24,6 +24,10 @@ ROUTES = {
                 lambda t, S, rp: S > 1),
     "A repacked": ([(1024, N, K) for K in (16384, 32768) for N in (5120, 8192, 16384)],
                    lambda t, S, rp: rp),
+    # the 32 x 32 tile: K split over each workgroup's waves, one segment per wave and two in turn
+    "32x32 split": ([(256, 256, 1024)], lambda t, S, rp: t == (32, 32, 1, 1) and 1 < S <= 4),
+    "32x32 two segments per wave": ([(512, 512, 4096), (256, 256, 4096)],
+                                    lambda t, S, rp: t == (32, 32, 1, 1) and S > 4),
 }
 REPLAYS = 3
 
