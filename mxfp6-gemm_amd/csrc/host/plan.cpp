@@ -172,21 +172,24 @@ void visit_plans(int M, int N, int Kp, F&& f) {
                 }
 }
 
-// The 32 x 32 tile (tiny_kernel.hpp): K split over a workgroup's four waves, every operand loaded
-// before the first MFMA, the segments summed and stored by all four waves. Routed by a measured
-// rule ahead of the model, which has no term for it: grids that fit the chip in one round (two
-// workgroups per CU: 176-192 VGPRs a lane leave room for two waves per SIMD) and 2 to 28 K-tiles;
-// up to 16 K-tiles in the fewest segments of at most four K-tiles (one per wave), past that in 8
-// (two per wave in turn). Against the routed pipelined plans on 26 shapes of 2-16 K-tiles: 3-36%
-// faster (256 x 256 x 1024 6.09 -> 3.88 us, 256 x 256 x 384 4.17 -> 3.73, 256 x 256 x 3072 8.22 ->
-// 6.30, 1024 x 512 x 1024 6.34 -> 5.42, 1024 x 512 x 3072 12.59 -> 10.12); slower with one K-tile
-// (3.69 -> 3.77) and on grids of three blocks per CU, which take a second round (1536 x 512 x 1024
-// 6.41 -> 7.29). Fewer segments measured within 3% of the best count (256 x 256 x 1024 3.88, 3.99
-// and 4.09 us in 2, 3 and 4). On 17 shapes of 17-32 K-tiles, 8 segments: up to 28 K-tiles 3-46%
-// faster on 11 of 12 (512 x 512 x 3264 9.88 -> 5.34 us, 512 x 512 x 4096 11.09 -> 7.63, 32 x 4096 x
-// 4096 8.91 -> 7.50, 64 x 2048 x 5376 9.58 -> 7.62; 96 x 4096 x 4096 4% slower), 6 better than 6
-// segments on all six measured; at 32 K-tiles slower on three of five (128 x 128 x 6144 7.09 ->
-// 9.57: a wave's segments in turn each wait a full memory latency).
+// The 32 x 32 tile (tiny_kernel.hpp): K split over a workgroup's waves, the segments summed and
+// stored by all of them. Routed by a measured rule ahead of the model, which has no term for it:
+// grids that fit the chip in one round (two four-wave workgroups per CU) with 2 to 28 K-tiles,
+// and on grids of one workgroup per CU (eight waves, A staged) up to 32 K-tiles, up to 64 on
+// those of at least a quarter as many blocks as CUs; up to 16 K-tiles in the fewest segments of
+// at most four K-tiles (one a wave), past that in max(8, ceil(K-tiles / 4)) (A staged through
+// LDS, two segments a wave at most). Against the routed pipelined plans, same sessions: 2-16
+// K-tiles, 26 shapes: 3-36% faster (256 x 256 x 1024 6.09 -> 3.88 us, 256 x 256 x 3072 8.22 ->
+// 6.30, 1024 x 512 x 1024 6.34 -> 5.42); slower with one K-tile (3.69 -> 3.77) and on grids of
+// three blocks per CU, which take a second round (1536 x 512 x 1024 6.41 -> 7.29). 17-28 K-tiles
+// (8 segments): 512 x 512 x 4096 11.09 -> 5.34, 1024 x 512 x 4096 13.65 -> 8.59, 96 x 4096 x 4096
+// 12.55 -> 10.92. 29-32 on one workgroup per CU: 256 x 256 x 6144 8.77 -> 5.84, 128 x 128 x 6144
+// 7.07 -> 5.71, 512 x 512 x 5568 11.54 -> 6.11; on two, mixed (1024 x 512 x 6144 15.16 -> 10.28,
+// 128 x 4096 x 6144 15.06 -> 16.77). 33-64 on 64-256 blocks: 512 x 512 x 8192 13.49 -> 8.05, 64 x
+// 2048 x 8192 10.70 -> 7.83, 32 x 8192 x 12288 19.16 -> 16.56, 256 x 256 x 12288 10.00 -> 9.61;
+// on 16 blocks slower (128 x 128 x 12288 8.36 -> 9.36). Fewer segments up to 16 K-tiles measured
+// within 3% of the best count (256 x 256 x 1024 3.88, 3.99 and 4.09 us in 2, 3 and 4); 8 beat 6
+// on all six 22-K-tile shapes measured, 11 beat 16 at 43 K-tiles on four of four.
 // The 32 x 32 tile splits K over its four waves: at most 16 segments of at most 4 K-tiles, on
 // row-major A (tiny_kernel.hpp).
 bool tiny_plan_ok(const TileChoice& tc, int Kp, int S, int a_layout) {
@@ -204,12 +207,14 @@ bool is_tiny(const TileChoice& tc) {
 bool tiny_routed(int M, int N, int Kp, int cus) {
     const long blocks = (long)((M + 31) / 32) * ((N + 31) / 32);
     const int kt = Kp / K_TILE;
-    return blocks <= 2L * cus && kt >= 2 && kt <= 28;
+    if (blocks > 2L * cus || kt < 2) return false;
+    if (blocks > cus) return kt <= 28;
+    return kt <= 32 || (kt <= 64 && 4 * blocks >= cus);
 }
 
 int tiny_segments(int Kp) {
     const int kt = Kp / K_TILE;
-    return kt <= 16 ? (kt + 3) / 4 : 8;
+    return kt <= 16 ? (kt + 3) / 4 : std::max(8, (kt + 3) / 4);
 }
 
 Plan best_plan(int M, int N, int Kp, int cus) {

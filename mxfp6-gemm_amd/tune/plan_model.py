@@ -22,8 +22,9 @@ SPLIT_CHOICES = (1, 2, 3, 4, 6, 8, 12, 16)
 TILES = [(256, 256, 4, 4), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2), (128, 512, 4, 4),
          (128, 256, 4, 2), (256, 256, 4, 2)]
 # the 32 x 32 tile (tiny_kernel.hpp): routed by a measured rule ahead of the model (plan.cpp
-# tiny_routed): at most two 32 x 32 blocks per CU and 2 to 28 K-tiles, in ceil(K-tiles / 4) segments
-# up to 16 K-tiles and 8 past that (tiny_segments)
+# tiny_routed): at most two 32 x 32 blocks per CU and 2 to 28 K-tiles; on at most one block per CU
+# up to 32, and up to 64 on at least a quarter as many blocks as CUs; in ceil(K-tiles / 4)
+# segments up to 16 K-tiles and max(8, ceil(K-tiles / 4)) past that (tiny_segments)
 TINY = (32, 32, 1, 1)
 # the tiles whose B goes straight to registers (wide_kernel.hpp)
 WIDE = {(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4, 2)}
@@ -123,12 +124,17 @@ def _pick(times):
 
 def tiny_routed(M, N, Kp):
     kt = Kp // K_TILE
-    return -(-M // 32) * -(-N // 32) <= 2 * CUS and 2 <= kt <= 28
+    blocks = -(-M // 32) * -(-N // 32)
+    if blocks > 2 * CUS or kt < 2:
+        return False
+    if blocks > CUS:
+        return kt <= 28
+    return kt <= 32 or (kt <= 64 and 4 * blocks >= CUS)
 
 
 def tiny_segments(Kp):
     kt = Kp // K_TILE
-    return -(-kt // 4) if kt <= 16 else 8
+    return -(-kt // 4) if kt <= 16 else max(8, -(-kt // 4))
 
 
 def best_plan(c, M, N, Kp):

@@ -205,22 +205,26 @@ def test_router_small_k_plans(mx):
 
 def test_router_tiny_rule(mx):
     """The 32 x 32 tile exactly on grids of at most two 32 x 32 blocks per CU (512 on MI355X) with 2
-    to 28 K-tiles, in ceil(K-tiles / 4) segments up to 16 K-tiles and 8 past that (at most four
-    K-tiles each); its workspace is the split's (the reference's S * M * N * 4 bytes, which its
-    LDS reduction leaves untouched)."""
+    to 28 K-tiles, and on grids of at most one block per CU with up to 32 K-tiles, up to 64 from
+    64 blocks on; in ceil(K-tiles / 4) segments up to 16 K-tiles and max(8, ceil(K-tiles / 4))
+    past that (at most four K-tiles each); its workspace is the split's (the reference's
+    S * M * N * 4 bytes, which its LDS reduction leaves untouched)."""
     for M in (1, 32, 96, 128, 256, 300, 512, 1024, 2048):
         for N in (32, 100, 256, 512, 1024, 4096):
             for K in (192, 384, 576, 768, 1024, 2048, 2304, 2500, 3072, 3264, 4224, 5376, 5568,
-                      6144):
+                      6144, 6336, 8192, 12288, 12480):
                 Kp = _kpad(K)
                 kt = Kp // 192
                 blocks = -(-M // 32) * -(-N // 32)
                 t = tuple(mx.choose_tile(M, N, Kp))
                 S = mx.splitk_segments(M, N, Kp)
-                want = blocks <= 512 and 2 <= kt <= 28
+                want = 2 <= kt and (kt <= 28 and blocks <= 512 or
+                                    kt <= 32 and blocks <= 256 or
+                                    kt <= 64 and 64 <= blocks <= 256)
                 assert (t == (32, 32, 1, 1)) == want, (M, N, K, t)
                 if want:
-                    assert S == (-(-kt // 4) if kt <= 16 else 8) and -(-kt // S) <= 4, (M, N, K, S)
+                    assert S == (-(-kt // 4) if kt <= 16 else max(8, -(-kt // 4))), (M, N, K, S)
+                    assert -(-kt // S) <= 4 and S <= 16, (M, N, K, S)
                     assert mx.workspace_size(M, N, Kp) == (S * M * N * 4 if S > 1 else 0)
 
 

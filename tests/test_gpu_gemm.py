@@ -144,8 +144,8 @@ SKINNY = [(32, 128, 1, 1), (32, 256, 1, 2), (64, 128, 2, 1), (64, 256, 2, 2)]
                                    (160, 256, 2048), (224, 512, 4096), (32, 4096, 8192)])
 def test_routed_skinny_m(g, orc, out_type, M, N, K):
     """M not a multiple of 128 routes to the 32- and 64-row tiles (the 32 x 32 one among them on
-    grids of at most two 32 x 32 blocks per CU with 2 to 16 K-tiles); the routed output meets the
-    oracle's bar."""
+    grids of at most two 32 x 32 blocks per CU with up to 28-64 K-tiles, by the grid); the routed
+    output meets the oracle's bar."""
     p = mx.make_problem(M, N, K, seed=M * 5 + N + K)
     t = mx.choose_tile(M, N, p.Kp)
     assert tuple(t) in SKINNY + [(32, 32, 1, 1)]
