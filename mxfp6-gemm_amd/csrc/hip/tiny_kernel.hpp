@@ -10,11 +10,11 @@
 // workspace and no second launch.
 // For grids of at most a few hundred blocks (the latency floor: 256 x 256 x 1024 runs on 64 of
 // the 256 CUs), where a pipelined tile spends its time on per-slab copy issue and barriers. Four
-// instantiations: MULTI = false for S <= 4 (four waves, one segment each, 16 KiB of LDS; 1.5-3%
-// faster than the loop, whose registers it does not need) and MULTI = true for S = 5-16: A staged
-// (below) by NW = 8 waves where the grid leaves one workgroup per CU (twice the loads in flight at
-// the occupancy of two waves per SIMD), by NW = 4 where two workgroups share a CU and S <= 8, and
-// loaded directly by four waves for S = 9-16 there.
+// instantiations: MULTI = false for S <= 4 on the smallest grids (four waves, one segment each, A
+// loaded directly, 16 KiB of LDS) and MULTI = true otherwise: A staged (below) by NW = 8 waves for
+// S > 4 where the grid leaves one workgroup per CU (twice the loads in flight at the occupancy of
+// two waves per SIMD), by NW = 4 for S <= 8 elsewhere, and loaded directly by four waves for
+// S = 9-16 on grids past one workgroup per CU.
 // A is row-major. With one segment per wave a lane reads its row's 24 bytes of a slab as a 16- and
 // an 8-byte load at 8-byte alignment (as the direct kernel's compiled loads do): each load then
 // touches all 32 rows of the block. The looping instantiations, whose waves together load far
@@ -274,13 +274,18 @@ int tiny_launch(const mxfp6_launch_desc* d, hipStream_t st) {
     const uint8_t* A = static_cast<const uint8_t*>(d->A);
     const uint8_t* B = static_cast<const uint8_t*>(d->Bsh);
     OutT* D = static_cast<OutT*>(d->D);
-    // S <= 4: one segment a wave; past that A is staged, by eight waves where the grid leaves
-    // one workgroup per CU (two segments a wave at most), else by four up to S = 8; four waves
-    // with A loaded directly take S = 9-16 on larger grids
+    // S <= 4: one segment a wave, A staged by four waves once the grid's blocks times K-tiles
+    // reach twice the CUs (below that, a few waves a CU with short segments, the direct loads
+    // were 1-5% faster: 256 x 256 x 1024, 256 x 256 x 384; above it staging was 14-34% faster:
+    // 1024 x 512 x 1024, 256 x 256 x 3072, 1024 x 512 x 3072); past four segments A is staged,
+    // by eight waves where the grid leaves one workgroup per CU (two segments a wave at most),
+    // else by four up to S = 8; four waves with A loaded directly take S = 9-16 on larger grids
     const bool multi = d->splits > 4;
-    const int cus = mxfp6_hip_device_cus();
-    const bool eight = multi && (long)grid.x * grid.y <= (cus > 0 ? cus : 256);
-    const bool staged4 = multi && !eight && d->splits <= 8;
+    const int reported = mxfp6_hip_device_cus();
+    const long cus = reported > 0 ? reported : 256;
+    const long blocks = (long)grid.x * grid.y;
+    const bool eight = multi && blocks <= cus;
+    const bool staged4 = multi ? !eight && d->splits <= 8 : blocks * kt >= 2 * cus;
     auto k = eight     ? (mask ? tiny_kernel<OutT, true, true, 8, true> : tiny_kernel<OutT, false, true, 8, true>)
              : staged4 ? (mask ? tiny_kernel<OutT, true, true, 4, true> : tiny_kernel<OutT, false, true, 4, true>)
              : multi   ? (mask ? tiny_kernel<OutT, true, true, 4, false> : tiny_kernel<OutT, false, true, 4, false>)

@@ -35,11 +35,12 @@ def test_tiny_bitwise_equals_direct_split(M, N, K, S):
 
 @pytest.mark.parametrize("M,N,K,S", [(100, 200, 960, 3), (33, 97, 192, 1), (250, 31, 1344, 2),
                                      (1, 1, 3072, 4), (100, 200, 4224, 8), (1000, 300, 4224, 6),
-                                     (1000, 300, 8256, 11)])
+                                     (1000, 300, 8256, 11), (1000, 300, 2112, 3)])
 def test_tiny_ragged_equals_slab_split(M, N, K, S):
     """Ragged shapes (the last block row / column masked) against the 32 x 128 slab tile's split
-    plan with the same segments (the same 1 x 1 grouping, the same sums); past four segments A is
-    staged by eight waves (28 blocks) or four (320 blocks, S = 6), or loaded directly (S = 11)."""
+    plan with the same segments (the same 1 x 1 grouping, the same sums); A loaded directly on the
+    smallest grids and at S = 11 on 320 blocks, staged by eight waves (28 blocks, S = 8) or four
+    (320 blocks, S = 6 and S = 3)."""
     seed = M * 7 + N + K
     p = checks.spread_scales(mx.make_problem(M, N, K, **T3, seed=seed), seed=seed)
     dt = g.DevProblem(p, TINY)
