@@ -177,8 +177,9 @@ void visit_plans(int M, int N, int Kp, F&& f) {
 // grids that fit the chip in one round (two four-wave workgroups per CU) with 2 to 28 K-tiles,
 // and on grids of one workgroup per CU (eight waves, A staged) up to 32 K-tiles, up to 64 on
 // those of at least a quarter as many blocks as CUs; up to 16 K-tiles in the fewest segments of
-// at most four K-tiles (one a wave), past that in max(8, ceil(K-tiles / 4)) (A staged through
-// LDS, two segments a wave at most). Against the routed pipelined plans, same sessions: 2-16
+// at most four K-tiles (one a wave), except 13-16 K-tiles on one workgroup per CU in 8 (eight
+// waves, A staged), and past 16 in max(8, ceil(K-tiles / 4)) (A staged through LDS, two
+// segments a wave at most). Against the routed pipelined plans, same sessions: 2-16
 // K-tiles, 26 shapes: 3-36% faster (256 x 256 x 1024 6.09 -> 3.88 us, 256 x 256 x 3072 8.22 ->
 // 6.30, 1024 x 512 x 1024 6.34 -> 5.42); slower with one K-tile (3.69 -> 3.77) and on grids of
 // three blocks per CU, which take a second round (1536 x 512 x 1024 6.41 -> 7.29). 17-28 K-tiles
@@ -187,9 +188,11 @@ void visit_plans(int M, int N, int Kp, F&& f) {
 // 7.07 -> 5.71, 512 x 512 x 5568 11.54 -> 6.11; on two, mixed (1024 x 512 x 6144 15.16 -> 10.28,
 // 128 x 4096 x 6144 15.06 -> 16.77). 33-64 on 64-256 blocks: 512 x 512 x 8192 13.49 -> 8.05, 64 x
 // 2048 x 8192 10.70 -> 7.83, 32 x 8192 x 12288 19.16 -> 16.56, 256 x 256 x 12288 10.00 -> 9.61;
-// on 16 blocks slower (128 x 128 x 12288 8.36 -> 9.36). Fewer segments up to 16 K-tiles measured
-// within 3% of the best count (256 x 256 x 1024 3.88, 3.99 and 4.09 us in 2, 3 and 4); 8 beat 6
-// on all six 22-K-tile shapes measured, 11 beat 16 at 43 K-tiles on four of four.
+// on 16 blocks slower (128 x 128 x 12288 8.36 -> 9.36). The fewest segments measured best or
+// within 3% up to 12 K-tiles (256 x 256 x 1024 3.88, 3.99 and 4.09 us in 2, 3 and 4; 6 and 8
+// segments 1-7% slower on 8-12 K-tiles but for one 16-block grid); 8 beat 4 at 13-16 K-tiles on
+// all nine grids of 4-256 blocks measured (64 x 64 x 3072 5.95 -> 4.42 us, 256 x 256 x 3072 4.92 ->
+// 4.76); 8 beat 6 on all six 22-K-tile shapes, 11 beat 16 at 43 K-tiles on four of four.
 // The 32 x 32 tile splits K over its four waves: at most 16 segments of at most 4 K-tiles, on
 // row-major A (tiny_kernel.hpp).
 bool tiny_plan_ok(const TileChoice& tc, int Kp, int S, int a_layout) {
@@ -212,15 +215,17 @@ bool tiny_routed(int M, int N, int Kp, int cus) {
     return kt <= 32 || (kt <= 64 && 4 * blocks >= cus);
 }
 
-int tiny_segments(int Kp) {
+int tiny_segments(int M, int N, int Kp, int cus) {
+    const long blocks = (long)((M + 31) / 32) * ((N + 31) / 32);
     const int kt = Kp / K_TILE;
-    return kt <= 16 ? (kt + 3) / 4 : std::max(8, (kt + 3) / 4);
+    if (kt > 16) return std::max(8, (kt + 3) / 4);
+    return kt > 12 && blocks <= cus ? 8 : (kt + 3) / 4;
 }
 
 Plan best_plan(int M, int N, int Kp, int cus) {
     Plan best = {{128, 128, 2, 2}, 1, false};
     if (!shape_ok(M, N, Kp)) return best;
-    if (tiny_routed(M, N, Kp, cus)) return {kTiny, tiny_segments(Kp), false};
+    if (tiny_routed(M, N, Kp, cus)) return {kTiny, tiny_segments(M, N, Kp, cus), false};
     double best_t = -1.0;
     visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
         const double t = plan_time_us(tc, M, N, Kp, S, rp, cus);

@@ -24,7 +24,8 @@ TILES = [(256, 256, 4, 4), (128, 384, 4, 3), (128, 256, 2, 4), (128, 128, 2, 2),
 # the 32 x 32 tile (tiny_kernel.hpp): routed by a measured rule ahead of the model (plan.cpp
 # tiny_routed): at most two 32 x 32 blocks per CU and 2 to 28 K-tiles; on at most one block per CU
 # up to 32, and up to 64 on at least a quarter as many blocks as CUs; in ceil(K-tiles / 4)
-# segments up to 16 K-tiles and max(8, ceil(K-tiles / 4)) past that (tiny_segments)
+# segments up to 16 K-tiles (8 at 13-16 on at most one block per CU) and max(8, ceil(K-tiles / 4))
+# past that (tiny_segments)
 TINY = (32, 32, 1, 1)
 # the tiles whose B goes straight to registers (wide_kernel.hpp)
 WIDE = {(128, 512, 4, 4), (128, 384, 4, 3), (128, 256, 4, 2), (256, 256, 4, 2)}
@@ -132,16 +133,18 @@ def tiny_routed(M, N, Kp):
     return kt <= 32 or (kt <= 64 and 4 * blocks >= CUS)
 
 
-def tiny_segments(Kp):
+def tiny_segments(M, N, Kp):
     kt = Kp // K_TILE
-    return -(-kt // 4) if kt <= 16 else max(8, -(-kt // 4))
+    if kt > 16:
+        return max(8, -(-kt // 4))
+    return 8 if kt > 12 and -(-M // 32) * -(-N // 32) <= CUS else -(-kt // 4)
 
 
 def best_plan(c, M, N, Kp):
     """(tile, S, repack) with the least predicted time, as plan.cpp best_plan (the 32 x 32 tile's
     rule first)."""
     if tiny_routed(M, N, Kp):
-        return (TINY, tiny_segments(Kp), False)
+        return (TINY, tiny_segments(M, N, Kp), False)
     cands = candidates(M, N, Kp)
     if not cands:
         return ((128, 128, 2, 2), 1, False)

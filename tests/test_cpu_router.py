@@ -206,8 +206,9 @@ def test_router_small_k_plans(mx):
 def test_router_tiny_rule(mx):
     """The 32 x 32 tile exactly on grids of at most two 32 x 32 blocks per CU (512 on MI355X) with 2
     to 28 K-tiles, and on grids of at most one block per CU with up to 32 K-tiles, up to 64 from
-    64 blocks on; in ceil(K-tiles / 4) segments up to 16 K-tiles and max(8, ceil(K-tiles / 4))
-    past that (at most four K-tiles each); its workspace is the split's (the reference's
+    64 blocks on; in ceil(K-tiles / 4) segments up to 16 K-tiles (8 at 13-16 on at most 256
+    blocks) and max(8, ceil(K-tiles / 4)) past that (at most four K-tiles each); its workspace
+    is the split's (the reference's
     S * M * N * 4 bytes, which its LDS reduction leaves untouched)."""
     for M in (1, 32, 96, 128, 256, 300, 512, 1024, 2048):
         for N in (32, 100, 256, 512, 1024, 4096):
@@ -223,7 +224,9 @@ def test_router_tiny_rule(mx):
                                     kt <= 64 and 64 <= blocks <= 256)
                 assert (t == (32, 32, 1, 1)) == want, (M, N, K, t)
                 if want:
-                    assert S == (-(-kt // 4) if kt <= 16 else max(8, -(-kt // 4))), (M, N, K, S)
+                    want_S = (max(8, -(-kt // 4)) if kt > 16 else
+                              8 if kt > 12 and blocks <= 256 else -(-kt // 4))
+                    assert S == want_S, (M, N, K, S)
                     assert -(-kt // S) <= 4 and S <= 16, (M, N, K, S)
                     assert mx.workspace_size(M, N, Kp) == (S * M * N * 4 if S > 1 else 0)
 
@@ -232,7 +235,10 @@ def test_router_equals_the_tuning_model(mx):
     """The Python model in mxfp6-gemm_amd/tune (the one the constants are fitted with) and the
     library's router make the same choice on every shape of the recorded plan measurements and
     on a grid of other shapes; and with the committed constants every pick was measured and the
-    picks are within 3% of the measured best on average."""
+    model's picks are within 3% of the measured best on average. The shapes the 32 x 32 tile's
+    measured rule takes are not the model's (the fit leaves them out too): their plans run in
+    about 5 us, where the sweep's back-to-back launches from an idle queue rank segment counts
+    differently from the queue-primed A/B runs that set the rule."""
     import math
     import os
     import sys
@@ -250,6 +256,7 @@ def test_router_equals_the_tuning_model(mx):
         assert got == (tile, S, rp), (M, N, K, got, (tile, S, rp))
     ev = pm.evaluate(pm.CONSTANTS, recs)
     assert all(g == g for _, g in ev), [s for s, g in ev if g != g]
+    ev = [(s, g) for s, g in ev if not pm.tiny_routed(s[0], s[1], _kpad(s[2]))]
     big = [g for s, g in ev if s[0] % 128 == 0 and s[1] % 128 == 0]
     skinny = [g for s, g in ev if s[0] % 128 != 0 and s[0] % 32 == 0 and s[1] % 128 == 0]
     ragged = [g for s, g in ev if s[0] % 32 != 0 or s[1] % 128 != 0]
@@ -257,7 +264,7 @@ def test_router_equals_the_tuning_model(mx):
               if M % 32 == 0 and N % 128 == 0 and N % pm.best_plan(
                   pm.CONSTANTS, M, N, _kpad(K))[0][1] != 0]
     gm = math.exp(sum(math.log(g) for g in big) / len(big))
-    assert len(big) >= 60 and gm < 1.03, (len(big), gm)
+    assert len(big) >= 50 and gm < 1.03, (len(big), gm)
     # N-masked picks on regular shapes are among them (the reference's NMASK route)
     assert len(masked) >= 5
     # the skinny-M and the ragged shapes use the same constants (fitted on M % 128 == 0):

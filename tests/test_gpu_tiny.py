@@ -18,8 +18,8 @@ T3 = {"dist_a": mx.DIST_STUDENT_T3, "dist_b": mx.DIST_STUDENT_T3}
 
 @pytest.mark.parametrize("M,N", [(256, 256), (64, 512), (512, 128), (2048, 1024)])
 @pytest.mark.parametrize("K,S", [(192, 1), (384, 2), (576, 3), (768, 4), (1152, 4), (1344, 2),
-                                 (2112, 3), (3072, 4), (768, 1), (4224, 6), (4224, 8),
-                                 (8256, 11), (8256, 16), (12288, 16)])
+                                 (2112, 3), (3072, 4), (768, 1), (3072, 8), (4224, 6),
+                                 (4224, 8), (8256, 11), (8256, 16), (12288, 16)])
 def test_tiny_bitwise_equals_direct_split(M, N, K, S):
     """K-tile counts 1 to 64 in 1 to 16 segments of at most four K-tiles (segments of uneven
     length among them: 7 in 2, 11 in 3, 22 in 6, 43 in 11; past four segments a wave computes
