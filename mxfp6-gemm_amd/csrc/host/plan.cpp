@@ -532,8 +532,19 @@ int tune(int out_type, int M, int N, int Kp, const void* dA, const void* dBsh, c
         Plan plan;
     };
     std::vector<Ranked> ranked;
-    // the routed plan is always measured (the 32 x 32 tile is not among the model's plans)
+    // the routed plan is always measured (the 32 x 32 tile is not among the model's plans), and
+    // for the 32 x 32 tile the nearest valid segment counts below and above the routed one next
+    // (their times are within a few percent of each other, in an order that varies by box)
     if (plan_fits(M, N, Kp, routed.S, routed.repack, ws_bytes)) ranked.push_back({-1.0, routed});
+    if (is_tiny(routed.tc)) {
+        for (int dir = -1; dir <= 1; dir += 2)
+            for (int S = routed.S + dir; S >= 1 && S <= 16; S += dir)
+                if (tiny_plan_ok(routed.tc, Kp, S, MXFP6_A_ROWS)) {
+                    if (plan_fits(M, N, Kp, S, false, ws_bytes))
+                        ranked.push_back({-0.5, {routed.tc, S, false}});
+                    break;
+                }
+    }
     visit_plans(M, N, Kp, [&](const TileChoice& tc, int S, bool rp) {
         if (tc.MT == routed.tc.MT && tc.NT == routed.tc.NT && S == routed.S && rp == routed.repack)
             return;

@@ -41,7 +41,7 @@ def _gemm(dp, ot, ws_bytes):
 
 
 @pytest.mark.parametrize("M,N,K", [(8192, 1024, 16384), (1536, 1536, 5120), (1024, 4096, 1024),
-                                   (512, 2048, 8192)])
+                                   (512, 2048, 8192), (256, 256, 1024), (256, 256, 4096)])
 def test_tuned_plan_is_used_and_correct(orc, M, N, K):
     ot = mx.OUT_F16
     p = mx.make_problem(M, N, K, seed=M + 3 * N + 5 * K)
