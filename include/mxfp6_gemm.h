@@ -138,8 +138,10 @@ int mxfp6_gemm_repacks_a(int M, int N, int Kp);
 /* Measured plan selection. No counterpart in the reference (its router is a fixed rule).
  *
  * mxfp6_gemm_tune times up to `candidates` plans for (out_type, M, N, Kp) -- the routed plan
- * first, then the router's best-predicted ones with choose_tile's scale grouping (the operands'
- * scales are tiled for it), each whose workspace fits ws_bytes -- on the caller's operands (D is overwritten), and keeps the fastest for
+ * first (where it is the 32 x 32 tile, then that tile at the nearest valid segment counts below
+ * and above), then the router's best-predicted ones with choose_tile's scale grouping (the
+ * operands' scales are tiled for it), each whose workspace fits ws_bytes -- on the caller's
+ * operands (D is overwritten), and keeps the fastest for
  * the process: later gemm() calls of the shape and output type run it whenever their workspace
  * holds it (else the router's plan). It waits for `stream`, so it must not be called during graph
  * capture. The chosen plan is returned in tile, *splits and *a_repack (each may be NULL). A
