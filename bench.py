@@ -24,9 +24,10 @@ drawn from N(0,1) with the seeded PCG32 generator and quantised with the OCP MX 
                                out; R > 1: R more runs per library, alternating their order)
 
 Prints one JSON line per workload (only the default one unless --all). The headline `value` is
-the mean over exactly K timed steps after W warm-up steps (no extra warm-up: an idle MI355X sits
-in deep sleep near 160 MHz, so a short warm-up leaves part of the clock ramp inside the timed
-loop; `sclk_mhz` reports the clock the loop ran at). Besides the contract fields it reports:
+the mean over exactly K timed steps after W warm-up steps. The per_config comparisons (below) run
+before it, on the GPU only, so its W warm-ups follow seconds of GEMMs rather than an idle MI355X
+near 160 MHz, whose clock would still be ramping through a short timed loop; the CPU baselines
+run after it. `sclk_mhz` reports the clock the loop ran at. Besides the contract fields it reports:
   sclk_mhz      the mean graphics clock over the timed loop (each XCD's shader cycle counter
                 against the 100 MHz reference counter, read by the library's clock sample just
                 before and just after the loop, outside its events; mean over the XCDs), and
@@ -42,7 +43,8 @@ loop; `sclk_mhz` reports the clock the loop ran at). Besides the contract fields
   vs_baseline   value / the reference GPU library's TFLOPs on the same operands in this process
                 (oracle/_ref/libmxfp6ref.so, built from the reference's own sources; its own
                 router and workspace), timed by the reference's method (tests/test_gemm.cpp:33-55:
-                8 warm-ups, best mean of 4 x 20 back-to-back launches) after the headline loop;
+                8 warm-ups, best mean of 4 x 20 back-to-back launches) after the headline loop
+                (and again, with the other workloads, in per_config before it);
   per_config    the five workloads, this library and the reference library each timed by that
                 same method on identical operands: TFLOPs, fraction of 10.1 PF, ratio, and for the
                 split-K workload the algorithmic HBM GB/s;
@@ -362,11 +364,13 @@ def compare(w, stream):
     return out
 
 
-def headline(name, steps, warmup, ref):
+def headline(name, steps, warmup, ref, w=None):
     """The contract measurement of one workload: `warmup` untimed steps, then exactly `steps`
-    steps between two synchronisations; then the dominant kernel timed alone."""
+    steps between two synchronisations; then the dominant kernel timed alone. w: the workload's
+    operands when already on the device."""
     import torch
-    w = Workload(name, ref)
+    if w is None:
+        w = Workload(name, ref)
     M, N, K, p = w.M, w.N, w.K, w.p
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
@@ -465,8 +469,23 @@ def run(names, steps, warmup, with_cpu, with_ref, per_config):
     ref = reference_library() if with_ref else None
     lines = []
     cpu_done = {}
+    # The per-workload comparisons (GPU launches only) run before the headline, its operands
+    # already on the device, so the headline's warm-up and timed steps follow seconds of GEMMs
+    # instead of an idle GPU near 160 MHz; the CPU baselines run last.
+    pc, probs, ready = {}, {}, {}
+    if per_config:
+        # the headline's own workload last: the timed loop then follows the same GEMM (after a
+        # different one, the 20-step loop ran at 1356 MHz against 1496 in that comparison)
+        ready[names[0]] = Workload(names[0], ref)
+        for n in sorted(CONFIGS, key=lambda c: (c == names[0], c)):
+            w = ready[n] if n in ready else Workload(n, ref)
+            pc[n] = compare(w, torch.cuda.current_stream())
+            probs[n] = w.p
+            if n not in ready:
+                del w
+                torch.cuda.empty_cache()
     for n in names:
-        w, out = headline(n, steps, warmup, ref)
+        w, out = headline(n, steps, warmup, ref, ready.pop(n, None))
         if ref is not None:
             c = compare(w, torch.cuda.current_stream())
             out["vs_baseline"] = round(out["value"] / c["ref_tflops"], 3)
@@ -476,28 +495,23 @@ def run(names, steps, warmup, with_cpu, with_ref, per_config):
                         "(8 warm-ups, best mean of 4 x 20 launches)",
                 "value": c["ref_tflops"], "unit": "TFLOP/s", "tile": c["ref_tile"],
                 "ours_same_method_tflops": c["tflops"], "ratio_same_method": c["ratio"]}
-        if with_cpu and n == names[0]:
-            log(f"[bench] {n}: CPU baseline ...")
-            out["cpu_baseline"] = cpu_baseline(w.p)
-            cpu_done[n] = out["cpu_baseline"]
+        probs.setdefault(n, w.p)
         lines.append((w, out))
         del w
         torch.cuda.empty_cache()
+    if with_cpu:
+        log(f"[bench] {names[0]}: CPU baseline ...")
+        lines[0][1]["cpu_baseline"] = cpu_done[names[0]] = cpu_baseline(probs[names[0]])
     if per_config:
-        pc = {}
         for n in sorted(CONFIGS):
-            w = Workload(n, ref)
-            pc[n] = compare(w, torch.cuda.current_stream())
             if with_cpu:
                 # every workload beside the reference CPU path (the headline's own sample where
                 # it was just taken; the small workload runs in full)
                 if n not in cpu_done:
                     log(f"[bench] {n}: CPU baseline ...")
-                    cpu_done[n] = cpu_baseline(w.p)
+                    cpu_done[n] = cpu_baseline(probs[n])
                 pc[n]["cpu_baseline"] = cpu_done[n]
-            del w
-            torch.cuda.empty_cache()
-        lines[0][1]["per_config"] = pc
+        lines[0][1]["per_config"] = {n: pc[n] for n in sorted(pc)}
     for _, out in lines:
         print(json.dumps(out), flush=True)
 
