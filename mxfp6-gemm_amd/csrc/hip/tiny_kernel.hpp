@@ -1,29 +1,28 @@
 // Tiny-shape kernel of libmxfp6gemm (tile {32, 32, 1, 1}): one workgroup per 32 x 32 block of D,
-// its four waves splitting K. The K-tiles form S segments (split_segment, S <= TINY_MAX_SEG, at
-// most TINY_MAX_KT K-tiles each); wave w computes segments w, w + 4, w + 8, ... in turn, each as one
-// MFMA accumulation from zero in K order with every A, B and scale load of the segment issued
-// before its first MFMA (the operands of up to 12 slabs held in registers: one memory latency per
-// segment instead of one per K slab), and leaves each segment's partial block in LDS. The four
-// waves then sum the S partials, a quarter of the block each, in segment order from zero,
-// ((0 + P0) + P1) + ..., as the split-K reduce does (reduce_kernel.hpp), and store D. The output
-// therefore has the bits of any S-segment split plan with a 1 x 1 scale grouping, with no
-// workspace and no second launch.
+// its NW waves (4 or 8) splitting K. The K-tiles form S segments (split_segment, S <=
+// TINY_MAX_SEG, at most TINY_MAX_KT K-tiles each); wave w computes segments w, w + NW, ... in turn,
+// each as one MFMA accumulation from zero in K order with every A, B and scale load of the segment
+// issued before its first MFMA (the operands of up to 12 slabs held in registers: one memory
+// latency per segment instead of one per K slab). The waves then sum the S partial blocks from
+// LDS, a share of the block each, in segment order from zero, ((0 + P0) + P1) + ..., as the split-K
+// reduce does (reduce_kernel.hpp), and store D. The output therefore has the bits of any S-segment
+// split plan with a 1 x 1 scale grouping, with no workspace and no second launch.
 // For grids of at most a few hundred blocks (the latency floor: 256 x 256 x 1024 runs on 64 of
-// the 256 CUs), where a pipelined tile spends its time on per-slab copy issue and barriers. Four
-// instantiations: MULTI = false for S <= 4 on the smallest grids (four waves, one segment each, A
-// loaded directly, 16 KiB of LDS) and MULTI = true otherwise: A staged (below) by NW = 8 waves for
-// S > 4 where the grid leaves one workgroup per CU (twice the loads in flight at the occupancy of
-// two waves per SIMD), by NW = 4 for S <= 8 elsewhere, and loaded directly by four waves for
-// S = 9-16 on grids past one workgroup per CU.
-// A is row-major. With one segment per wave a lane reads its row's 24 bytes of a slab as a 16- and
-// an 8-byte load at 8-byte alignment (as the direct kernel's compiled loads do): each load then
-// touches all 32 rows of the block. The looping instantiations, whose waves together load far
-// more A per CU, read each segment's A along its rows instead (consecutive lanes on consecutive
-// 16-byte pieces of a row: a few cache lines per load; 256 x 256 x 4096 7.2 -> 4.6 us with such
-// loads in a timing probe), write it to the wave's own LDS region and read it back in the MFMA
-// layout; the segments' partial blocks wait in registers until every wave is done with its
-// region, which then holds them. B
-// preshuffled, scales tiled with groups of one 32-block. MASK: the last block row / column
+// the 256 CUs), where a pipelined tile spends its time on per-slab copy issue and barriers.
+// A is row-major. Read straight into the MFMA layout (a lane takes its row's 24 bytes of a slab as
+// a 16- and an 8-byte load at 8-byte alignment, as the direct kernel's compiled loads do) every
+// load touches all 32 rows of the block; where many waves a CU load A that bounds the kernel, so
+// the STAGED instantiations read each segment's A along its rows instead (consecutive lanes on
+// consecutive 16-byte pieces of a row, a few cache lines per load; 256 x 256 x 4096 7.2 -> 4.6 us
+// with such loads in a timing probe), copy it into the wave's own LDS region and read it back in
+// the MFMA layout; their segments' partial blocks wait in registers until every wave is done with
+// its region, which then holds them. Four instantiations (tiny_launch picks one):
+//   MULTI = false, NW = 4, direct A: S <= 4 on the smallest grids (one segment a wave, 16 KiB LDS);
+//   STAGED, NW = 8: S > 4 on grids of at most one workgroup per CU (two segments a wave at most;
+//     twice the loads in flight at the occupancy of two waves per SIMD);
+//   STAGED, NW = 4: S <= 8 otherwise (two workgroups a CU);
+//   MULTI, NW = 4, direct A: S = 9-16 on grids past one workgroup per CU (partials in LDS).
+// B preshuffled, scales tiled with groups of one 32-block. MASK: the last block row / column
 // clamps its A row and masks its stores (the layouts hold whole 32-blocks). The conversion to
 // FP16 / BF16 is cvt_out's round to nearest-even, the split-K reduce's.
 #pragma once
