@@ -193,7 +193,7 @@ void visit_plans(int M, int N, int Kp, F&& f) {
 // segments 1-7% slower on 8-12 K-tiles but for one 16-block grid); 8 beat 4 at 13-16 K-tiles on
 // all nine grids of 4-256 blocks measured (64 x 64 x 3072 5.95 -> 4.42 us, 256 x 256 x 3072 4.92 ->
 // 4.76); 8 beat 6 on all six 22-K-tile shapes, 11 beat 16 at 43 K-tiles on four of four.
-// The 32 x 32 tile splits K over its four waves: at most 16 segments of at most 4 K-tiles, on
+// The 32 x 32 tile splits K over its waves: at most 16 segments of at most 4 K-tiles, on
 // row-major A (tiny_kernel.hpp).
 bool tiny_plan_ok(const TileChoice& tc, int Kp, int S, int a_layout) {
     if (tc.MT != 32 || tc.NT != 32) return true;
